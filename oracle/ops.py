@@ -1,0 +1,242 @@
+"""numpy restatement of the hot-path ops (test oracle; see oracle/__init__).
+
+All inputs are numpy arrays; computation is float64 so the oracle is at
+least as accurate as the f32 CPU reference it stands in for.  Citations are
+to files under the reference repository.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+_SQRT1_2 = 1.0 / math.sqrt(2.0)
+
+
+def _f64(x):
+    return np.asarray(x, dtype=np.float64)
+
+
+# ---------------------------------------------------------------------------
+# layer norm — fast_aten_native_layer_norm (eager_kernels/aten_fast.py:5248-5371),
+# backward fast_aten_native_layer_norm_backward (aten_fast.py:5374-5517)
+# ---------------------------------------------------------------------------
+def layer_norm(x, gamma=None, beta=None, eps=1e-5):
+    """y over the last dim; returns (y, mean, rstd) with biased variance."""
+    x = _f64(x)
+    mean = x.mean(-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(-1, keepdims=True)
+    rstd = 1.0 / np.sqrt(var + eps)
+    y = (x - mean) * rstd
+    if gamma is not None:
+        y = y * _f64(gamma)
+    if beta is not None:
+        y = y + _f64(beta)
+    return y, mean, rstd
+
+
+def layer_norm_backward(dy, x, mean, rstd, gamma=None):
+    """(dx, dgamma, dbeta) for y = (x-mean)*rstd*gamma + beta."""
+    dy, x = _f64(dy), _f64(x)
+    xh = (x - mean) * rstd
+    g = dy * (_f64(gamma) if gamma is not None else 1.0)
+    n = x.shape[-1]
+    dx = rstd * (g - g.sum(-1, keepdims=True) / n - xh * (g * xh).sum(-1, keepdims=True) / n)
+    red = tuple(range(x.ndim - 1))
+    return dx, (dy * xh).sum(red), dy.sum(red)
+
+
+# ---------------------------------------------------------------------------
+# GELU — fast_aten_gelu / gelu_backward (aten_fast.py:2940-3009;
+# activation_forward_kernels.mojo:1-60, activation_backward_ops.mojo:80-233)
+# ---------------------------------------------------------------------------
+def _erf(x):
+    return np.vectorize(math.erf, otypes=[np.float64])(x)
+
+
+def gelu(x, approximate="none"):
+    x = _f64(x)
+    if approximate == "tanh":
+        k = math.sqrt(2.0 / math.pi)
+        return 0.5 * x * (1.0 + np.tanh(k * (x + 0.044715 * x**3)))
+    return 0.5 * x * (1.0 + _erf(x * _SQRT1_2))
+
+
+def gelu_backward(dy, x, approximate="none"):
+    dy, x = _f64(dy), _f64(x)
+    if approximate == "tanh":
+        k = math.sqrt(2.0 / math.pi)
+        inner = k * (x + 0.044715 * x**3)
+        t = np.tanh(inner)
+        return dy * (0.5 * (1 + t) + 0.5 * x * (1 - t * t) * k * (1 + 3 * 0.044715 * x * x))
+    cdf = 0.5 * (1.0 + _erf(x * _SQRT1_2))
+    pdf = np.exp(-0.5 * x * x) / math.sqrt(2 * math.pi)
+    return dy * (cdf + x * pdf)
+
+
+# ---------------------------------------------------------------------------
+# softmax / log_softmax — fast_aten__softmax (aten_fast.py:9220-9254),
+# fast_aten__log_softmax (aten_fast.py:5792-5825) and backward
+# (aten_fast.py:5828-5971; softmax_backward_kernels.mojo:76-231)
+# ---------------------------------------------------------------------------
+def softmax(x, axis=-1):
+    x = _f64(x)
+    m = np.max(x, axis=axis, keepdims=True)
+    e = np.exp(x - m)
+    return e / e.sum(axis=axis, keepdims=True)
+
+
+def log_softmax(x, axis=-1):
+    x = _f64(x)
+    m = np.max(x, axis=axis, keepdims=True)
+    return x - m - np.log(np.exp(x - m).sum(axis=axis, keepdims=True))
+
+
+def log_softmax_backward(dy, y, axis=-1):
+    dy, y = _f64(dy), _f64(y)
+    return dy - np.exp(y) * dy.sum(axis=axis, keepdims=True)
+
+
+def softmax_backward(dy, y, axis=-1):
+    dy, y = _f64(dy), _f64(y)
+    return y * (dy - (dy * y).sum(axis=axis, keepdims=True))
+
+
+# ---------------------------------------------------------------------------
+# NLL — fast_aten_nll_loss_forward_output / _backward_grad_input
+# (aten_fast.py:5974-6130; loss_ops.mojo:73-306)
+# ---------------------------------------------------------------------------
+def nll_loss(logp, target, weight=None, reduction="mean", ignore_index=-100):
+    """(output, total_weight)."""
+    logp = _f64(logp)
+    target = np.asarray(target, dtype=np.int64)
+    n = target.shape[0]
+    valid = target != ignore_index
+    t = np.where(valid, target, 0)
+    w = (_f64(weight)[t] if weight is not None else np.ones(n)) * valid
+    losses = -logp[np.arange(n), t] * w
+    total = w.sum()
+    if reduction == "none":
+        return losses, total
+    if reduction == "sum":
+        return losses.sum(), total
+    return losses.sum() / total, total
+
+
+def nll_loss_backward(grad, logp_shape, target, weight=None, reduction="mean",
+                      ignore_index=-100, total_weight=None):
+    n, c = logp_shape
+    target = np.asarray(target, dtype=np.int64)
+    valid = target != ignore_index
+    t = np.where(valid, target, 0)
+    w = (_f64(weight)[t] if weight is not None else np.ones(n)) * valid
+    g = _f64(grad)
+    vals = -w * (g if reduction == "none" else g.reshape(()))
+    if reduction == "mean":
+        vals = vals / total_weight
+    out = np.zeros((n, c))
+    out[np.arange(n), t] = np.where(valid, vals, 0.0)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# embedding — fast_aten_embedding (aten_fast.py:9262-9304, Gather0
+# nn_ops.mojo:1774-1796) and embedding_dense_backward (aten_fast.py:9307-9368)
+# ---------------------------------------------------------------------------
+def embedding(weight, idx):
+    return np.asarray(weight)[np.asarray(idx, dtype=np.int64)]
+
+
+def embedding_backward_f32(grad_out, idx, num_weights, padding_idx=-1):
+    """Sequential f32 accumulation in index order (ATen CPU's index_add
+    order), so the result is the bit pattern a sequential f32 sum gives."""
+    g = np.asarray(grad_out, dtype=np.float32).reshape(-1, np.asarray(grad_out).shape[-1])
+    ids = np.asarray(idx, dtype=np.int64).reshape(-1)
+    out = np.zeros((num_weights, g.shape[1]), dtype=np.float32)
+    for n, r in enumerate(ids):
+        if r != padding_idx:
+            out[r] += g[n]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# attention — fused flash attention forward/backward
+# (flash_attention_fwd_kernels.mojo:885-963, flash_attention_bwd_kernels.mojo:
+# 13-26 math, 63-66 top-left causal, 1403-1404 natural-log LSE)
+# ---------------------------------------------------------------------------
+def _scores(q, k, scale, causal):
+    s = np.einsum("...id,...jd->...ij", _f64(q), _f64(k)) * scale
+    if causal:
+        sq, skv = s.shape[-2], s.shape[-1]
+        mask = np.arange(skv)[None, :] > np.arange(sq)[:, None]  # top-left
+        s = np.where(mask, -np.inf, s)
+    return s
+
+
+def sdpa_forward(q, k, v, scale=None, causal=False):
+    """(O, LSE) with LSE the natural-log row log-sum-exp."""
+    d = q.shape[-1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    s = _scores(q, k, scale, causal)
+    m = s.max(-1, keepdims=True)
+    e = np.exp(s - m)
+    lse = (m + np.log(e.sum(-1, keepdims=True)))[..., 0]
+    p = np.exp(s - lse[..., None])
+    return np.einsum("...ij,...jd->...id", p, _f64(v)), lse
+
+
+def sdpa_backward(do, q, k, v, o, lse, scale=None, causal=False):
+    """(dQ, dK, dV) recomputing P from LSE and D_i = sum(dO*O)."""
+    d = q.shape[-1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    s = _scores(q, k, scale, causal)
+    p = np.exp(s - _f64(lse)[..., None])
+    do, o = _f64(do), _f64(o)
+    dv = np.einsum("...ij,...id->...jd", p, do)
+    dp = np.einsum("...id,...jd->...ij", do, _f64(v))
+    delta = (do * o).sum(-1, keepdims=True)
+    ds = p * (dp - delta)
+    dq = scale * np.einsum("...ij,...jd->...id", ds, _f64(k))
+    dk = scale * np.einsum("...ij,...id->...jd", ds, _f64(q))
+    return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
+# GEMM — fast_aten_mm / addmm / bmm (aten_fast.py:8713-8935)
+# ---------------------------------------------------------------------------
+def addmm(a, b, bias=None):
+    c = _f64(a) @ _f64(b)
+    if bias is not None:
+        c = c + _f64(bias)
+    return c
+
+
+# ---------------------------------------------------------------------------
+# AdamW — _fused_adamw_f32 update rule (optimizer_kernels.mojo:59-74,100-132)
+# ---------------------------------------------------------------------------
+def adamw_step(p, g, m, v, step, lr, beta1, beta2, weight_decay, eps, maximize=False,
+               amsgrad=False, vmax=None, grad_scale=None):
+    """One AdamW update of (p, m, v[, vmax]) at the already-incremented step."""
+    p, g, m, v = _f64(p).copy(), _f64(g).copy(), _f64(m).copy(), _f64(v).copy()
+    if grad_scale is not None:
+        g = g / grad_scale
+    if maximize:
+        g = -g
+    if weight_decay != 0.0:  # IEEE guard: no 0*inf when decay is off
+        p = p - lr * weight_decay * p
+    m = beta1 * m + (1 - beta1) * g
+    v = beta2 * v + (1 - beta2) * g * g
+    bc1 = 1 - beta1**step
+    bc2 = 1 - beta2**step
+    vv = v
+    if amsgrad:
+        vmax = np.maximum(_f64(vmax), v)
+        vv = vmax
+    denom = np.sqrt(vv) / math.sqrt(bc2) + eps
+    p = p - (lr / bc1) * m / denom
+    return (p, m, v, vmax) if amsgrad else (p, m, v)
+
+
+def l2_norm(x):
+    return float(np.sqrt((_f64(x) ** 2).sum()))

@@ -1,0 +1,195 @@
+"""GPU parity of the MFMA GEMM and fused flash attention through the C ABI.
+
+GEMM: the oracle is the f64 product of the bf16-rounded inputs (exact up to
+f64), tolerance grows with sqrt(K).  Attention: f64 oracle of the same
+bf16 inputs; bf16 outputs within atol = rtol = 2e-2."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from abi import CODE, bhs, call, dev, host, i64, lib, np64, p, tol_close, workspace  # noqa: F401
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+G = torch.Generator().manual_seed(1234)
+
+
+def randn(*shape):
+    return torch.randn(*shape, generator=G)
+
+
+def _gemm(c, a, b, m, n, k, a_rs, a_cs, b_rs, b_cs, dt, bias=None, beta=0, batch=1, a_bs=0, b_bs=0, c_bs=0):
+    call("mi355x_gemm", p(c), CODE[c.dtype], n if c.dim() == 2 else c.stride(-2), c_bs,
+         p(a), a_rs, a_cs, a_bs, p(b), b_rs, b_cs, b_bs, CODE[dt], p(bias),
+         CODE[bias.dtype] if bias is not None else 0, beta, batch, m, n, k, None, 0, None)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
+@pytest.mark.parametrize("mnk", [(256, 384, 768), (357, 789, 333), (1, 50, 64), (64, 1, 17), (130, 66, 1)])
+def test_gemm_layouts_and_shapes(kernels, dtype, layout, mnk):
+    m, n, k = mnk
+    A = randn(m, k).to(dtype)
+    B = randn(k, n).to(dtype) * 0.1
+    bias = (randn(n) * 0.1).to(dtype)
+    # A: "N" = row-major [m,k]; "T" = stored [k,m]
+    if layout[0] == "N":
+        ta = dev(A)
+        a_rs, a_cs = k, 1
+    else:
+        ta = dev(A.t().contiguous())
+        a_rs, a_cs = 1, m
+    if layout[1] == "N":
+        tb = dev(B)
+        b_rs, b_cs = n, 1
+    else:
+        tb = dev(B.t().contiguous())
+        b_rs, b_cs = 1, k
+    if m == 1 and a_rs == 1:
+        a_rs = k
+    c = torch.empty(m, n, dtype=dtype, device="cuda")
+    _gemm(c, ta, tb, m, n, k, a_rs, a_cs, b_rs, b_cs, dtype, bias=dev(bias))
+    exp = O.addmm(A.double().numpy(), B.double().numpy(), bias.double().numpy())
+    if dtype == torch.float32:
+        tol = 1e-4 * math.sqrt(k)
+    else:
+        tol = 2e-2 * max(1.0, math.sqrt(k) / 16)
+    tol_close(np64(c), exp, atol=tol, rtol=2e-2 if dtype != torch.float32 else 1e-4, what=f"{layout}{mnk}")
+
+
+def test_gemm_accumulate_and_batched(kernels):
+    bsz, m, n, k = 3, 100, 72, 96
+    A = randn(bsz, m, k).bfloat16()
+    B = randn(bsz, k, n).bfloat16()
+    C0 = randn(bsz, m, n)
+    ta, tb, tc = dev(A), dev(B), dev(C0)
+    call("mi355x_gemm", p(tc), 0, n, m * n, p(ta), k, 1, m * k, p(tb), n, 1, k * n, 1, None, 0, 1,
+         bsz, m, n, k, None, 0, None)
+    exp = C0.double().numpy() + np.einsum("bmk,bkn->bmn", A.double().numpy(), B.double().numpy())
+    tol_close(np64(tc), exp, atol=2e-2, rtol=1e-2, what="batched beta=1")
+
+
+@pytest.mark.parametrize("K,N", [(768, 2304), (3072, 768)])
+def test_gemm_gpt2_training_shapes(kernels, K, N):
+    """fwd x W^T, dX = dY W, dW = dY^T X at M = 4096 (cfg 2 shapes, smaller M)."""
+    M = 4096
+    X = randn(M, K).bfloat16()
+    W = (randn(N, K) * 0.02).bfloat16()
+    dY = randn(M, N).bfloat16()
+    tx, tw, tdy = dev(X), dev(W), dev(dY)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _gemm(y, tx, tw, M, N, K, K, 1, 1, K, torch.bfloat16)  # B = W^T: (k, n) at n*K + k
+    tol_close(np64(y), X.double().numpy() @ W.double().numpy().T, atol=2e-2, rtol=2e-2, what="fwd")
+    dx = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
+    _gemm(dx, tdy, tw, M, K, N, N, 1, K, 1, torch.bfloat16)
+    tol_close(np64(dx), dY.double().numpy() @ W.double().numpy(), atol=3e-2, rtol=2e-2, what="dX")
+    dw = torch.empty(N, K, dtype=torch.float32, device="cuda")
+    _gemm(dw, tdy, tx, N, K, M, 1, N, K, 1, torch.bfloat16)  # A = dY^T: (m,k) at k*N + m
+    ref = dY.double().numpy().T @ X.double().numpy()
+    tol_close(np64(dw), ref, atol=0.05 * math.sqrt(M / 64), rtol=1e-2, what="dW")
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+def _attn_fwd(q, k, v, causal, scale=None):
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    dense = torch.empty(B, Sq, H, D, dtype=q.dtype, device="cuda")
+    o = dense.transpose(1, 2)
+    lse = torch.empty(B, H, Sq, device="cuda")
+    call("mi355x_attn_fwd", p(o), bhs(o), p(lse), p(q), bhs(q), p(k), bhs(k), p(v), bhs(v),
+         B, H, Sq, Skv, D, scale, int(causal), CODE[q.dtype], None)
+    return o, lse
+
+
+def _attn_bwd(do, q, k, v, o, lse, causal, scale=None):
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    dq = torch.empty(B, Sq, H, D, dtype=q.dtype, device="cuda").transpose(1, 2)
+    dk = torch.empty(B, Skv, H, D, dtype=q.dtype, device="cuda").transpose(1, 2)
+    dv = torch.empty(B, Skv, H, D, dtype=q.dtype, device="cuda").transpose(1, 2)
+    ws_n = lib().mi355x_attn_bwd_workspace_bytes(B, H, Sq, Skv, D)
+    ws = workspace(ws_n)
+    call("mi355x_attn_bwd", p(dq), bhs(dq), p(dk), bhs(dk), p(dv), bhs(dv), p(do), bhs(do),
+         p(q), bhs(q), p(k), bhs(k), p(v), bhs(v), p(o), bhs(o), p(lse),
+         B, H, Sq, Skv, D, scale, int(causal), CODE[q.dtype], p(ws), ws_n, None)
+    return dq, dk, dv
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 128, 128, 64), (1, 2, 100, 160, 64), (2, 2, 160, 100, 64),
+                                   (1, 2, 192, 192, 32), (1, 2, 130, 130, 128), (1, 1, 1, 1, 64)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_fwd_bwd_matches_oracle(kernels, shape, causal):
+    B, H, Sq, Skv, D = shape
+    q = randn(B, H, Sq, D).bfloat16()
+    k = randn(B, H, Skv, D).bfloat16()
+    v = randn(B, H, Skv, D).bfloat16()
+    do = randn(B, H, Sq, D).bfloat16()
+    tq, tk, tv, tdo = dev(q), dev(k), dev(v), dev(do)
+    o, lse = _attn_fwd(tq, tk, tv, causal)
+    eo, else_ = O.sdpa_forward(q.double().numpy(), k.double().numpy(), v.double().numpy(), causal=causal)
+    tol_close(np64(o), eo, atol=2e-2, rtol=2e-2, what="O")
+    tol_close(np64(lse), else_, atol=1e-3, rtol=1e-3, what="LSE")
+    dq, dk, dv = _attn_bwd(tdo, tq, tk, tv, o, lse, causal)
+    edq, edk, edv = O.sdpa_backward(do.double().numpy(), q.double().numpy(), k.double().numpy(),
+                                    v.double().numpy(), np64(o), np64(lse), causal=causal)
+    tol_close(np64(dv), edv, atol=3e-2, rtol=2e-2, what="dV")
+    tol_close(np64(dk), edk, atol=3e-2, rtol=2e-2, what="dK")
+    tol_close(np64(dq), edq, atol=3e-2, rtol=2e-2, what="dQ")
+
+
+def test_attention_special_cases(kernels):
+    """S = 1 gives O = V; causal row 0 attends only to key 0."""
+    q = randn(1, 2, 64, 64).bfloat16()
+    k = randn(1, 2, 64, 64).bfloat16()
+    v = randn(1, 2, 64, 64).bfloat16()
+    o, lse = _attn_fwd(dev(q[:, :, :1]), dev(k[:, :, :1]), dev(v[:, :, :1]), True)
+    assert torch.allclose(host(o).float(), v[:, :, :1].float(), atol=1e-2)
+    o, lse = _attn_fwd(dev(q), dev(k), dev(v), True)
+    assert torch.allclose(host(o)[:, :, 0].float(), v[:, :, 0].float(), atol=1e-2)
+    s00 = (q[:, :, 0].float() * k[:, :, 0].float()).sum(-1) / 8.0
+    assert torch.allclose(host(lse)[:, :, 0], s00, atol=1e-3)
+
+
+def test_attention_gapped_qkv_views(kernels):
+    """q/k/v as split+view+transpose of one fused qkv projection (BTHD storage
+    with a 3C row stride), as nanoGPT hands them over."""
+    B, T, H, D = 2, 256, 4, 64
+    C = H * D
+    qkv = randn(B, T, 3 * C).bfloat16()
+    tqkv = dev(qkv)
+    tq, tk, tv = (t.view(B, T, H, D).transpose(1, 2) for t in tqkv.split(C, dim=2))
+    assert tq.stride() == (T * 3 * C, D, 3 * C, 1)
+    o, lse = _attn_fwd(tq, tk, tv, True)
+    q, k, v = (t.view(B, T, H, D).transpose(1, 2).double().numpy() for t in qkv.split(C, dim=2))
+    eo, _ = O.sdpa_forward(q, k, v, causal=True)
+    tol_close(np64(o), eo, atol=2e-2, rtol=2e-2, what="gapped O")
+
+
+def test_attention_cfg1_shape_properties(kernels):
+    """BASELINE cfg 1 shape [8,12,1024,64]: fwd vs oracle on two heads, and
+    sum_j dK_j = 0 (softmax rows are shift-invariant) over the full size."""
+    B, H, S, D = 8, 12, 1024, 64
+    q = randn(B, H, S, D).bfloat16()
+    k = randn(B, H, S, D).bfloat16()
+    v = randn(B, H, S, D).bfloat16()
+    do = randn(B, H, S, D).bfloat16()
+    tq, tk, tv, tdo = dev(q), dev(k), dev(v), dev(do)
+    o, lse = _attn_fwd(tq, tk, tv, True)
+    sel = (slice(0, 1), slice(0, 2))
+    eo, el = O.sdpa_forward(q[sel].double().numpy(), k[sel].double().numpy(), v[sel].double().numpy(), causal=True)
+    tol_close(np64(o[sel]), eo, atol=2e-2, rtol=2e-2, what="O cfg1")
+    tol_close(np64(lse[sel]), el, atol=1e-3, rtol=1e-3, what="LSE cfg1")
+    dq, dk, dv = _attn_bwd(tdo, tq, tk, tv, o, lse, True)
+    # dS rows sum to zero, so sum over keys of dK (and of dQ's row contributions) cancels
+    tot = host(dk).double().sum(2)
+    assert tot.abs().max().item() < 0.5
+    # dV columns: sum over keys of dV = sum over queries of dO (P rows sum to 1)
+    tol_close(host(dv).double().sum(2).numpy(), do.double().sum(2).numpy(), atol=0.5, rtol=2e-2, what="sum dV")

@@ -1,0 +1,330 @@
+"""GPU parity of the HBM-bound kernels, called through the C ABI, against the
+oracle (and bit-exact where the op is integer/index/copy work)."""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from abi import (CODE, AdamWTensor, bhs, call, dev, host, i64, lib, np64, p, tol_close,  # noqa: F401
+                 workspace)
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+G = torch.Generator().manual_seed(20260718)
+
+
+def randn(*shape, dtype=torch.float32):
+    return torch.randn(*shape, generator=G).to(dtype)
+
+
+# ---------------------------------------------------------------------------
+# copies / casts / elementwise
+# ---------------------------------------------------------------------------
+def test_cast_f32_to_bf16_is_rne_bit_exact(kernels):
+    x = randn(1000, 257) * 37.0
+    x[0, :4] = torch.tensor([float("inf"), float("-inf"), float("nan"), 1e-40])
+    src = dev(x)
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device="cuda")
+    call("mi355x_copy", p(out), 1, i64(*out.stride()), p(src), 0, i64(*src.stride()), i64(*x.shape), 2, None)
+    expect = x.to(torch.bfloat16)
+    got = host(out)
+    assert torch.equal(got.view(torch.int16)[1:], expect.view(torch.int16)[1:])
+    assert torch.isnan(got[0, 2])
+
+
+def test_strided_broadcast_copy(kernels):
+    x = randn(64, 48)
+    src = dev(x)
+    # transpose view of src into a dense [48, 64] bf16, and broadcast a row
+    out = torch.empty(48, 64, dtype=torch.bfloat16, device="cuda")
+    call("mi355x_copy", p(out), 1, i64(64, 1), p(src), 0, i64(1, 48), i64(48, 64), 2, None)
+    assert torch.equal(host(out), x.t().to(torch.bfloat16))
+    row = dev(randn(1, 64))
+    out2 = torch.empty(5, 64, device="cuda")
+    call("mi355x_copy", p(out2), 0, i64(64, 1), p(row), 0, i64(0, 1), i64(5, 64), 2, None)
+    assert torch.equal(host(out2), host(row).expand(5, 64))
+
+
+@pytest.mark.parametrize("op,fn", [(0, lambda a, b: a + 0.5 * b), (1, lambda a, b: a - 0.5 * b),
+                                   (2, lambda a, b: a * b), (4, torch.maximum), (11, lambda a, b: a > b)])
+def test_map_binary_broadcast_exact(kernels, op, fn):
+    a, b = randn(33, 70), randn(1, 70)
+    ta, tb = dev(a), dev(b)
+    out_dt = torch.bool if op == 11 else torch.float32
+    out = torch.empty(33, 70, dtype=out_dt, device="cuda")
+    ins = (ctypes.c_void_p * 3)(p(ta), p(tb), None)
+    dts = (ctypes.c_int * 3)(0, 0, 0)
+    call("mi355x_map", op, p(out), CODE[out_dt], 2, ins, dts, i64(70, 1, 70, 1, 0, 1), i64(33, 70), 2, 0.5, 0.0, None)
+    assert torch.equal(host(out), fn(a, b).to(out_dt))
+
+
+def test_map_scalar_operand_and_integer_math(kernels):
+    x = torch.arange(-20, 20, dtype=torch.int64)
+    tx = dev(x)
+    out = torch.empty(40, dtype=torch.int64, device="cuda")
+    ins = (ctypes.c_void_p * 3)(p(tx), None, None)
+    dts = (ctypes.c_int * 3)(4, 4, 0)
+    # floor_divide by scalar 3 (NULL input reads s1)
+    call("mi355x_map", 20, p(out), 4, 2, ins, dts, i64(1, 1, 0), i64(40), 1, 0.0, 3.0, None)
+    assert torch.equal(host(out), torch.floor_divide(x, 3))
+    call("mi355x_map", 19, p(out), 4, 2, ins, dts, i64(1, 1, 0), i64(40), 1, 0.0, 7.0, None)
+    assert torch.equal(host(out), torch.remainder(x, 7))
+
+
+def test_fill_and_arange(kernels):
+    out = torch.empty(1000, dtype=torch.int64, device="cuda")
+    call("mi355x_arange", p(out), 4, 1000, 5.0, 3.0, None)
+    assert torch.equal(host(out), torch.arange(5, 5 + 3 * 1000, 3))
+    f = torch.empty(7, 9, dtype=torch.bfloat16, device="cuda")
+    call("mi355x_fill", p(f), 1, i64(9, 1), i64(7, 9), 2, 0.1, None)
+    assert torch.equal(host(f), torch.full((7, 9), 0.1, dtype=torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------
+# reductions / index
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,axis", [((16384, 768), 0), ((64, 50257), 1), ((3, 1 << 20), 1), ((5, 7, 9), 1)])
+def test_reduce_sum_matches_oracle(kernels, shape, axis):
+    x = randn(*shape)
+    tx = dev(x)
+    outer = math.prod(shape[:axis])
+    r = shape[axis]
+    inner = math.prod(shape[axis + 1:])
+    out = torch.empty(outer * inner, device="cuda")
+    ws_n = lib().mi355x_reduce_workspace_bytes(outer, r, inner)
+    ws = workspace(ws_n)
+    call("mi355x_reduce", 0, p(out), 0, p(tx), 0, outer, r, inner, r * inner, inner, 1, p(ws), ws_n, None)
+    expect = x.double().numpy().reshape(outer, r, inner).sum(1).reshape(-1)
+    tol_close(np64(out), expect, atol=1e-3, rtol=1e-5, what="sum")
+
+
+def test_reduce_max_norm_mean(kernels):
+    x = randn(37, 1000)
+    x[3, 5] = float("nan")
+    tx = dev(x)
+    out = torch.empty(37, device="cuda")
+    for op, fn in ((2, lambda a: np.max(a, 1)), (4, lambda a: np.sqrt((a ** 2).sum(1))), (1, lambda a: a.mean(1))):
+        call("mi355x_reduce", op, p(out), 0, p(tx), 0, 37, 1000, 1, 1000, 1, 1, None, 0, None)
+        tol_close(np64(out), fn(x.double().numpy()), atol=1e-5, rtol=1e-5, what=f"op{op}")
+
+
+def test_argmax_bit_exact_with_ties_and_nan(kernels):
+    x = torch.randint(0, 5, (64, 300), generator=G).float()
+    x[7, 100] = float("nan")
+    tx = dev(x)
+    out = torch.empty(64, dtype=torch.int64, device="cuda")
+    call("mi355x_argreduce", 0, p(out), None, p(tx), 0, 64, 300, 1, 300, 1, 1, None)
+    assert torch.equal(host(out), torch.argmax(x, 1))
+    out2 = torch.empty(300, dtype=torch.int64, device="cuda")
+    call("mi355x_argreduce", 1, p(out2), None, p(tx), 0, 1, 64, 300, 0, 300, 1, None)
+    assert torch.equal(host(out2), torch.argmin(x, 0))
+
+
+def test_index_select_and_embedding_forward_bit_exact(kernels):
+    w = randn(50257, 768)
+    idx = torch.randint(0, 50257, (4, 256), generator=G)
+    tw, ti = dev(w), dev(idx)
+    out = torch.empty(4 * 256, 768, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    call("mi355x_embedding_fwd", p(out), p(tw), 0, p(ti), 1024, 50257, 768, 768, p(err), None)
+    assert torch.equal(host(out), w[idx.reshape(-1)])
+    assert host(err).item() == 0
+    bad = dev(torch.tensor([0, 50257, -1]))
+    out3 = torch.empty(3, 768, device="cuda")
+    call("mi355x_embedding_fwd", p(out3), p(tw), 0, p(bad), 3, 50257, 768, 768, p(err), None)
+    assert host(err).item() == 1
+    assert torch.equal(host(out3)[1:], torch.zeros(2, 768))
+
+
+def test_embedding_backward_bit_exact_vs_sequential_f32(kernels):
+    n, num, dim = 4096, 300, 96
+    idx = torch.randint(0, num, (n,), generator=G)
+    idx[:50] = 7  # heavy repetition
+    g = randn(n, dim)
+    tg, ti = dev(g), dev(idx)
+    gw = torch.empty(num, dim, device="cuda")
+    ws_n = lib().mi355x_embedding_bwd_workspace_bytes(n, num)
+    ws = workspace(ws_n)
+    call("mi355x_embedding_bwd", p(gw), p(tg), 0, p(ti), n, num, dim, 3, p(ws), ws_n, None)
+    expect = O.embedding_backward_f32(g.numpy(), idx.numpy(), num, padding_idx=3)
+    assert np.array_equal(host(gw).numpy(), expect)
+    # and ATen's own CPU kernel gives the same bits
+    ref = torch.ops.aten.embedding_dense_backward(g, idx, num, 3, False)
+    assert torch.equal(host(gw), ref)
+
+
+# ---------------------------------------------------------------------------
+# layer norm / gelu / softmax / nll
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,rows,cols", [(torch.float32, 16384, 768), (torch.float32, 33, 1000),
+                                             (torch.bfloat16, 300, 768), (torch.float32, 7, 4099)])
+def test_layer_norm_fwd_bwd(kernels, dtype, rows, cols):
+    x = randn(rows, cols) * 3 + 1
+    g, b = randn(cols), randn(cols)
+    dy = randn(rows, cols)
+    xq, gq, bq, dyq = (t.to(dtype) for t in (x, g, b, dy))
+    tx, tg, tb, tdy = dev(xq), dev(gq), dev(bq), dev(dyq)
+    y = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    mean = torch.empty(rows, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    call("mi355x_layer_norm_fwd", p(y), p(mean), p(rstd), p(tx), p(tg), p(tb), rows, cols, 1e-5, CODE[dtype], None)
+    ey, em, er = O.layer_norm(xq.double().numpy(), gq.double().numpy(), bq.double().numpy())
+    atol = 1e-4 if dtype == torch.float32 else 2e-2
+    tol_close(np64(y), ey, atol=atol, rtol=atol, what="ln y")
+    tol_close(np64(mean), em[:, 0], atol=1e-5, rtol=1e-5, what="ln mean")
+    tol_close(np64(rstd), er[:, 0], atol=1e-5, rtol=1e-4, what="ln rstd")
+    dx = torch.empty_like(tx)
+    dg = torch.empty_like(tg)
+    db = torch.empty_like(tb)
+    ws_n = lib().mi355x_layer_norm_bwd_workspace_bytes(rows, cols)
+    ws = workspace(ws_n)
+    call("mi355x_layer_norm_bwd", p(dx), p(dg), p(db), p(tdy), p(tx), p(mean), p(rstd), p(tg), rows, cols,
+         CODE[dtype], p(ws), ws_n, None)
+    edx, edg, edb = O.layer_norm_backward(dyq.double().numpy(), xq.double().numpy(), em, er, gq.double().numpy())
+    tol_close(np64(dx), edx, atol=atol * 5, rtol=atol, what="ln dx")
+    scale = math.sqrt(rows)
+    tol_close(np64(dg), edg, atol=atol * scale, rtol=atol, what="ln dgamma")
+    tol_close(np64(db), edb, atol=atol * scale, rtol=atol, what="ln dbeta")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("approx", [0, 1])
+def test_gelu(kernels, dtype, approx):
+    n = 16384 * 3 + 5
+    x = randn(n) * 4
+    dy = randn(n)
+    xq, dyq = x.to(dtype), dy.to(dtype)
+    tx, tdy = dev(xq), dev(dyq)
+    y = torch.empty_like(tx)
+    call("mi355x_gelu_fwd", p(y), p(tx), n, approx, CODE[dtype], None)
+    mode = "tanh" if approx else "none"
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    tol_close(np64(y), O.gelu(xq.double().numpy(), mode), atol=tol, rtol=tol, what="gelu")
+    dx = torch.empty_like(tx)
+    call("mi355x_gelu_bwd", p(dx), p(tdy), p(tx), n, approx, CODE[dtype], None)
+    tol_close(np64(dx), O.gelu_backward(dyq.double().numpy(), xq.double().numpy(), mode), atol=tol, rtol=tol,
+              what="gelu bwd")
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(64, 50257, torch.bfloat16), (300, 1000, torch.float32),
+                                             (17, 3, torch.float32), (8, 4096, torch.float32)])
+@pytest.mark.parametrize("log", [0, 1])
+def test_softmax_fwd_bwd(kernels, rows, cols, dtype, log):
+    x = randn(rows, cols) * 3
+    x[1, :] = float("-inf") if cols > 3 else x[1, :]
+    x[2, 0] = float("-inf")
+    xq = x.to(dtype)
+    tx = dev(xq)
+    y = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    call("mi355x_softmax_fwd", p(y), CODE[dtype], p(tx), CODE[dtype], rows, cols, log, None)
+    with np.errstate(invalid="ignore"):
+        ey = (O.log_softmax if log else O.softmax)(xq.double().numpy())
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    tol_close(np64(y), ey, atol=tol, rtol=tol, what="softmax")
+    dy = randn(rows, cols).to(dtype)
+    tdy = dev(dy)
+    yy = torch.where(torch.isnan(y), torch.zeros_like(y), y)
+    dx = torch.empty_like(y)
+    call("mi355x_softmax_bwd", p(dx), CODE[dtype], p(tdy), CODE[dtype], p(yy), CODE[dtype], rows, cols, log, None)
+    fn = O.log_softmax_backward if log else O.softmax_backward
+    tol_close(np64(dx), fn(dy.double().numpy(), np64(yy)), atol=tol * 10, rtol=tol * 10, what="softmax bwd")
+
+
+@pytest.mark.parametrize("reduction", [0, 1, 2])
+def test_nll_fwd_bwd(kernels, reduction):
+    n, c = 1000, 50257
+    logp = torch.log_softmax(randn(n, c), 1)
+    tgt = torch.randint(0, c, (n,), generator=G)
+    tgt[::7] = -100
+    w = None
+    tl, tt = dev(logp), dev(tgt)
+    out = torch.empty(n if reduction == 0 else (), device="cuda")
+    tw = torch.empty((), device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    call("mi355x_nll_fwd", p(out), p(tw), p(tl), 0, p(tt), None, n, c, reduction, -100, p(err), None, 0, None)
+    red = {0: "none", 1: "mean", 2: "sum"}[reduction]
+    eo, etw = O.nll_loss(logp.numpy(), tgt.numpy(), w, red, -100)
+    tol_close(np64(out), eo, atol=1e-4, rtol=1e-5, what="nll")
+    assert host(tw).item() == etw
+    assert host(err).item() == 0
+    go = dev(randn(n) if reduction == 0 else torch.tensor(1.7))
+    gi = torch.empty(n, c, device="cuda")
+    call("mi355x_nll_bwd", p(gi), p(go), p(tt), None, p(tw), n, c, reduction, -100, 0, None)
+    egi = O.nll_loss_backward(np64(go), (n, c), tgt.numpy(), None, red, -100, etw)
+    assert np.array_equal(host(gi).numpy(), egi.astype(np.float32))
+    bad = dev(torch.tensor([0, c + 5]))
+    call("mi355x_nll_fwd", p(out), p(tw), p(tl), 0, p(bad), None, 2, c, 1, -100, p(err), None, 0, None)
+    assert host(err).item() == 1
+
+
+# ---------------------------------------------------------------------------
+# optimizer
+# ---------------------------------------------------------------------------
+def _adam_descs(params, grads, ms, vs, steps, vmax=None):
+    n = len(params)
+    d = (AdamWTensor * n)()
+    for i in range(n):
+        d[i].param, d[i].grad, d[i].exp_avg, d[i].exp_avg_sq = p(params[i]), p(grads[i]), p(ms[i]), p(vs[i])
+        d[i].max_exp_avg_sq = p(vmax[i]) if vmax else None
+        d[i].step = p(steps[i])
+        d[i].numel = params[i].numel()
+    return d
+
+
+@pytest.mark.parametrize("amsgrad,maximize,wd", [(False, False, 0.1), (True, False, 0.1), (False, True, 0.0)])
+def test_fused_adamw_matches_oracle(kernels, amsgrad, maximize, wd):
+    sizes = [768 * 768, 3, 50257, 1, 4 * 65536 + 17] + [10] * 40  # > one 32-tensor batch
+    ps = [randn(s) for s in sizes]
+    gs = [randn(s) for s in sizes]
+    ms = [randn(s) * 0.1 for s in sizes]
+    vs = [randn(s).abs() * 0.01 for s in sizes]
+    vm = [v + 0.001 for v in vs]
+    step = 7.0
+    tp, tg, tm, tv = ([dev(x) for x in xs] for xs in (ps, gs, ms, vs))
+    tvm = [dev(x) for x in vm] if amsgrad else None
+    steps = [dev(torch.tensor(step)) for _ in sizes]
+    d = _adam_descs(tp, tg, tm, tv, steps, tvm)
+    flags = (1 if amsgrad else 0) | (2 if maximize else 0)
+    call("mi355x_fused_adamw", d, len(sizes), 6e-4, None, 0.9, 0.95, wd, 1e-8, flags, None, None, None)
+    for i in range(len(sizes)):
+        exp = O.adamw_step(ps[i].numpy(), gs[i].numpy(), ms[i].numpy(), vs[i].numpy(), step, 6e-4, 0.9, 0.95,
+                           wd, 1e-8, maximize, amsgrad, vm[i].numpy() if amsgrad else None)
+        tol_close(np64(tp[i]), exp[0], atol=1e-6, rtol=1e-5, what=f"p{i}")
+        tol_close(np64(tm[i]), exp[1], atol=1e-6, rtol=1e-5, what=f"m{i}")
+        tol_close(np64(tv[i]), exp[2], atol=1e-7, rtol=1e-5, what=f"v{i}")
+
+
+def test_fused_adamw_found_inf_skips_and_wd0_keeps_inf(kernels):
+    pp = torch.tensor([float("inf"), 1.0, 2.0])
+    tp, tg, tm, tv = dev(pp), dev(torch.ones(3)), dev(torch.zeros(3)), dev(torch.zeros(3))
+    step = dev(torch.tensor(1.0))
+    fi = dev(torch.tensor(1.0))
+    d = _adam_descs([tp], [tg], [tm], [tv], [step])
+    call("mi355x_fused_adamw", d, 1, 1e-3, None, 0.9, 0.999, 0.0, 1e-8, 0, None, p(fi), None)
+    assert torch.equal(host(tp), pp)
+    call("mi355x_fused_adamw", d, 1, 1e-3, None, 0.9, 0.999, 0.0, 1e-8, 0, None, None, None)
+    out = host(tp)
+    assert math.isinf(out[0].item()) and not math.isnan(out[0].item())
+
+
+def test_foreach_norm_and_apply(kernels):
+    sizes = [100000, 7, 768, 65] + [3] * 70
+    xs = [randn(s) for s in sizes]
+    tx = [dev(x) for x in xs]
+    outs = [torch.empty((), device="cuda") for _ in sizes]
+    numels = i64(*sizes)
+    ws_n = lib().mi355x_foreach_norm_workspace_bytes(numels, len(sizes))
+    ws = workspace(ws_n)
+    ptrs_out = (ctypes.c_void_p * len(sizes))(*[p(o) for o in outs])
+    ptrs_in = (ctypes.c_void_p * len(sizes))(*[p(t) for t in tx])
+    call("mi355x_foreach_norm", ptrs_out, 0, ptrs_in, 0, numels, len(sizes), 2.0, p(ws), ws_n, None)
+    for o, x in zip(outs, xs):
+        assert abs(host(o).item() - O.l2_norm(x.numpy())) <= 1e-5 * max(1.0, O.l2_norm(x.numpy()))
+    coef = dev(torch.tensor(0.25))
+    call("mi355x_foreach_apply", 2, ptrs_in, None, None, None, numels, len(sizes), 0, 0.0, p(coef), None)
+    for t, x in zip(tx, xs):
+        assert torch.equal(host(t), x * 0.25)

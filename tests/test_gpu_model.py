@@ -1,0 +1,76 @@
+"""The mojo device end to end on the GPU: ops through `model.to("mojo")`,
+compared with stock PyTorch CPU f32 (the reference's oracle)."""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from torch_mojo_backend.eager_kernels import aten_fast
+from torch_mojo_backend.gpt2 import BETAS, LEARNING_RATE, WEIGHT_DECAY, GPT, GPTConfig, make_batches, training_step
+
+pytestmark = pytest.mark.gpu
+
+
+def test_device_basics(mojo):
+    x = torch.randn(4, 8)
+    xm = x.to("mojo")
+    assert xm.device.type == "mojo"
+    assert torch.equal((xm * 2 + 1).cpu(), x * 2 + 1)
+    assert torch.equal(xm.t().contiguous().cpu(), x.t().contiguous())
+    assert torch.allclose(xm.sum(0).cpu(), x.sum(0))
+    assert xm[1, 2].item() == x[1, 2].item()
+    assert torch.equal(torch.arange(10, device="mojo").cpu(), torch.arange(10))
+
+
+def test_sdpa_autograd_uses_fused_kernels(mojo):
+    B, H, T, D = 2, 4, 256, 64
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, H, T, D, generator=g) for _ in range(3))
+    qm, km, vm = (t.to("mojo").bfloat16().requires_grad_() for t in (q, k, v))
+    out = F.scaled_dot_product_attention(qm, km, vm, is_causal=True)
+    out.float().sum().backward()
+    qc, kc, vc = (t.bfloat16().float().requires_grad_() for t in (q, k, v))
+    ref = F.scaled_dot_product_attention(qc, kc, vc, is_causal=True)
+    ref.sum().backward()
+    assert torch.allclose(out.float().cpu(), ref, atol=2e-2, rtol=2e-2)
+    for a, b in ((qm, qc), (km, kc), (vm, vc)):
+        assert torch.allclose(a.grad.float().cpu(), b.grad, atol=5e-2, rtol=5e-2)
+
+
+def _small_cfg():
+    return GPTConfig(block_size=256, vocab_size=1000, n_layer=2, n_head=4, n_embd=256)
+
+
+@pytest.mark.parametrize("amp", [False, True])
+def test_gpt_training_steps_match_cpu(mojo, amp):
+    cfg = _small_cfg()
+    torch.manual_seed(0)
+    ref = GPT(cfg)
+    torch.manual_seed(0)
+    model = GPT(cfg)
+    model.load_state_dict(ref.state_dict())
+    model.to("mojo")
+    assert model.lm_head.weight is model.transformer.wte.weight
+    opt = model.configure_optimizers(WEIGHT_DECAY, LEARNING_RATE, BETAS, fused=True)
+    ropt = ref.configure_optimizers(WEIGHT_DECAY, LEARNING_RATE, BETAS, fused=True)
+    batches = make_batches(4, 256, cfg.vocab_size, 2, 7, "cpu")
+    for step in range(4):
+        x, y = batches[step % 2]
+        lr_ = training_step(ref, ropt, x, y).item()
+        lm = training_step(model, opt, x.to("mojo"), y.to("mojo"),
+                           autocast_dtype=torch.bfloat16 if amp else None).item()
+        tol = 1e-2 if amp else 1e-4
+        assert math.isfinite(lm)
+        assert abs(lm - lr_) <= tol * abs(lr_), (step, lm, lr_)
+    for (name, p_ref), p_m in zip(ref.named_parameters(), model.parameters()):
+        tol = 2e-2 if amp else 1e-4
+        assert torch.allclose(p_m.detach().cpu(), p_ref.detach(), atol=tol, rtol=tol), name
+
+
+def test_bounds_errors_surface(mojo):
+    w = torch.randn(10, 4).to("mojo")
+    with pytest.raises(IndexError):
+        F.embedding(torch.tensor([1, 10]).to("mojo"), w)
+    assert aten_fast is not None

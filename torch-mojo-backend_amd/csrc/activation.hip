@@ -1,0 +1,127 @@
+// GELU forward/backward, exact (erf) and tanh forms.
+//
+// Read-once/write-once elementwise passes: 8 elements per thread per step
+// (one 16-byte bf16 access or two 16-byte f32 accesses), computed in f32 and
+// rounded once to the storage type, as ATen does for reduced precision.
+//   exact: y = 0.5 x (1 + erf(x/sqrt2)),  dy/dx = Phi(x) + x phi(x)
+//   tanh:  y = 0.5 x (1 + tanh(k (x + 0.044715 x^3))),  k = sqrt(2/pi)
+#include <math.h>
+
+#include "common.h"
+
+namespace mi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr float kInvSqrt2 = 0.70710678118654752440f;
+constexpr float kInvSqrt2Pi = 0.39894228040143267794f;
+constexpr float kSqrt2OverPi = 0.79788456080286535588f;
+constexpr float kTanhC = 0.044715f;
+
+__device__ __forceinline__ float gelu_f(float x, int approx) {
+  if (approx) {
+    const float inner = kSqrt2OverPi * (x + kTanhC * x * x * x);
+    return 0.5f * x * (1.f + tanhf(inner));
+  }
+  return 0.5f * x * (1.f + erff(x * kInvSqrt2));
+}
+
+__device__ __forceinline__ float gelu_grad_f(float dy, float x, int approx) {
+  if (approx) {
+    const float x2 = x * x;
+    const float inner = kSqrt2OverPi * (x + kTanhC * x2 * x);
+    const float t = tanhf(inner);
+    const float left = 0.5f * x;
+    const float right = 1.f + t;
+    const float left_d = 0.5f * right;
+    const float tanh_d = 1.f - t * t;
+    const float inner_d = kSqrt2OverPi * (1.f + 3.f * kTanhC * x2);
+    const float right_d = left * tanh_d * inner_d;
+    return dy * (left_d + right_d);
+  }
+  const float cdf = 0.5f * (1.f + erff(x * kInvSqrt2));
+  const float pdf = kInvSqrt2Pi * expf(-0.5f * x * x);
+  return dy * (cdf + x * pdf);
+}
+
+__device__ __forceinline__ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <typename T>
+struct alignas(16) Pack8 {
+  T v[8];
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) gelu_fwd_kernel(T* __restrict__ y, const T* __restrict__ x,
+                                                            int64_t n, int approx) {
+  const int64_t n8 = (aligned16(y) && aligned16(x)) ? n / 8 : 0;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n8; i += stride) {
+    Pack8<T> a = ((const Pack8<T>*)x)[i];
+    Pack8<T> r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.v[e] = from_f32<T>(gelu_f(to_f32(a.v[e]), approx));
+    ((Pack8<T>*)y)[i] = r;
+  }
+  for (int64_t i = n8 * 8 + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride)
+    y[i] = from_f32<T>(gelu_f(to_f32(x[i]), approx));
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) gelu_bwd_kernel(T* __restrict__ dx, const T* __restrict__ dy,
+                                                            const T* __restrict__ x, int64_t n,
+                                                            int approx) {
+  const int64_t n8 = (aligned16(dx) && aligned16(dy) && aligned16(x)) ? n / 8 : 0;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n8; i += stride) {
+    Pack8<T> a = ((const Pack8<T>*)x)[i];
+    Pack8<T> g = ((const Pack8<T>*)dy)[i];
+    Pack8<T> r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r.v[e] = from_f32<T>(gelu_grad_f(to_f32(g.v[e]), to_f32(a.v[e]), approx));
+    ((Pack8<T>*)dx)[i] = r;
+  }
+  for (int64_t i = n8 * 8 + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride)
+    dx[i] = from_f32<T>(gelu_grad_f(to_f32(dy[i]), to_f32(x[i]), approx));
+}
+
+unsigned grid_for(int64_t n) {
+  int64_t b = (n / 8 + kThreads - 1) / kThreads;
+  if (b < 1) b = 1;
+  if (b > 8192) b = 8192;
+  return (unsigned)b;
+}
+
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi355x_gelu_fwd(void* y, const void* x, int64_t n, int approximate, int dtype,
+                               mi355x_stream_t stream) {
+  MI_REQUIRE(n >= 0, "mi355x_gelu_fwd: negative size");
+  if (n == 0) return MI355X_OK;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MI355X_F32: gelu_fwd_kernel<float><<<grid_for(n), kThreads, 0, s>>>((float*)y, (const float*)x, n, approximate); break;
+    case MI355X_BF16: gelu_fwd_kernel<bf16><<<grid_for(n), kThreads, 0, s>>>((bf16*)y, (const bf16*)x, n, approximate); break;
+    case MI355X_F16: gelu_fwd_kernel<f16><<<grid_for(n), kThreads, 0, s>>>((f16*)y, (const f16*)x, n, approximate); break;
+    default: return fail(MI355X_EUNSUPPORTED, "mi355x_gelu_fwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("mi355x_gelu_fwd");
+}
+
+extern "C" int mi355x_gelu_bwd(void* dx, const void* dy, const void* x, int64_t n, int approximate,
+                               int dtype, mi355x_stream_t stream) {
+  MI_REQUIRE(n >= 0, "mi355x_gelu_bwd: negative size");
+  if (n == 0) return MI355X_OK;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MI355X_F32: gelu_bwd_kernel<float><<<grid_for(n), kThreads, 0, s>>>((float*)dx, (const float*)dy, (const float*)x, n, approximate); break;
+    case MI355X_BF16: gelu_bwd_kernel<bf16><<<grid_for(n), kThreads, 0, s>>>((bf16*)dx, (const bf16*)dy, (const bf16*)x, n, approximate); break;
+    case MI355X_F16: gelu_bwd_kernel<f16><<<grid_for(n), kThreads, 0, s>>>((f16*)dx, (const f16*)dy, (const f16*)x, n, approximate); break;
+    default: return fail(MI355X_EUNSUPPORTED, "mi355x_gelu_bwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("mi355x_gelu_bwd");
+}

@@ -1,0 +1,560 @@
+// Fused flash attention on MFMA (bf16/f16 in, f32 accumulation).
+//
+// Semantics (the reference's fused path, flash_attention_bwd_kernels.mojo:
+// 13-26, 63-66, 1403-1404):
+//   S = scale * Q K^T, masked (causal: key j visible to query i iff j <= i,
+//   top-left aligned, also when Sq != Skv), O = softmax(S) V,
+//   LSE_i = natural-log log-sum-exp of row i (f32, [B, H, Sq]).
+//   Backward: D_i = sum(dO_i * O_i), P = exp(S - LSE), dV = P^T dO,
+//   dP = dO V^T, dS = P * (dP - D), dQ = scale dS K, dK = scale dS^T Q.
+//
+// Layout strategy.  Every product is issued in the orientation that keeps
+// the per-query softmax state in the lane that owns the query:
+//   forward   S^T = K Q^T   (lane = query column, 4 keys per lane-group)
+//             O^T += V^T P^T (P^T fed straight from the S^T accumulators)
+// The MFMA k index of the P^T operand is a permutation of the keys (lane
+// group g carries keys 4g..4g+3 of two 16-key tiles); V^T is read from a
+// transposed LDS tile with the same permutation, which the MFMA sum does not
+// observe.  Q lives in registers for the whole key loop; K and V^T tiles of
+// 64 keys are staged through LDS.  Blocks take 128 queries (4 waves x 32) and
+// the heaviest causal blocks are scheduled first.
+//
+// Backward is two kernels plus a row-term pass (no atomics, every output
+// written exactly once):
+//   dK/dV: a block owns 64 keys (a wave 16); it walks the query blocks that
+//          can see them, recomputing S and dP with the key tile as the MFMA
+//          column, and accumulates dV^T = dO^T P and dK^T = Q^T dS.
+//   dQ:    a block owns 64 queries (a wave 16); it walks the visible key
+//          blocks, recomputing S^T and dP^T, and accumulates dQ^T = K^T dS^T.
+#include <math.h>
+
+#include "common.h"
+#include "mfma.h"
+
+namespace mi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+template <typename T>
+struct alignas(16) V8 {
+  T v[8];
+};
+template <typename T>
+struct alignas(8) V4 {
+  T v[4];
+};
+
+struct AttnArgs {
+  void* o; int64_t o_b, o_h, o_s;
+  float* lse;
+  const void* q; int64_t q_b, q_h, q_s;
+  const void* k; int64_t k_b, k_h, k_s;
+  const void* v; int64_t v_b, v_h, v_s;
+  int64_t B, H, Sq, Skv;
+  float scale_log2;  // scale * log2(e)
+  float scale;
+  int causal;
+};
+
+// Stage a 64-row x D tile (rows row0.., row stride rs) into LDS: row-major
+// [64][D+8] and/or transposed [D][64+8].  Rows past nrows read as zero.
+template <typename T, int D>
+__device__ __forceinline__ void stage_tile(T* rm, T* tr, const T* g, int64_t rs, int64_t row0,
+                                           int64_t nrows) {
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  for (int c = threadIdx.x; c < 64 * CPR; c += kThreads) {
+    const int r = c / CPR, dc = (c % CPR) * 8;
+    V8<T> val;
+    if (row0 + r < nrows) {
+      val = *(const V8<T>*)(g + (row0 + r) * rs + dc);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) val.v[e] = (T)0.f;
+    }
+    if (rm) *(V8<T>*)(rm + r * (D + 8) + dc) = val;
+    if (tr) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tr[(dc + e) * 72 + r] = val.v[e];
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag zero_frag() {
+  typename Mfma<T>::frag f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = (T)0.f;
+  return f;
+}
+
+// 8 keys of the permuted k index from a transposed [D][72] tile:
+// slots 0-3 = cols t0*16+4g..+3, slots 4-7 = cols t1*16+4g..+3.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag perm_frag(const T* tr, int row, int t0, int t1,
+                                                            int g) {
+  typename Mfma<T>::frag f;
+  V4<T> a = *(const V4<T>*)(tr + row * 72 + t0 * 16 + 4 * g);
+  V4<T> b = *(const V4<T>*)(tr + row * 72 + t1 * 16 + 4 * g);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) f[e] = a.v[e], f[4 + e] = b.v[e];
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnArgs p) {
+  typedef typename Mfma<T>::frag frag;
+  constexpr int KS = D / 32;  // MFMA k-steps over the head dim
+  constexpr int DT = D / 16;  // 16-wide head-dim tiles
+  __shared__ __attribute__((aligned(16))) T Ks[64 * (D + 8)];
+  __shared__ __attribute__((aligned(16))) T Vt[D * 72];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const int64_t q0 = qblock * 128;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const T* Q = (const T*)p.q + b * p.q_b + h * p.q_h;
+  const T* K = (const T*)p.k + b * p.k_b + h * p.k_h;
+  const T* V = (const T*)p.v + b * p.v_b + h * p.v_h;
+
+  // Q^T operand fragments (query column = lane row index)
+  frag qf[2][KS];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[qt][ks] = qi < p.Sq ? *(const frag*)(Q + qi * p.q_s + ks * 32 + lg * 8) : zero_frag<T>();
+  }
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  f32x4 oacc[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) oacc[dt][0] = oacc[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int64_t kv_end = p.Skv;
+  if (p.causal) kv_end = min(p.Skv, q0 + 128);
+  for (int64_t kb0 = 0; kb0 < kv_end; kb0 += 64) {
+    __syncthreads();
+    stage_tile<T, D>(Ks, nullptr, K, p.k_s, kb0, p.Skv);
+    stage_tile<T, D>(nullptr, Vt, V, p.v_s, kb0, p.Skv);
+    __syncthreads();
+
+    f32x4 s[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      frag kf[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const frag*)(Ks + (kt * 16 + lr) * (D + 8) + ks * 32 + lg * 8);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a = Mfma<T>::mma(kf[ks], qf[qt][ks], a);
+        s[kt][qt] = a;
+      }
+    }
+    // masking + online softmax (per query = per lane column)
+    const bool need_mask = (kb0 + 64 > p.Skv) || (p.causal && kb0 + 64 > q0 + wave * 32);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = s[kt][qt][e] * p.scale_log2;
+          if (need_mask) {
+            const int64_t kj = kb0 + kt * 16 + lg * 4 + e;
+            if (kj >= p.Skv || (p.causal && kj > qi)) v = -INFINITY;
+          }
+          s[kt][qt][e] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m[qt], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m[qt] - m_use);
+      float rs = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pv = exp2f(s[kt][qt][e] - m_use);
+          s[kt][qt][e] = pv;
+          rs += pv;
+        }
+      rs += __shfl_xor(rs, 16, 64);
+      rs += __shfl_xor(rs, 32, 64);
+      l[qt] = l[qt] * alpha + rs;
+      m[qt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
+    }
+    // O^T += V^T P^T over two 32-key k-steps
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      frag pf[2];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pf[qt][e] = (T)s[2 * ks2][qt][e];
+          pf[qt][4 + e] = (T)s[2 * ks2 + 1][qt][e];
+        }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const frag vf = perm_frag<T>(Vt, dt * 16 + lr, 2 * ks2, 2 * ks2 + 1, lg);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = Mfma<T>::mma(vf, pf[qt], oacc[dt][qt]);
+      }
+    }
+  }
+
+  // epilogue: lane holds O[query lr][d = dt*16 + 4*lg + e]
+  T* O = (T*)p.o + b * p.o_b + h * p.o_h;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+    if (qi >= p.Sq) continue;
+    const float inv = l[qt] > 0.f ? 1.f / l[qt] : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      V4<T> o4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4.v[e] = (T)(oacc[dt][qt][e] * inv);
+      *(V4<T>*)(O + qi * p.o_s + dt * 16 + lg * 4) = o4;
+    }
+    if (lg == 0)
+      p.lse[(b * p.H + h) * p.Sq + qi] = l[qt] > 0.f ? (m[qt] + log2f(l[qt])) * kLn2 : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+struct AttnBwdArgs {
+  AttnArgs f;  // o = forward output (read), q/k/v inputs, lse
+  const void* dout; int64_t do_b, do_h, do_s;
+  void* dq; int64_t dq_b, dq_h, dq_s;
+  void* dk; int64_t dk_b, dk_h, dk_s;
+  void* dv; int64_t dv_b, dv_h, dv_s;
+  float* delta;  // [B, H, Sq]
+};
+
+// D_i = sum_d dO[i, d] * O[i, d]; one wave per row.
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads) attn_bwd_delta(AttnBwdArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // over B*H*Sq
+  const int64_t total = p.f.B * p.f.H * p.f.Sq;
+  if (row >= total) return;
+  const int64_t i = row % p.f.Sq, bh = row / p.f.Sq;
+  const int64_t h = bh % p.f.H, b = bh / p.f.H;
+  const T* O = (const T*)p.f.o + b * p.f.o_b + h * p.f.o_h + i * p.f.o_s;
+  const T* dO = (const T*)p.dout + b * p.do_b + h * p.do_h + i * p.do_s;
+  float acc = 0.f;
+  for (int d = lane; d < D; d += 64) acc += to_f32(O[d]) * to_f32(dO[d]);
+  acc = wave_sum(acc);
+  if (lane == 0) p.delta[row] = acc;
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads) attn_bwd_dkv(AttnBwdArgs p) {
+  typedef typename Mfma<T>::frag frag;
+  constexpr int KS = D / 32, DT = D / 16;
+  __shared__ __attribute__((aligned(16))) T Qs[64 * (D + 8)];
+  __shared__ __attribute__((aligned(16))) T Qt[D * 72];
+  __shared__ __attribute__((aligned(16))) T dOs[64 * (D + 8)];
+  __shared__ __attribute__((aligned(16))) T dOt[D * 72];
+  __shared__ float lse_s[64], delta_s[64];
+
+  const AttnArgs& f = p.f;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int64_t k0 = (int64_t)blockIdx.x * 64;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const T* Q = (const T*)f.q + b * f.q_b + h * f.q_h;
+  const T* K = (const T*)f.k + b * f.k_b + h * f.k_h;
+  const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
+  const T* dO = (const T*)p.dout + b * p.do_b + h * p.do_h;
+  const float* LSE = f.lse + (b * f.H + h) * f.Sq;
+  const float* DEL = p.delta + (b * f.H + h) * f.Sq;
+
+  const int64_t kw = k0 + wave * 16;  // this wave's 16 keys
+  const int64_t kj = kw + lr;        // key of this lane's MFMA column
+  frag kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    kf[ks] = kj < f.Skv ? *(const frag*)(K + kj * f.k_s + ks * 32 + lg * 8) : zero_frag<T>();
+    vf[ks] = kj < f.Skv ? *(const frag*)(V + kj * f.v_s + ks * 32 + lg * 8) : zero_frag<T>();
+  }
+  f32x4 dva[DT], dka[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dva[dt] = dka[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t qstart = f.causal ? (k0 / 64) * 64 : 0;
+  for (int64_t qb0 = qstart; qb0 < f.Sq; qb0 += 64) {
+    __syncthreads();
+    stage_tile<T, D>(Qs, Qt, Q, f.q_s, qb0, f.Sq);
+    stage_tile<T, D>(dOs, dOt, dO, p.do_s, qb0, f.Sq);
+    if (threadIdx.x < 64) {
+      const int64_t qi = qb0 + threadIdx.x;
+      lse_s[threadIdx.x] = qi < f.Sq ? LSE[qi] * kLog2e : 0.f;
+      delta_s[threadIdx.x] = qi < f.Sq ? DEL[qi] : 0.f;
+    }
+    __syncthreads();
+    // S and dP tiles: lane = key column, rows = queries 4*lg + e of tile qt
+    f32x4 pt[4], ds[4];
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const frag qa = *(const frag*)(Qs + (qt * 16 + lr) * (D + 8) + ks * 32 + lg * 8);
+        const frag da = *(const frag*)(dOs + (qt * 16 + lr) * (D + 8) + ks * 32 + lg * 8);
+        sa = Mfma<T>::mma(qa, kf[ks], sa);
+        pa = Mfma<T>::mma(da, vf[ks], pa);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int qr = qt * 16 + lg * 4 + e;
+        const int64_t qi = qb0 + qr;
+        float pv = exp2f(sa[e] * f.scale_log2 - lse_s[qr]);
+        if (qi >= f.Sq || kj >= f.Skv || (f.causal && kj > qi)) pv = 0.f;
+        pt[qt][e] = pv;
+        ds[qt][e] = pv * (pa[e] - delta_s[qr]);
+      }
+    }
+    // dV^T += dO^T P ; dK^T += Q^T dS   (k index = queries, permuted)
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      frag pb, sb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pb[e] = (T)pt[2 * qs][e];
+        pb[4 + e] = (T)pt[2 * qs + 1][e];
+        sb[e] = (T)ds[2 * qs][e];
+        sb[4 + e] = (T)ds[2 * qs + 1][e];
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const frag dof = perm_frag<T>(dOt, dt * 16 + lr, 2 * qs, 2 * qs + 1, lg);
+        const frag qtf = perm_frag<T>(Qt, dt * 16 + lr, 2 * qs, 2 * qs + 1, lg);
+        dva[dt] = Mfma<T>::mma(dof, pb, dva[dt]);
+        dka[dt] = Mfma<T>::mma(qtf, sb, dka[dt]);
+      }
+    }
+  }
+  if (kj >= f.Skv) return;
+  T* dK = (T*)p.dk + b * p.dk_b + h * p.dk_h + kj * p.dk_s;
+  T* dV = (T*)p.dv + b * p.dv_b + h * p.dv_h + kj * p.dv_s;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    V4<T> k4, v4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      k4.v[e] = (T)(dka[dt][e] * f.scale);
+      v4.v[e] = (T)dva[dt][e];
+    }
+    *(V4<T>*)(dK + dt * 16 + lg * 4) = k4;
+    *(V4<T>*)(dV + dt * 16 + lg * 4) = v4;
+  }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads) attn_bwd_dq(AttnBwdArgs p) {
+  typedef typename Mfma<T>::frag frag;
+  constexpr int KS = D / 32, DT = D / 16;
+  __shared__ __attribute__((aligned(16))) T Ks[64 * (D + 8)];
+  __shared__ __attribute__((aligned(16))) T Kt[D * 72];
+  __shared__ __attribute__((aligned(16))) T Vs[64 * (D + 8)];
+
+  const AttnArgs& f = p.f;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const int64_t q0 = qblock * 64;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const T* Q = (const T*)f.q + b * f.q_b + h * f.q_h;
+  const T* K = (const T*)f.k + b * f.k_b + h * f.k_h;
+  const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
+  const T* dO = (const T*)p.dout + b * p.do_b + h * p.do_h;
+
+  const int64_t qi = q0 + wave * 16 + lr;  // this lane's query (MFMA column)
+  const bool qok = qi < f.Sq;
+  frag qf[KS], df[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qf[ks] = qok ? *(const frag*)(Q + qi * f.q_s + ks * 32 + lg * 8) : zero_frag<T>();
+    df[ks] = qok ? *(const frag*)(dO + qi * p.do_s + ks * 32 + lg * 8) : zero_frag<T>();
+  }
+  const float lse2 = qok ? f.lse[(b * f.H + h) * f.Sq + qi] * kLog2e : 0.f;
+  const float dlt = qok ? p.delta[(b * f.H + h) * f.Sq + qi] : 0.f;
+  f32x4 dqa[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dqa[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int64_t kv_end = f.Skv;
+  if (f.causal) kv_end = min(f.Skv, q0 + 64);
+  for (int64_t kb0 = 0; kb0 < kv_end; kb0 += 64) {
+    __syncthreads();
+    stage_tile<T, D>(Ks, Kt, K, f.k_s, kb0, f.Skv);
+    stage_tile<T, D>(Vs, nullptr, V, f.v_s, kb0, f.Skv);
+    __syncthreads();
+    f32x4 ds[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const frag ka = *(const frag*)(Ks + (kt * 16 + lr) * (D + 8) + ks * 32 + lg * 8);
+        const frag va = *(const frag*)(Vs + (kt * 16 + lr) * (D + 8) + ks * 32 + lg * 8);
+        sa = Mfma<T>::mma(ka, qf[ks], sa);
+        pa = Mfma<T>::mma(va, df[ks], pa);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t kj = kb0 + kt * 16 + lg * 4 + e;
+        float pv = exp2f(sa[e] * f.scale_log2 - lse2);
+        if (!qok || kj >= f.Skv || (f.causal && kj > qi)) pv = 0.f;
+        ds[kt][e] = pv * (pa[e] - dlt);
+      }
+    }
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      frag sb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sb[e] = (T)ds[2 * ks2][e];
+        sb[4 + e] = (T)ds[2 * ks2 + 1][e];
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const frag kf = perm_frag<T>(Kt, dt * 16 + lr, 2 * ks2, 2 * ks2 + 1, lg);
+        dqa[dt] = Mfma<T>::mma(kf, sb, dqa[dt]);
+      }
+    }
+  }
+  if (!qok) return;
+  T* dQ = (T*)p.dq + b * p.dq_b + h * p.dq_h + qi * p.dq_s;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    V4<T> q4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q4.v[e] = (T)(dqa[dt][e] * f.scale);
+    *(V4<T>*)(dQ + dt * 16 + lg * 4) = q4;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host
+// ---------------------------------------------------------------------------
+bool strides_ok(const void* ptr, const int64_t* bhs) {
+  return ((uintptr_t)ptr % 16 == 0) && bhs[0] % 8 == 0 && bhs[1] % 8 == 0 && bhs[2] % 8 == 0;
+}
+
+int check_common(int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D, int dtype) {
+  if (dtype != MI355X_BF16 && dtype != MI355X_F16)
+    return fail(MI355X_EUNSUPPORTED, "mi355x_attn: dtype %d not supported (bf16/f16 only)", dtype);
+  if (D != 32 && D != 64 && D != 128)
+    return fail(MI355X_EUNSUPPORTED, "mi355x_attn: head_dim %lld not supported (32/64/128)", (long long)D);
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 || B >= 65536 || H >= 65536)
+    return fail(MI355X_EINVAL, "mi355x_attn: bad shape");
+  return MI355X_OK;
+}
+
+template <typename T, int D>
+int fwd_launch(const AttnArgs& a, hipStream_t s) {
+  dim3 grid(ceil_div(a.Sq, 128), (unsigned)a.H, (unsigned)a.B);
+  attn_fwd_kernel<T, D><<<grid, kThreads, 0, s>>>(a);
+  return check_launch("mi355x_attn_fwd");
+}
+
+template <typename T, int D>
+int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
+  const int64_t rows = a.f.B * a.f.H * a.f.Sq;
+  attn_bwd_delta<T, D><<<ceil_div(rows, 4), kThreads, 0, s>>>(a);
+  dim3 gk(ceil_div(a.f.Skv, 64), (unsigned)a.f.H, (unsigned)a.f.B);
+  attn_bwd_dkv<T, D><<<gk, kThreads, 0, s>>>(a);
+  dim3 gq(ceil_div(a.f.Sq, 64), (unsigned)a.f.H, (unsigned)a.f.B);
+  attn_bwd_dq<T, D><<<gq, kThreads, 0, s>>>(a);
+  return check_launch("mi355x_attn_bwd");
+}
+
+#define MI_ATTN_DISPATCH(dtype, D, FN, ...)                                   \
+  do {                                                                        \
+    if (dtype == MI355X_BF16) {                                               \
+      if (D == 32) return FN<bf16, 32>(__VA_ARGS__);                          \
+      if (D == 64) return FN<bf16, 64>(__VA_ARGS__);                          \
+      return FN<bf16, 128>(__VA_ARGS__);                                      \
+    }                                                                         \
+    if (D == 32) return FN<f16, 32>(__VA_ARGS__);                             \
+    if (D == 64) return FN<f16, 64>(__VA_ARGS__);                             \
+    return FN<f16, 128>(__VA_ARGS__);                                         \
+  } while (0)
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi355x_attn_fwd(void* o, const int64_t* o_bhs, float* lse, const void* q,
+                               const int64_t* q_bhs, const void* k, const int64_t* k_bhs,
+                               const void* v, const int64_t* v_bhs, int64_t batch, int64_t heads,
+                               int64_t sq, int64_t skv, int64_t d, double scale, int causal,
+                               int dtype, mi355x_stream_t stream) {
+  int rc = check_common(batch, heads, sq, skv, d, dtype);
+  if (rc) return rc;
+  MI_REQUIRE(strides_ok(q, q_bhs) && strides_ok(k, k_bhs) && strides_ok(v, v_bhs),
+             "mi355x_attn_fwd: q/k/v need 16-byte aligned bases and strides that are multiples of 8");
+  MI_REQUIRE(((uintptr_t)o % 8 == 0) && o_bhs[0] % 4 == 0 && o_bhs[1] % 4 == 0 && o_bhs[2] % 4 == 0,
+             "mi355x_attn_fwd: o needs 8-byte aligned rows");
+  AttnArgs a{o, o_bhs[0], o_bhs[1], o_bhs[2], lse, q, q_bhs[0], q_bhs[1], q_bhs[2],
+             k, k_bhs[0], k_bhs[1], k_bhs[2], v, v_bhs[0], v_bhs[1], v_bhs[2],
+             batch, heads, sq, skv, (float)(scale * 1.4426950408889634), (float)scale, causal};
+  MI_ATTN_DISPATCH(dtype, d, fwd_launch, a, (hipStream_t)stream);
+}
+
+extern "C" int64_t mi355x_attn_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t sq,
+                                                   int64_t skv, int64_t d) {
+  (void)skv; (void)d;
+  return batch * heads * sq * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs,
+                               void* dv, const int64_t* dv_bhs, const void* dout,
+                               const int64_t* do_bhs, const void* q, const int64_t* q_bhs,
+                               const void* k, const int64_t* k_bhs, const void* v,
+                               const int64_t* v_bhs, const void* o, const int64_t* o_bhs,
+                               const float* lse, int64_t batch, int64_t heads, int64_t sq,
+                               int64_t skv, int64_t d, double scale, int causal, int dtype,
+                               void* workspace, int64_t ws_bytes, mi355x_stream_t stream) {
+  int rc = check_common(batch, heads, sq, skv, d, dtype);
+  if (rc) return rc;
+  MI_REQUIRE(strides_ok(q, q_bhs) && strides_ok(k, k_bhs) && strides_ok(v, v_bhs) &&
+                 strides_ok(dout, do_bhs),
+             "mi355x_attn_bwd: q/k/v/dout need 16-byte aligned bases and strides that are multiples of 8");
+  for (const int64_t* s : {dq_bhs, dk_bhs, dv_bhs})
+    MI_REQUIRE(s[0] % 4 == 0 && s[1] % 4 == 0 && s[2] % 4 == 0, "mi355x_attn_bwd: grads need 8-byte aligned rows");
+  const int64_t need = mi355x_attn_bwd_workspace_bytes(batch, heads, sq, skv, d);
+  if (!workspace || ws_bytes < need)
+    return fail(MI355X_EWORKSPACE, "mi355x_attn_bwd: workspace %lld < %lld", (long long)ws_bytes, (long long)need);
+  AttnBwdArgs a;
+  a.f = AttnArgs{(void*)o, o_bhs[0], o_bhs[1], o_bhs[2], (float*)lse, q, q_bhs[0], q_bhs[1], q_bhs[2],
+                 k, k_bhs[0], k_bhs[1], k_bhs[2], v, v_bhs[0], v_bhs[1], v_bhs[2],
+                 batch, heads, sq, skv, (float)(scale * 1.4426950408889634), (float)scale, causal};
+  a.dout = dout; a.do_b = do_bhs[0]; a.do_h = do_bhs[1]; a.do_s = do_bhs[2];
+  a.dq = dq; a.dq_b = dq_bhs[0]; a.dq_h = dq_bhs[1]; a.dq_s = dq_bhs[2];
+  a.dk = dk; a.dk_b = dk_bhs[0]; a.dk_h = dk_bhs[1]; a.dk_s = dk_bhs[2];
+  a.dv = dv; a.dv_b = dv_bhs[0]; a.dv_h = dv_bhs[1]; a.dv_s = dv_bhs[2];
+  a.delta = (float*)workspace;
+  MI_ATTN_DISPATCH(dtype, d, bwd_launch, a, (hipStream_t)stream);
+}

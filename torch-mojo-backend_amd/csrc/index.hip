@@ -1,0 +1,200 @@
+// Row gathers (index_select, embedding forward) and the deterministic
+// embedding backward.
+//
+// Gathers copy whole rows: one 64-lane wave per output row, 16-byte accesses
+// when the row size and pointers allow, so every row is one coalesced read
+// and one coalesced write.  An index outside [0, rows) is never dereferenced:
+// its row is zero-filled and the caller's error flag is raised.
+//
+// Embedding backward (the counterpart of embedding_dense_backward, which
+// ATen's CPU kernel computes as an index_add in index order):
+//   1. stable radix sort of (idx[n], n) pairs -> positions grouped by row,
+//      ascending within each row;
+//   2. one block per weight row binary-searches its segment and sums the
+//      grad rows in that order into f32, then writes the row once.
+// Every weight row is written exactly once (no zero pre-pass, no atomics),
+// and the per-row summation order equals the sequential CPU order, so f32
+// results match ATen's CPU result bit for bit.
+#include <hipcub/hipcub.hpp>
+
+#include "common.h"
+
+namespace mi {
+namespace {
+
+constexpr int kThreads = 256;
+
+// out[o, j, :] = in[o*so + idx[j]*sj, :], row of `row_bytes` bytes.
+template <typename V>
+__global__ void __launch_bounds__(kThreads)
+    gather_rows(uint8_t* __restrict__ out, const uint8_t* __restrict__ in,
+                const int64_t* __restrict__ idx, int64_t outer, int64_t n_idx, int64_t rows,
+                int64_t row_bytes, int64_t so_bytes, int64_t sj_bytes, int32_t* err) {
+  const int lane = threadIdx.x & 63;
+  const int64_t job = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (job >= outer * n_idx) return;
+  const int64_t o = job / n_idx, j = job % n_idx;
+  const int64_t r = idx[j];
+  V* dst = (V*)(out + job * row_bytes);
+  const int64_t nv = row_bytes / (int64_t)sizeof(V);
+  if (r < 0 || r >= rows) {
+    if (lane == 0 && err) *err = 1;
+    V z;
+    memset(&z, 0, sizeof(V));
+    for (int64_t k = lane; k < nv; k += 64) dst[k] = z;
+    return;
+  }
+  const V* src = (const V*)(in + o * so_bytes + r * sj_bytes);
+  for (int64_t k = lane; k < nv; k += 64) dst[k] = src[k];
+}
+
+int launch_gather(void* out, const void* in, const int64_t* idx, int64_t outer, int64_t n_idx,
+                  int64_t rows, int64_t row_bytes, int64_t so_bytes, int64_t sj_bytes,
+                  int32_t* err, hipStream_t s) {
+  const int64_t jobs = outer * n_idx;
+  if (jobs == 0 || row_bytes == 0) return MI355X_OK;
+  const unsigned grid = ceil_div(jobs, kThreads / 64);
+  auto al = [](int64_t v, int64_t a) { return v % a == 0; };
+  const bool a16 = al(row_bytes, 16) && al(so_bytes, 16) && al(sj_bytes, 16) &&
+                   al((int64_t)(uintptr_t)out, 16) && al((int64_t)(uintptr_t)in, 16);
+  const bool a4 = al(row_bytes, 4) && al(so_bytes, 4) && al(sj_bytes, 4) &&
+                  al((int64_t)(uintptr_t)out, 4) && al((int64_t)(uintptr_t)in, 4);
+  if (a16)
+    gather_rows<uint4><<<grid, kThreads, 0, s>>>((uint8_t*)out, (const uint8_t*)in, idx, outer, n_idx,
+                                                 rows, row_bytes, so_bytes, sj_bytes, err);
+  else if (a4)
+    gather_rows<uint32_t><<<grid, kThreads, 0, s>>>((uint8_t*)out, (const uint8_t*)in, idx, outer,
+                                                    n_idx, rows, row_bytes, so_bytes, sj_bytes, err);
+  else
+    gather_rows<uint8_t><<<grid, kThreads, 0, s>>>((uint8_t*)out, (const uint8_t*)in, idx, outer,
+                                                   n_idx, rows, row_bytes, so_bytes, sj_bytes, err);
+  return check_launch("gather_rows");
+}
+
+__global__ void iota_i32(int32_t* v, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) v[i] = (int32_t)i;
+}
+
+// One block per weight row (grid-stride): ordered segment sum.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    embedding_bwd_rows(T* __restrict__ gw, const T* __restrict__ go,
+                       const int64_t* __restrict__ keys, const int32_t* __restrict__ pos,
+                       int64_t n, int64_t num_weights, int64_t dim, int64_t padding_idx) {
+  for (int64_t row = blockIdx.x; row < num_weights; row += gridDim.x) {
+    // lower_bound(row), upper_bound(row) in the sorted keys
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (keys[mid] < row) lo = mid + 1; else hi = mid;
+    }
+    int64_t end = lo;
+    {
+      int64_t l2 = lo, h2 = n;
+      while (l2 < h2) {
+        const int64_t mid = (l2 + h2) >> 1;
+        if (keys[mid] <= row) l2 = mid + 1; else h2 = mid;
+      }
+      end = l2;
+    }
+    const bool skip = row == padding_idx;
+    for (int64_t c = threadIdx.x; c < dim; c += kThreads) {
+      float acc = 0.f;
+      if (!skip)
+        for (int64_t k = lo; k < end; ++k) acc += to_f32(go[(int64_t)pos[k] * dim + c]);
+      gw[row * dim + c] = from_f32<T>(acc);
+    }
+  }
+}
+
+struct EmbWs {
+  size_t keys_off, vals_in_off, vals_out_off, temp_off, temp_bytes, total;
+};
+
+EmbWs emb_ws_layout(int64_t n) {
+  size_t temp = 0;
+  hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (const int64_t*)nullptr, (int64_t*)nullptr,
+                                     (const int32_t*)nullptr, (int32_t*)nullptr, (int)n);
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  EmbWs w;
+  w.keys_off = 0;
+  w.vals_in_off = up(w.keys_off + (size_t)n * 8);
+  w.vals_out_off = up(w.vals_in_off + (size_t)n * 4);
+  w.temp_off = up(w.vals_out_off + (size_t)n * 4);
+  w.temp_bytes = temp;
+  w.total = up(w.temp_off + temp);
+  return w;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi355x_index_select(void* out, const void* in, int dtype, const int64_t* idx,
+                                   int64_t outer, int64_t n_idx, int64_t in_rows, int64_t inner,
+                                   int64_t in_so, int64_t in_sj, int32_t* err_flag,
+                                   mi355x_stream_t stream) {
+  const int64_t es = (int64_t)dtype_size(dtype);
+  MI_REQUIRE(es > 0, "mi355x_index_select: bad dtype");
+  MI_REQUIRE(outer >= 0 && n_idx >= 0 && inner >= 0, "mi355x_index_select: negative extent");
+  return launch_gather(out, in, idx, outer, n_idx, in_rows, inner * es, in_so * es, in_sj * es,
+                       err_flag, (hipStream_t)stream);
+}
+
+extern "C" int mi355x_embedding_fwd(void* out, const void* weight, int dtype, const int64_t* idx,
+                                    int64_t n_idx, int64_t num_weights, int64_t dim,
+                                    int64_t w_row_stride, int32_t* err_flag,
+                                    mi355x_stream_t stream) {
+  const int64_t es = (int64_t)dtype_size(dtype);
+  MI_REQUIRE(es > 0, "mi355x_embedding_fwd: bad dtype");
+  MI_REQUIRE(n_idx >= 0 && dim >= 0 && num_weights >= 0, "mi355x_embedding_fwd: bad shape");
+  return launch_gather(out, weight, idx, 1, n_idx, num_weights, dim * es, 0, w_row_stride * es,
+                       err_flag, (hipStream_t)stream);
+}
+
+extern "C" int64_t mi355x_embedding_bwd_workspace_bytes(int64_t n_idx, int64_t num_weights) {
+  (void)num_weights;
+  return (int64_t)emb_ws_layout(n_idx).total;
+}
+
+extern "C" int mi355x_embedding_bwd(void* grad_weight, const void* grad_out, int dtype,
+                                    const int64_t* idx, int64_t n_idx, int64_t num_weights,
+                                    int64_t dim, int64_t padding_idx, void* workspace,
+                                    int64_t ws_bytes, mi355x_stream_t stream) {
+  MI_REQUIRE(n_idx >= 0 && n_idx < (1ll << 31), "mi355x_embedding_bwd: bad index count");
+  MI_REQUIRE(num_weights >= 0 && dim >= 0, "mi355x_embedding_bwd: bad shape");
+  if (num_weights == 0 || dim == 0) return MI355X_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const EmbWs w = emb_ws_layout(n_idx);
+  if (n_idx > 0 && (!workspace || ws_bytes < (int64_t)w.total))
+    return fail(MI355X_EWORKSPACE, "mi355x_embedding_bwd: workspace %lld < %lld",
+                (long long)ws_bytes, (long long)w.total);
+  uint8_t* base = (uint8_t*)workspace;
+  int64_t* keys = (int64_t*)(base + w.keys_off);
+  int32_t* vin = (int32_t*)(base + w.vals_in_off);
+  int32_t* vout = (int32_t*)(base + w.vals_out_off);
+  if (n_idx > 0) {
+    iota_i32<<<ceil_div(n_idx, kThreads), kThreads, 0, s>>>(vin, n_idx);
+    size_t temp = w.temp_bytes;
+    hipError_t e = hipcub::DeviceRadixSort::SortPairs(base + w.temp_off, temp, idx, keys, vin, vout,
+                                                      (int)n_idx, 0, 64, s);
+    if (e != hipSuccess) return fail(MI355X_ELAUNCH, "mi355x_embedding_bwd: sort failed: %s", hipGetErrorString(e));
+  }
+  int64_t grid = num_weights < 65536 ? num_weights : 65536;
+  switch (dtype) {
+    case MI355X_F32:
+      embedding_bwd_rows<float><<<(unsigned)grid, kThreads, 0, s>>>((float*)grad_weight, (const float*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx);
+      break;
+    case MI355X_BF16:
+      embedding_bwd_rows<bf16><<<(unsigned)grid, kThreads, 0, s>>>((bf16*)grad_weight, (const bf16*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx);
+      break;
+    case MI355X_F16:
+      embedding_bwd_rows<f16><<<(unsigned)grid, kThreads, 0, s>>>((f16*)grad_weight, (const f16*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx);
+      break;
+    default:
+      return fail(MI355X_EUNSUPPORTED, "mi355x_embedding_bwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("mi355x_embedding_bwd");
+}

@@ -1,0 +1,390 @@
+// LayerNorm forward/backward over rows of `cols` contiguous elements.
+//
+// Forward: one 64-lane wave per row; the row stays in registers (4 elements
+// per lane per vector, NV vectors) so x is read once and y written once: the
+// HBM traffic is rows*cols*(2*sizeof(T)) + 8*rows bytes.  Mean and variance
+// use two passes over the registers (no cancellation), variance biased, as
+// ATen's layer_norm does (mean/rstd in f32).
+//
+// Backward: the same wave-per-row layout computes
+//   xhat = (x-mean)*rstd, g = dy*gamma,
+//   dx   = rstd * (g - mean(g) - xhat*mean(g*xhat)),
+// while each lane accumulates dgamma += dy*xhat and dbeta += dy for its
+// columns over the rows its block owns.  Block partials go to a workspace
+// [blocks, cols] and a second kernel sums them in a fixed order, so the
+// result is deterministic.
+#include "common.h"
+#include "vec.h"
+
+namespace mi {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxBwdBlocks = 512;
+
+template <typename T, int NV>
+__global__ void __launch_bounds__(kThreads)
+    ln_fwd_wave(T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
+                const T* __restrict__ x, const T* __restrict__ gamma, const T* __restrict__ beta,
+                int64_t rows, int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  float v[NV][4];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+      Vec4<T>::load(xr + c, v[j]);
+    } else {
+      v[j][0] = v[j][1] = v[j][2] = v[j][3] = 0.f;
+    }
+    s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  }
+  const float inv_n = 1.f / (float)cols;
+  const float mu = wave_sum(s) * inv_n;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[j][e] - mu;
+        q += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(q) * inv_n;
+  const float r = 1.f / sqrtf(var + eps);
+  T* yr = y + row * cols;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+      float g[4] = {1.f, 1.f, 1.f, 1.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+      if (gamma) Vec4<T>::load(gamma + c, g);
+      if (beta) Vec4<T>::load(beta + c, b);
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - mu) * r * g[e] + b[e];
+      Vec4<T>::store(yr + c, o);
+    }
+  }
+  if (lane == 0) {
+    if (mean_out) mean_out[row] = mu;
+    if (rstd_out) rstd_out[row] = r;
+  }
+}
+
+// Any `cols`: one block per row, three passes over the row.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    ln_fwd_block(T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
+                 const T* __restrict__ x, const T* __restrict__ gamma, const T* __restrict__ beta,
+                 int64_t rows, int64_t cols, float eps) {
+  __shared__ float red[kWaves];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * cols;
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) s += to_f32(xr[c]);
+  const float mu = block_sum(s, red) / (float)cols;
+  float q = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float d = to_f32(xr[c]) - mu;
+    q += d * d;
+  }
+  const float var = block_sum(q, red) / (float)cols;
+  const float r = 1.f / sqrtf(var + eps);
+  T* yr = y + row * cols;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    float o = (to_f32(xr[c]) - mu) * r;
+    if (gamma) o *= to_f32(gamma[c]);
+    if (beta) o += to_f32(beta[c]);
+    yr[c] = from_f32<T>(o);
+  }
+  if (threadIdx.x == 0) {
+    if (mean_out) mean_out[row] = mu;
+    if (rstd_out) rstd_out[row] = r;
+  }
+}
+
+template <typename T, int NV>
+__global__ void __launch_bounds__(kThreads)
+    ln_bwd_wave(T* __restrict__ dx, float* __restrict__ part_g, float* __restrict__ part_b,
+                const T* __restrict__ dy, const T* __restrict__ x, const float* __restrict__ mean,
+                const float* __restrict__ rstd, const T* __restrict__ gamma, int64_t rows, int cols,
+                int64_t rows_per_block) {
+  __shared__ float lds[2][kWaves][NV * 256];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const bool want_params = part_g != nullptr;
+  float pg[NV][4], pb[NV][4], gm[NV][4];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pg[j][e] = pb[j][e] = 0.f, gm[j][e] = 1.f;
+    if (gamma && c < cols) Vec4<T>::load(gamma + c, gm[j]);
+  }
+  const float inv_n = 1.f / (float)cols;
+  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t r1 = min(rows, r0 + rows_per_block);
+  for (int64_t row = r0 + wid; row < r1; row += kWaves) {
+    const float mu = mean[row], rs = rstd[row];
+    float xh[NV][4], gy[NV][4];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (j * 64 + lane) * 4;
+      if (c < cols) {
+        float xv[4], dv[4];
+        Vec4<T>::load(x + row * cols + c, xv);
+        Vec4<T>::load(dy + row * cols + c, dv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xh[j][e] = (xv[e] - mu) * rs;
+          gy[j][e] = dv[e] * gm[j][e];
+          s1 += gy[j][e];
+          s2 += gy[j][e] * xh[j][e];
+          pg[j][e] += dv[e] * xh[j][e];
+          pb[j][e] += dv[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xh[j][e] = gy[j][e] = 0.f;
+      }
+    }
+    if (dx) {
+      const float m1 = wave_sum(s1) * inv_n;
+      const float m2 = wave_sum(s2) * inv_n;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (j * 64 + lane) * 4;
+        if (c < cols) {
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = rs * (gy[j][e] - m1 - xh[j][e] * m2);
+          Vec4<T>::store(dx + row * cols + c, o);
+        }
+      }
+    }
+  }
+  if (!want_params) return;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lds[0][wid][(j * 64 + lane) * 4 + e] = pg[j][e];
+      lds[1][wid][(j * 64 + lane) * 4 + e] = pb[j][e];
+    }
+  __syncthreads();
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
+    float g = 0.f, b = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) g += lds[0][w][c], b += lds[1][w][c];
+    part_g[(int64_t)blockIdx.x * cols + c] = g;
+    part_b[(int64_t)blockIdx.x * cols + c] = b;
+  }
+}
+
+// Any `cols`: dx with one block per row.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    ln_bwd_dx_block(T* __restrict__ dx, const T* __restrict__ dy, const T* __restrict__ x,
+                    const float* __restrict__ mean, const float* __restrict__ rstd,
+                    const T* __restrict__ gamma, int64_t cols) {
+  __shared__ float red[kWaves];
+  const int64_t row = blockIdx.x;
+  const float mu = mean[row], rs = rstd[row];
+  float s1 = 0.f, s2 = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float g = to_f32(dy[row * cols + c]) * (gamma ? to_f32(gamma[c]) : 1.f);
+    const float xh = (to_f32(x[row * cols + c]) - mu) * rs;
+    s1 += g;
+    s2 += g * xh;
+  }
+  const float m1 = block_sum(s1, red) / (float)cols;
+  const float m2 = block_sum(s2, red) / (float)cols;
+  for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
+    const float g = to_f32(dy[row * cols + c]) * (gamma ? to_f32(gamma[c]) : 1.f);
+    const float xh = (to_f32(x[row * cols + c]) - mu) * rs;
+    dx[row * cols + c] = from_f32<T>(rs * (g - m1 - xh * m2));
+  }
+}
+
+// Any `cols`: dgamma/dbeta partials, one thread per column per row chunk.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    ln_bwd_params_cols(float* __restrict__ part_g, float* __restrict__ part_b,
+                       const T* __restrict__ dy, const T* __restrict__ x,
+                       const float* __restrict__ mean, const float* __restrict__ rstd,
+                       int64_t rows, int64_t cols, int64_t rows_per_block) {
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= cols) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_block;
+  const int64_t r1 = min(rows, r0 + rows_per_block);
+  float g = 0.f, b = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float d = to_f32(dy[r * cols + c]);
+    g += d * (to_f32(x[r * cols + c]) - mean[r]) * rstd[r];
+    b += d;
+  }
+  part_g[(int64_t)blockIdx.y * cols + c] = g;
+  part_b[(int64_t)blockIdx.y * cols + c] = b;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    ln_bwd_params_final(T* __restrict__ dgamma, T* __restrict__ dbeta,
+                        const float* __restrict__ part_g, const float* __restrict__ part_b,
+                        int nparts, int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= cols) return;
+  float g = 0.f, b = 0.f;
+  for (int p = 0; p < nparts; ++p) g += part_g[(int64_t)p * cols + c], b += part_b[(int64_t)p * cols + c];
+  if (dgamma) dgamma[c] = from_f32<T>(g);
+  if (dbeta) dbeta[c] = from_f32<T>(b);
+}
+
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int wave_nv(int64_t cols) {
+  if (cols % 4 != 0 || cols > 2048) return 0;
+  const int64_t v = (cols + 255) / 256;
+  if (v <= 1) return 1;
+  if (v <= 2) return 2;
+  if (v <= 3) return 3;
+  if (v <= 4) return 4;
+  return 8;
+}
+
+int bwd_blocks(int64_t rows) {
+  int64_t b = (rows + 15) / 16;
+  if (b > kMaxBwdBlocks) b = kMaxBwdBlocks;
+  if (b < 1) b = 1;
+  return (int)b;
+}
+
+template <typename T>
+int fwd_impl(T* y, float* mean, float* rstd, const T* x, const T* g, const T* b, int64_t rows,
+             int64_t cols, float eps, hipStream_t s) {
+  const size_t al = 4 * sizeof(T);
+  const int nv = (aligned(x, al) && aligned(y, al) && aligned(g, al) && aligned(b, al)) ? wave_nv(cols) : 0;
+  const unsigned grid = ceil_div(rows, kWaves);
+  switch (nv) {
+    case 1: ln_fwd_wave<T, 1><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
+    case 2: ln_fwd_wave<T, 2><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
+    case 3: ln_fwd_wave<T, 3><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
+    case 4: ln_fwd_wave<T, 4><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
+    case 8: ln_fwd_wave<T, 8><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
+    default: ln_fwd_block<T><<<(unsigned)rows, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, cols, eps);
+  }
+  return check_launch("mi355x_layer_norm_fwd");
+}
+
+template <typename T>
+int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* mean,
+             const float* rstd, const T* gamma, int64_t rows, int64_t cols, float* ws,
+             hipStream_t s) {
+  const bool params = dgamma || dbeta;
+  const int nb = bwd_blocks(rows);
+  const int64_t rpb = (rows + nb - 1) / nb;
+  float* pg = params ? ws : nullptr;
+  float* pb = params ? ws + (int64_t)nb * cols : nullptr;
+  const size_t al = 4 * sizeof(T);
+  const int nv = (aligned(dx, al) && aligned(dy, al) && aligned(x, al) && aligned(gamma, al)) ? wave_nv(cols) : 0;
+  if (nv) {
+    if (!dx && !params) return MI355X_OK;
+    switch (nv) {
+#define LN_BWD_CASE(V)                                                                          \
+  case V:                                                                                       \
+    ln_bwd_wave<T, V><<<nb, kThreads, 0, s>>>(dx, pg, pb, dy, x, mean, rstd, gamma, rows,       \
+                                              (int)cols, rpb);                                  \
+    break;
+      LN_BWD_CASE(1)
+      LN_BWD_CASE(2)
+      LN_BWD_CASE(3)
+      LN_BWD_CASE(4)
+      LN_BWD_CASE(8)
+#undef LN_BWD_CASE
+    }
+  } else {
+    if (dx) ln_bwd_dx_block<T><<<(unsigned)rows, kThreads, 0, s>>>(dx, dy, x, mean, rstd, gamma, cols);
+    if (params) {
+      dim3 grid(ceil_div(cols, kThreads), nb);
+      ln_bwd_params_cols<T><<<grid, kThreads, 0, s>>>(pg, pb, dy, x, mean, rstd, rows, cols, rpb);
+    }
+  }
+  if (params)
+    ln_bwd_params_final<T><<<ceil_div(cols, kThreads), kThreads, 0, s>>>(dgamma, dbeta, pg, pb, nb, cols);
+  return check_launch("mi355x_layer_norm_bwd");
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,
+                                     const void* gamma, const void* beta, int64_t rows,
+                                     int64_t cols, double eps, int dtype, mi355x_stream_t stream) {
+  MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_layer_norm_fwd: bad shape [%lld, %lld]",
+             (long long)rows, (long long)cols);
+  if (rows == 0) return MI355X_OK;
+  MI_REQUIRE(y && x, "mi355x_layer_norm_fwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MI355X_F32:
+      return fwd_impl<float>((float*)y, mean, rstd, (const float*)x, (const float*)gamma,
+                             (const float*)beta, rows, cols, (float)eps, s);
+    case MI355X_BF16:
+      return fwd_impl<bf16>((bf16*)y, mean, rstd, (const bf16*)x, (const bf16*)gamma,
+                            (const bf16*)beta, rows, cols, (float)eps, s);
+    case MI355X_F16:
+      return fwd_impl<f16>((f16*)y, mean, rstd, (const f16*)x, (const f16*)gamma,
+                           (const f16*)beta, rows, cols, (float)eps, s);
+  }
+  return fail(MI355X_EUNSUPPORTED, "mi355x_layer_norm_fwd: unsupported dtype %d", dtype);
+}
+
+extern "C" int64_t mi355x_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
+  return 2 * (int64_t)bwd_blocks(rows) * cols * (int64_t)sizeof(float);
+}
+
+extern "C" int mi355x_layer_norm_bwd(void* dx, void* dgamma, void* dbeta, const void* dy,
+                                     const void* x, const float* mean, const float* rstd,
+                                     const void* gamma, int64_t rows, int64_t cols, int dtype,
+                                     void* workspace, int64_t ws_bytes, mi355x_stream_t stream) {
+  MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_layer_norm_bwd: bad shape");
+  hipStream_t s = (hipStream_t)stream;
+  if (rows == 0) {
+    // Empty batch: parameter gradients are zero.
+    const int64_t shape[1] = {cols}, strides[1] = {1};
+    if (dgamma) { int rc = mi355x_fill(dgamma, dtype, strides, shape, 1, 0.0, stream); if (rc) return rc; }
+    if (dbeta) { int rc = mi355x_fill(dbeta, dtype, strides, shape, 1, 0.0, stream); if (rc) return rc; }
+    return MI355X_OK;
+  }
+  if (dgamma || dbeta) {
+    const int64_t need = mi355x_layer_norm_bwd_workspace_bytes(rows, cols);
+    if (!workspace || ws_bytes < need)
+      return fail(MI355X_EWORKSPACE, "mi355x_layer_norm_bwd: workspace %lld < %lld bytes",
+                  (long long)ws_bytes, (long long)need);
+  }
+  switch (dtype) {
+    case MI355X_F32:
+      return bwd_impl<float>((float*)dx, (float*)dgamma, (float*)dbeta, (const float*)dy,
+                             (const float*)x, mean, rstd, (const float*)gamma, rows, cols,
+                             (float*)workspace, s);
+    case MI355X_BF16:
+      return bwd_impl<bf16>((bf16*)dx, (bf16*)dgamma, (bf16*)dbeta, (const bf16*)dy,
+                            (const bf16*)x, mean, rstd, (const bf16*)gamma, rows, cols,
+                            (float*)workspace, s);
+    case MI355X_F16:
+      return bwd_impl<f16>((f16*)dx, (f16*)dgamma, (f16*)dbeta, (const f16*)dy, (const f16*)x,
+                           mean, rstd, (const f16*)gamma, rows, cols, (float*)workspace, s);
+  }
+  return fail(MI355X_EUNSUPPORTED, "mi355x_layer_norm_bwd: unsupported dtype %d", dtype);
+}

@@ -1,0 +1,364 @@
+// Multi-tensor optimizer kernels: fused AdamW, per-tensor norms and in-place
+// foreach updates.
+//
+// All three use the same launch shape: up to kBatch tensors per launch,
+// described in the kernel arguments, each split into fixed-size chunks; the
+// grid is the total chunk count and a block locates its (tensor, chunk) by a
+// scan of the chunk prefix sums.  Contiguous f32 data moves as float4.
+//
+// AdamW (torch.optim.AdamW, decoupled weight decay), per element:
+//   g = maximize ? -g : g;  g /= grad_scale (if given)
+//   p -= lr*wd*p                         (skipped when wd == 0)
+//   m = b1*m + (1-b1)*g;  v = b2*v + (1-b2)*g*g
+//   vmax = max(vmax, v)                  (amsgrad)
+//   p -= (lr/(1-b1^t)) * m / (sqrt(v or vmax)/sqrt(1-b2^t) + eps)
+// with t read from the device step tensor (already incremented by the
+// caller's _foreach_add_), lr from a device scalar if given, and the whole
+// update skipped when *found_inf != 0.  HBM traffic per element: 16 B read
+// (p, g, m, v) + 12 B written (p, m, v) = 28 B.
+#include <math.h>
+
+#include "common.h"
+
+namespace mi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kAdamBatch = 32;
+constexpr int64_t kAdamChunk = 16384;
+
+struct AdamBatch {
+  mi355x_adamw_tensor t[kAdamBatch];
+  int64_t chunk_start[kAdamBatch + 1];
+  int n;
+};
+
+__device__ __forceinline__ int find_tensor(const int64_t* starts, int n, int64_t chunk) {
+  int k = 0;
+  while (k + 1 < n && starts[k + 1] <= chunk) ++k;
+  return k;
+}
+
+struct AdamScalars {
+  float lr, b1, b2, wd, eps;
+  int flags;
+  const float* lr_ptr;
+  const float* grad_scale;
+  const float* found_inf;
+};
+
+__device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v, float* vmax,
+                                          float lr, float b1, float b2, float wd, float eps,
+                                          float step_size, float bc2_sqrt, bool decay) {
+  if (decay) p -= lr * wd * p;
+  m = b1 * m + (1.f - b1) * g;
+  v = b2 * v + (1.f - b2) * g * g;
+  float vv = v;
+  if (vmax) {
+    *vmax = fmaxf(*vmax, v);
+    vv = *vmax;
+  }
+  const float denom = sqrtf(vv) / bc2_sqrt + eps;
+  p -= step_size * m / denom;
+}
+
+__global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalars s) {
+  if (s.found_inf && *s.found_inf != 0.f) return;
+  const int64_t chunk = blockIdx.x;
+  const int k = find_tensor(b.chunk_start, b.n, chunk);
+  const mi355x_adamw_tensor& t = b.t[k];
+  const int64_t begin = (chunk - b.chunk_start[k]) * kAdamChunk;
+  const int64_t end = min(t.numel, begin + kAdamChunk);
+  const float lr = s.lr_ptr ? *s.lr_ptr : s.lr;
+  const float step = *t.step;
+  const float bc1 = 1.f - powf(s.b1, step);
+  const float bc2 = 1.f - powf(s.b2, step);
+  const float step_size = lr / bc1;
+  const float bc2_sqrt = sqrtf(bc2);
+  const bool decay = s.wd != 0.f;
+  const bool maximize = s.flags & MI355X_ADAMW_MAXIMIZE;
+  const float inv_scale = s.grad_scale ? 1.f / *s.grad_scale : 1.f;
+  const bool vec = ((((uintptr_t)t.param | (uintptr_t)t.grad | (uintptr_t)t.exp_avg |
+                      (uintptr_t)t.exp_avg_sq) & 15) == 0) && t.max_exp_avg_sq == nullptr &&
+                   (begin % 4 == 0);
+  int64_t i = begin;
+  if (vec) {
+    const int64_t nv = (end - begin) / 4;
+    for (int64_t q = threadIdx.x; q < nv; q += kThreads) {
+      const int64_t e = begin + q * 4;
+      float4 p = *(float4*)(t.param + e);
+      float4 g = *(const float4*)(t.grad + e);
+      float4 m = *(float4*)(t.exp_avg + e);
+      float4 v = *(float4*)(t.exp_avg_sq + e);
+      float gg[4] = {g.x, g.y, g.z, g.w};
+      float pp[4] = {p.x, p.y, p.z, p.w}, mm[4] = {m.x, m.y, m.z, m.w}, vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float gj = (maximize ? -gg[j] : gg[j]) * inv_scale;
+        adam_elem(pp[j], gj, mm[j], vv[j], nullptr, lr, s.b1, s.b2, s.wd, s.eps, step_size, bc2_sqrt, decay);
+      }
+      *(float4*)(t.param + e) = make_float4(pp[0], pp[1], pp[2], pp[3]);
+      *(float4*)(t.exp_avg + e) = make_float4(mm[0], mm[1], mm[2], mm[3]);
+      *(float4*)(t.exp_avg_sq + e) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+    }
+    i = begin + nv * 4;
+  }
+  for (int64_t e = i + threadIdx.x; e < end; e += kThreads) {
+    float p = t.param[e], m = t.exp_avg[e], v = t.exp_avg_sq[e];
+    float g = t.grad[e];
+    g = (maximize ? -g : g) * inv_scale;
+    adam_elem(p, g, m, v, t.max_exp_avg_sq ? t.max_exp_avg_sq + e : nullptr, lr, s.b1, s.b2, s.wd,
+              s.eps, step_size, bc2_sqrt, decay);
+    t.param[e] = p;
+    t.exp_avg[e] = m;
+    t.exp_avg_sq[e] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// foreach norm
+// ---------------------------------------------------------------------------
+constexpr int kNormBatch = 64;
+constexpr int64_t kNormChunk = 32768;
+
+struct NormBatch {
+  const void* in[kNormBatch];
+  void* out[kNormBatch];
+  int64_t numel[kNormBatch];
+  int64_t chunk_start[kNormBatch + 1];
+  int n;
+};
+
+// kind: 0 = sum x^2, 1 = sum |x|, 2 = max |x|
+template <typename T>
+__global__ void __launch_bounds__(kThreads) norm_partial(NormBatch b, int kind, float* part) {
+  __shared__ float red[kThreads / 64];
+  const int64_t chunk = blockIdx.x;
+  const int k = find_tensor(b.chunk_start, b.n, chunk);
+  const T* x = (const T*)b.in[k];
+  const int64_t begin = (chunk - b.chunk_start[k]) * kNormChunk;
+  const int64_t end = min(b.numel[k], begin + kNormChunk);
+  float acc = 0.f;
+  for (int64_t e = begin + threadIdx.x; e < end; e += kThreads) {
+    const float v = to_f32(x[e]);
+    if (kind == 0) acc += v * v;
+    else if (kind == 1) acc += fabsf(v);
+    else acc = fmaxf(acc, fabsf(v));
+  }
+  if (kind == 2) {
+    acc = wave_max(acc);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    acc = red[0];
+    for (int w = 1; w < kThreads / 64; ++w) acc = fmaxf(acc, red[w]);
+  } else {
+    acc = block_sum(acc, red);
+  }
+  if (threadIdx.x == 0) part[chunk] = acc;
+}
+
+template <typename TO>
+__global__ void __launch_bounds__(kThreads) norm_final(NormBatch b, int kind, const float* part) {
+  __shared__ float red[kThreads / 64];
+  const int k = blockIdx.x;
+  const int64_t c0 = b.chunk_start[k], c1 = b.chunk_start[k + 1];
+  float acc = 0.f;
+  for (int64_t c = c0 + threadIdx.x; c < c1; c += kThreads)
+    acc = kind == 2 ? fmaxf(acc, part[c]) : acc + part[c];
+  if (kind == 2) {
+    acc = wave_max(acc);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    acc = red[0];
+    for (int w = 1; w < kThreads / 64; ++w) acc = fmaxf(acc, red[w]);
+  } else {
+    acc = block_sum(acc, red);
+  }
+  if (threadIdx.x == 0) {
+    const float r = kind == 0 ? sqrtf(acc) : acc;
+    *(TO*)b.out[k] = from_f32<TO>(r);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// foreach apply
+// ---------------------------------------------------------------------------
+constexpr int kApplyBatch = 40;
+constexpr int64_t kApplyChunk = 16384;
+
+struct ApplyBatch {
+  void* a[kApplyBatch];
+  const void* b[kApplyBatch];
+  const void* c[kApplyBatch];
+  double scal[kApplyBatch];
+  int64_t numel[kApplyBatch];
+  int64_t chunk_start[kApplyBatch + 1];
+  int n;
+  int has_scal;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) apply_kernel(ApplyBatch b, int op, float s0, const float* ts) {
+  const int64_t chunk = blockIdx.x;
+  const int k = find_tensor(b.chunk_start, b.n, chunk);
+  T* a = (T*)b.a[k];
+  const T* bb = (const T*)b.b[k];
+  const T* cc = (const T*)b.c[k];
+  const float sc = b.has_scal ? (float)b.scal[k] : s0;
+  const float tsv = ts ? *ts : 0.f;
+  const int64_t begin = (chunk - b.chunk_start[k]) * kApplyChunk;
+  const int64_t end = min(b.numel[k], begin + kApplyChunk);
+  for (int64_t e = begin + threadIdx.x; e < end; e += kThreads) {
+    float x = to_f32(a[e]);
+    switch (op) {
+      case MI355X_OP_ADD: x += s0 * (bb ? to_f32(bb[e]) : 1.f); break;
+      case MI355X_OP_MUL: x *= ts ? tsv : (b.has_scal ? sc : (bb ? to_f32(bb[e]) : s0)); break;
+      case MI355X_OP_DIV: x /= ts ? tsv : (b.has_scal ? sc : (bb ? to_f32(bb[e]) : s0)); break;
+      case MI355X_OP_LERP: { float y = to_f32(bb[e]); x = (fabsf(s0) < 0.5f) ? x + s0 * (y - x) : y - (y - x) * (1.f - s0); break; }
+      case MI355X_OP_ADDCMUL: x += sc * to_f32(bb[e]) * to_f32(cc[e]); break;
+      case MI355X_OP_ADDCDIV: x += sc * (to_f32(bb[e]) / to_f32(cc[e])); break;
+      case MI355X_OP_SQRT: x = sqrtf(x); break;
+    }
+    a[e] = from_f32<T>(x);
+  }
+}
+
+int64_t chunks_of(int64_t numel, int64_t chunk) { return (numel + chunk - 1) / chunk; }
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi355x_fused_adamw(const mi355x_adamw_tensor* tensors, int n, double lr,
+                                  const float* lr_ptr, double beta1, double beta2,
+                                  double weight_decay, double eps, int flags,
+                                  const float* grad_scale, const float* found_inf,
+                                  mi355x_stream_t stream) {
+  MI_REQUIRE(n >= 0 && (n == 0 || tensors), "mi355x_fused_adamw: bad tensor list");
+  hipStream_t s = (hipStream_t)stream;
+  AdamScalars sc{(float)lr, (float)beta1, (float)beta2, (float)weight_decay, (float)eps, flags,
+                 lr_ptr, grad_scale, found_inf};
+  for (int base = 0; base < n; base += kAdamBatch) {
+    AdamBatch b{};
+    b.n = 0;
+    int64_t chunks = 0;
+    for (int j = base; j < n && b.n < kAdamBatch; ++j) {
+      const mi355x_adamw_tensor& t = tensors[j];
+      MI_REQUIRE(t.numel >= 0, "mi355x_fused_adamw: negative numel");
+      MI_REQUIRE(t.numel == 0 || (t.param && t.grad && t.exp_avg && t.exp_avg_sq && t.step),
+                 "mi355x_fused_adamw: null pointer in tensor %d", j);
+      MI_REQUIRE(!(flags & MI355X_ADAMW_AMSGRAD) || t.numel == 0 || t.max_exp_avg_sq,
+                 "mi355x_fused_adamw: amsgrad needs max_exp_avg_sq (tensor %d)", j);
+      b.t[b.n] = t;
+      if (!(flags & MI355X_ADAMW_AMSGRAD)) b.t[b.n].max_exp_avg_sq = nullptr;
+      b.chunk_start[b.n] = chunks;
+      chunks += chunks_of(t.numel, kAdamChunk);
+      ++b.n;
+    }
+    b.chunk_start[b.n] = chunks;
+    if (chunks == 0) continue;
+    adamw_kernel<<<(unsigned)chunks, kThreads, 0, s>>>(b, sc);
+    int rc = check_launch("mi355x_fused_adamw");
+    if (rc) return rc;
+  }
+  return MI355X_OK;
+}
+
+extern "C" int64_t mi355x_foreach_norm_workspace_bytes(const int64_t* numels, int n) {
+  int64_t total = 0;
+  for (int j = 0; j < n; ++j) total += chunks_of(numels[j], kNormChunk);
+  return total * (int64_t)sizeof(float) + 256;
+}
+
+extern "C" int mi355x_foreach_norm(void* const* outs, int out_dtype, const void* const* ins,
+                                   int in_dtype, const int64_t* numels, int n, double ord,
+                                   void* workspace, int64_t ws_bytes, mi355x_stream_t stream) {
+  int kind;
+  if (ord == 2.0) kind = 0;
+  else if (ord == 1.0) kind = 1;
+  else if (isinf(ord) && ord > 0) kind = 2;
+  else return fail(MI355X_EUNSUPPORTED, "mi355x_foreach_norm: ord %g not supported", ord);
+  MI_REQUIRE(in_dtype == MI355X_F32 || in_dtype == MI355X_BF16 || in_dtype == MI355X_F16,
+             "mi355x_foreach_norm: unsupported input dtype");
+  MI_REQUIRE(out_dtype == MI355X_F32 || out_dtype == MI355X_BF16 || out_dtype == MI355X_F16,
+             "mi355x_foreach_norm: unsupported output dtype");
+  const int64_t need = mi355x_foreach_norm_workspace_bytes(numels, n);
+  if (n > 0 && (!workspace || ws_bytes < need))
+    return fail(MI355X_EWORKSPACE, "mi355x_foreach_norm: workspace %lld < %lld", (long long)ws_bytes, (long long)need);
+  hipStream_t s = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  for (int base = 0; base < n; base += kNormBatch) {
+    NormBatch b{};
+    int64_t chunks = 0;
+    b.n = 0;
+    for (int j = base; j < n && b.n < kNormBatch; ++j) {
+      b.in[b.n] = ins[j];
+      b.out[b.n] = outs[j];
+      b.numel[b.n] = numels[j];
+      b.chunk_start[b.n] = chunks;
+      chunks += chunks_of(numels[j], kNormChunk);
+      ++b.n;
+    }
+    b.chunk_start[b.n] = chunks;
+    if (chunks > 0) {
+      switch (in_dtype) {
+        case MI355X_F32: norm_partial<float><<<(unsigned)chunks, kThreads, 0, s>>>(b, kind, part); break;
+        case MI355X_BF16: norm_partial<bf16><<<(unsigned)chunks, kThreads, 0, s>>>(b, kind, part); break;
+        default: norm_partial<f16><<<(unsigned)chunks, kThreads, 0, s>>>(b, kind, part); break;
+      }
+    }
+    switch (out_dtype) {
+      case MI355X_F32: norm_final<float><<<b.n, kThreads, 0, s>>>(b, kind, part); break;
+      case MI355X_BF16: norm_final<bf16><<<b.n, kThreads, 0, s>>>(b, kind, part); break;
+      default: norm_final<f16><<<b.n, kThreads, 0, s>>>(b, kind, part); break;
+    }
+    int rc = check_launch("mi355x_foreach_norm");
+    if (rc) return rc;
+    part += chunks;
+  }
+  return MI355X_OK;
+}
+
+extern "C" int mi355x_foreach_apply(int op, void* const* a, const void* const* b,
+                                    const void* const* c, const double* scalars,
+                                    const int64_t* numels, int n, int dtype, double s0,
+                                    const float* tensor_scalar, mi355x_stream_t stream) {
+  switch (op) {
+    case MI355X_OP_ADD: case MI355X_OP_MUL: case MI355X_OP_DIV: case MI355X_OP_SQRT: break;
+    case MI355X_OP_LERP: MI_REQUIRE(b, "mi355x_foreach_apply: lerp needs b"); break;
+    case MI355X_OP_ADDCMUL: case MI355X_OP_ADDCDIV: MI_REQUIRE(b && c, "mi355x_foreach_apply: needs b and c"); break;
+    default: return fail(MI355X_EUNSUPPORTED, "mi355x_foreach_apply: op %d not supported", op);
+  }
+  MI_REQUIRE(dtype == MI355X_F32 || dtype == MI355X_BF16 || dtype == MI355X_F16,
+             "mi355x_foreach_apply: unsupported dtype");
+  hipStream_t s = (hipStream_t)stream;
+  for (int base = 0; base < n; base += kApplyBatch) {
+    ApplyBatch bt{};
+    int64_t chunks = 0;
+    bt.n = 0;
+    bt.has_scal = scalars != nullptr;
+    for (int j = base; j < n && bt.n < kApplyBatch; ++j) {
+      bt.a[bt.n] = a[j];
+      bt.b[bt.n] = b ? b[j] : nullptr;
+      bt.c[bt.n] = c ? c[j] : nullptr;
+      bt.scal[bt.n] = scalars ? scalars[j] : 0.0;
+      bt.numel[bt.n] = numels[j];
+      bt.chunk_start[bt.n] = chunks;
+      chunks += chunks_of(numels[j], kApplyChunk);
+      ++bt.n;
+    }
+    bt.chunk_start[bt.n] = chunks;
+    if (chunks == 0) continue;
+    switch (dtype) {
+      case MI355X_F32: apply_kernel<float><<<(unsigned)chunks, kThreads, 0, s>>>(bt, op, (float)s0, tensor_scalar); break;
+      case MI355X_BF16: apply_kernel<bf16><<<(unsigned)chunks, kThreads, 0, s>>>(bt, op, (float)s0, tensor_scalar); break;
+      default: apply_kernel<f16><<<(unsigned)chunks, kThreads, 0, s>>>(bt, op, (float)s0, tensor_scalar); break;
+    }
+    int rc = check_launch("mi355x_foreach_apply");
+    if (rc) return rc;
+  }
+  return MI355X_OK;
+}

@@ -1,0 +1,217 @@
+"""Loader for the gfx950 kernel library (`libmi355x_kernels.so`).
+
+The reference builds one CPython extension per (op, dtype) variant with the
+Mojo compiler and caches it (torch_mojo_backend/eager_kernels/__init__.py:
+409-418, 463-510).  Here every kernel is compiled ahead of time by hipcc into
+one shared library with a C ABI (`include/mi355x_kernels.h`), so there is no
+JIT, no variant cache and no background build pool: loading is a single
+`ctypes.CDLL`.
+
+`lib()` returns the loaded library with argtypes/restype set for every
+exported function.  A missing or stale library raises `KernelLibraryError`
+with the build command: there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_NAME = "libmi355x_kernels.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+ABI_VERSION = 1
+
+c_int = ctypes.c_int
+c_i64 = ctypes.c_int64
+c_double = ctypes.c_double
+c_vp = ctypes.c_void_p
+c_char_p = ctypes.c_char_p
+P_i64 = ctypes.POINTER(ctypes.c_int64)
+P_int = ctypes.POINTER(ctypes.c_int)
+P_vp = ctypes.POINTER(ctypes.c_void_p)
+P_double = ctypes.POINTER(ctypes.c_double)
+
+
+class AdamWTensor(ctypes.Structure):
+    """`mi355x_adamw_tensor` (layout of include/mi355x_kernels.h)."""
+
+    _fields_ = [
+        ("param", c_vp),
+        ("grad", c_vp),
+        ("exp_avg", c_vp),
+        ("exp_avg_sq", c_vp),
+        ("max_exp_avg_sq", c_vp),
+        ("step", c_vp),
+        ("numel", c_i64),
+    ]
+
+
+# name -> (restype, argtypes).  Kept in the order of the header.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "mi355x_abi_version": (c_int, []),
+    "mi355x_last_error": (c_char_p, []),
+    "mi355x_target": (c_char_p, []),
+    "mi355x_copy": (c_int, [c_vp, c_int, P_i64, c_vp, c_int, P_i64, P_i64, c_int, c_vp]),
+    "mi355x_fill": (c_int, [c_vp, c_int, P_i64, P_i64, c_int, c_double, c_vp]),
+    "mi355x_arange": (c_int, [c_vp, c_int, c_i64, c_double, c_double, c_vp]),
+    "mi355x_map": (
+        c_int,
+        [c_int, c_vp, c_int, c_int, P_vp, P_int, P_i64, P_i64, c_int, c_double, c_double, c_vp],
+    ),
+    "mi355x_reduce_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
+    "mi355x_reduce": (
+        c_int,
+        [c_int, c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
+    ),
+    "mi355x_argreduce": (
+        c_int,
+        [c_int, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp],
+    ),
+    "mi355x_index_select": (
+        c_int,
+        [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
+    ),
+    "mi355x_embedding_fwd": (
+        c_int,
+        [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
+    ),
+    "mi355x_embedding_bwd_workspace_bytes": (c_i64, [c_i64, c_i64]),
+    "mi355x_embedding_bwd": (
+        c_int,
+        [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
+    ),
+    "mi355x_layer_norm_fwd": (
+        c_int,
+        [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],
+    ),
+    "mi355x_layer_norm_bwd_workspace_bytes": (c_i64, [c_i64, c_i64]),
+    "mi355x_layer_norm_bwd": (
+        c_int,
+        [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_int, c_vp, c_i64, c_vp],
+    ),
+    "mi355x_gelu_fwd": (c_int, [c_vp, c_vp, c_i64, c_int, c_int, c_vp]),
+    "mi355x_gelu_bwd": (c_int, [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_vp]),
+    "mi355x_softmax_fwd": (c_int, [c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_int, c_vp]),
+    "mi355x_softmax_bwd": (
+        c_int,
+        [c_vp, c_int, c_vp, c_int, c_vp, c_int, c_i64, c_i64, c_int, c_vp],
+    ),
+    "mi355x_nll_workspace_bytes": (c_i64, [c_i64]),
+    "mi355x_nll_fwd": (
+        c_int,
+        [c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_i64, c_i64, c_int, c_i64, c_vp, c_vp, c_i64, c_vp],
+    ),
+    "mi355x_nll_bwd": (
+        c_int,
+        [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_int, c_i64, c_int, c_vp],
+    ),
+    "mi355x_fused_adamw": (
+        c_int,
+        [
+            ctypes.POINTER(AdamWTensor), c_int, c_double, c_vp, c_double, c_double,
+            c_double, c_double, c_int, c_vp, c_vp, c_vp,
+        ],
+    ),
+    "mi355x_foreach_norm_workspace_bytes": (c_i64, [P_i64, c_int]),
+    "mi355x_foreach_norm": (
+        c_int,
+        [P_vp, c_int, P_vp, c_int, P_i64, c_int, c_double, c_vp, c_i64, c_vp],
+    ),
+    "mi355x_foreach_apply": (
+        c_int,
+        [c_int, P_vp, P_vp, P_vp, P_double, P_i64, c_int, c_int, c_double, c_vp, c_vp],
+    ),
+    "mi355x_gemm_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_int]),
+    "mi355x_gemm": (
+        c_int,
+        [
+            c_vp, c_int, c_i64, c_i64,
+            c_vp, c_i64, c_i64, c_i64,
+            c_vp, c_i64, c_i64, c_i64,
+            c_int, c_vp, c_int, c_int,
+            c_i64, c_i64, c_i64, c_i64,
+            c_vp, c_i64, c_vp,
+        ],
+    ),
+    "mi355x_attn_fwd": (
+        c_int,
+        [
+            c_vp, P_i64, c_vp, c_vp, P_i64, c_vp, P_i64, c_vp, P_i64,
+            c_i64, c_i64, c_i64, c_i64, c_i64, c_double, c_int, c_int, c_vp,
+        ],
+    ),
+    "mi355x_attn_bwd_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "mi355x_attn_bwd": (
+        c_int,
+        [
+            c_vp, P_i64, c_vp, P_i64, c_vp, P_i64, c_vp, P_i64,
+            c_vp, P_i64, c_vp, P_i64, c_vp, P_i64, c_vp, P_i64, c_vp,
+            c_i64, c_i64, c_i64, c_i64, c_i64, c_double, c_int, c_int,
+            c_vp, c_i64, c_vp,
+        ],
+    ),
+}
+
+
+class KernelLibraryError(RuntimeError):
+    """The gfx950 kernel library is missing, stale or reported an error."""
+
+
+class KernelCallError(RuntimeError):
+    """A library call returned a nonzero status."""
+
+    def __init__(self, name: str, code: int, message: str):
+        super().__init__(f"{name} failed (status {code}): {message}")
+        self.code = code
+
+
+_LIB = None
+
+
+def _load() -> ctypes.CDLL:
+    path = Path(os.environ.get("MI355X_KERNELS_LIB", LIB_PATH))
+    if not path.exists():
+        raise KernelLibraryError(
+            f"{path} is missing: build it with `python torch-mojo-backend_amd/build.py`"
+            " (or __graft_entry__.build())"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        try:
+            fn = getattr(lib, name)
+        except AttributeError as exc:
+            raise KernelLibraryError(f"{path} does not export {name}: rebuild it") from exc
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = lib.mi355x_abi_version()
+    if version != ABI_VERSION:
+        raise KernelLibraryError(f"{path} has ABI {version}, expected {ABI_VERSION}: rebuild it")
+    return lib
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded kernel library (loaded on first use)."""
+    global _LIB
+    if _LIB is None:
+        _LIB = _load()
+    return _LIB
+
+
+def set_library_for_tests(replacement) -> object:
+    """Swap the library object (host-only tests); returns the previous one."""
+    global _LIB
+    previous = _LIB
+    _LIB = replacement
+    return previous
+
+
+def last_error() -> str:
+    msg = lib().mi355x_last_error()
+    return msg.decode() if isinstance(msg, bytes) else str(msg)
+
+
+def check(name: str, status: int) -> None:
+    """Raise KernelCallError when a library call returned nonzero."""
+    if status:
+        raise KernelCallError(name, status, last_error())

@@ -1,0 +1,28 @@
+"""The dispatch bracket between `__torch_dispatch__` and the op table.
+
+Counterpart of the reference's deferred_compile.dispatch
+(torch_mojo_backend/mojo_device/deferred_compile.py:77-90).  There is no
+kernel-call queue here: every kernel is compiled ahead of time, so a launch
+is never blocked on a build and ops are issued directly, in order, on the
+device stream.  `drain()` therefore reduces to a stream synchronisation at
+host reads (`synchronize`, `.item()`, `.cpu()`).
+"""
+
+from __future__ import annotations
+
+import torch
+
+# OpOverload -> python implementation (filled by register_mojo_devices)
+DIRECT: dict = {}
+
+_DISABLE = torch._C._DisableTorchDispatch
+
+
+def dispatch(func, args, kwargs):
+    impl = DIRECT.get(func)
+    if impl is not None:
+        return impl(*args, **kwargs)
+    # Not a direct entry: let the dispatcher pick the PrivateUse1 kernel (one
+    # of ours, or a composite decomposition whose pieces come back here).
+    with _DISABLE():
+        return func(*args, **kwargs)

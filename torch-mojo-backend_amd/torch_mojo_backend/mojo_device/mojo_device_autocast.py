@@ -1,0 +1,80 @@
+"""AutocastPrivateUse1 policies for eager mojo tensors.
+
+Same policy table as the reference (torch_mojo_backend/mojo_device/
+mojo_device_autocast.py:537-567): matmul and attention run in the active
+lower precision; layer_norm and NLL run in f32; everything else falls
+through.  Casts are ordinary ``_to_copy`` ops on the device.
+"""
+
+from __future__ import annotations
+
+import functools
+from collections.abc import Mapping
+
+import torch
+
+_registered = False
+_fallback_library = None
+_aten_library = None
+
+_AUTOCAST_KEYSET = torch._C.DispatchKeySet(torch._C.DispatchKey.AutocastPrivateUse1)
+
+
+def _cast_mojo_floating(value, dtype):
+    if isinstance(value, torch.Tensor):
+        if (
+            value.device.type == "mojo"
+            and value.is_floating_point()
+            and value.dtype != torch.float64
+            and value.dtype != dtype
+        ):
+            return value.to(dtype=dtype)
+        return value
+    if isinstance(value, tuple):
+        return tuple(_cast_mojo_floating(v, dtype) for v in value)
+    if isinstance(value, list):
+        return [_cast_mojo_floating(v, dtype) for v in value]
+    if isinstance(value, Mapping):
+        return {k: _cast_mojo_floating(v, dtype) for k, v in value.items()}
+    return value
+
+
+def _policy_wrapper(op, dtype_getter):
+    @functools.wraps(op)
+    def wrapper(*args, **kwargs):
+        with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYSET):
+            dtype = dtype_getter()
+            return op(*_cast_mojo_floating(args, dtype), **_cast_mojo_floating(kwargs, dtype))
+
+    return wrapper
+
+
+def register_autocast_ops() -> None:
+    global _registered, _fallback_library, _aten_library
+    if _registered:
+        return
+    _fallback_library = torch.library.Library("_", "IMPL", "AutocastPrivateUse1")
+    _fallback_library.fallback(torch.library.fallthrough_kernel)
+    _aten_library = torch.library.Library("aten", "IMPL", "AutocastPrivateUse1")
+    lower = (
+        torch.ops.aten.addmm.default,
+        torch.ops.aten.bmm.default,
+        torch.ops.aten.linear.default,
+        torch.ops.aten.matmul.default,
+        torch.ops.aten.mm.default,
+        torch.ops.aten.scaled_dot_product_attention.default,
+        torch.ops.aten._scaled_dot_product_flash_attention.default,
+    )
+    fp32 = (
+        torch.ops.aten.layer_norm.default,
+        torch.ops.aten.native_layer_norm.default,
+        torch.ops.aten.nll_loss.default,
+        torch.ops.aten.nll_loss_forward.default,
+    )
+    for op in lower:
+        _aten_library.impl(
+            op._schema.name, _policy_wrapper(op, lambda: torch.get_autocast_dtype("mojo"))
+        )
+    for op in fp32:
+        _aten_library.impl(op._schema.name, _policy_wrapper(op, lambda: torch.float32))
+    _registered = True

@@ -1,0 +1,59 @@
+"""AutogradPrivateUse1 implementation of ``aten::scaled_dot_product_attention``.
+
+Routing follows the reference (torch_mojo_backend/mojo_device/
+mojo_device_autograd.py:565-643), re-targeted at gfx950:
+
+- grad needed and the fused kernels accept the inputs -> the ATen flash op
+  pair ``_scaled_dot_product_flash_attention`` / ``..._backward``; generated
+  autograd saves (q, k, v, out, logsumexp) and calls the backward op, which
+  recomputes P from the saved natural-log LSE (never the S x S matrix);
+- no grad -> ``scaled_dot_product_attention`` on the device (fused kernel or
+  decomposition);
+- otherwise (masks, GQA, ...) -> the math decomposition built from device
+  ops, differentiated through its pieces.
+
+There is no queue to drain before these routes: kernels are issued directly.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ..eager_kernels import aten_fast
+
+_registered = False
+_library = None
+
+
+def _scaled_dot_product_attention_autograd(
+    query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, *, scale=None,
+    enable_gqa=False,
+):
+    needs_backward = torch.is_grad_enabled() and (
+        query.requires_grad or key.requires_grad or value.requires_grad
+    )
+    fused = aten_fast.fused_fa_inputs(
+        query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa
+    )
+    if not needs_backward:
+        with torch._C._AutoDispatchBelowAutograd():
+            return torch.ops.aten.scaled_dot_product_attention.default(
+                query, key, value, attn_mask, dropout_p, is_causal, scale=scale,
+                enable_gqa=enable_gqa,
+            )
+    if fused is not None:
+        return torch.ops.aten._scaled_dot_product_flash_attention.default(
+            query, key, value, dropout_p, is_causal, False, scale=scale
+        )[0]
+    return aten_fast.sdpa_math(
+        query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa
+    )
+
+
+def register_autograd_ops() -> None:
+    global _registered, _library
+    if _registered:
+        return
+    _library = torch.library.Library("aten", "IMPL", "AutogradPrivateUse1")
+    _library.impl("scaled_dot_product_attention", _scaled_dot_product_attention_autograd)
+    _registered = True
