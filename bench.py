@@ -1,0 +1,281 @@
+"""Benchmark: nanoGPT-124M eager training on the mojo device (one MI355X).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only all|model|sdpa|gemm|hbm]
+
+Prints ONE JSON line.  `value` is the whole-job training throughput in
+tokens/s of BASELINE config 3 (GPT-2 small, batch 16 x 1024 tokens, bf16
+autocast, fused AdamW, clip_grad_norm_ 1.0; synthetic uniform token ids,
+random N(0, 0.02) init), timed over K steps between device synchronisations
+after W warmup steps.  Alongside it:
+  roofline      causal SDPA fwd+bwd at config 1 ([8,12,1024,64] bf16) on
+                MFMA: algorithmic 45.097 GFLOP per fwd+bwd / the measured
+                average time of the four attention kernels (HIP events on the
+                stream they run on), against 2.5 PFLOP/s dense bf16;
+  gemm          config 2 sweep (M = 16384, fwd / dX / dW) TFLOP/s;
+  hbm           HBM-bound kernels at config 3 shapes, GB/s vs 8 TB/s;
+  cpu_baseline  the same training step in f32 on the host's cores with
+                stock PyTorch CPU (the reference's oracle), on a bounded
+                sample (one 1 x 1024-token step).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "torch-mojo-backend_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+METRIC = "nanoGPT-124M eager train tokens/s; SDPA fwd+bwd TFLOP/s and % of bf16 MFMA peak"
+
+
+def _events():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_gpu(fn, iters, warmup=2):
+    """Average milliseconds per call of fn() with HIP events on the default
+    stream (the stream every mojo kernel is launched on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = _events()
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def bench_model(args):
+    from torch_mojo_backend.gpt2 import (BETAS, GRAD_CLIP, LEARNING_RATE, WEIGHT_DECAY, GPT, GPTConfig,
+                                         make_batches, training_step)
+
+    torch.manual_seed(1337)
+    model = GPT(GPTConfig())
+    nparams = model.num_params()
+    model.to("mojo")
+    opt = model.configure_optimizers(WEIGHT_DECAY, LEARNING_RATE, BETAS, fused=True)
+    batches = make_batches(args.batch, args.block, 50257, 2, 20260718, "mojo")
+    losses = []
+    for i in range(args.warmup):
+        x, y = batches[i % 2]
+        losses.append(training_step(model, opt, x, y, torch.bfloat16, grad_clip=GRAD_CLIP))
+    torch.accelerator.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        x, y = batches[(args.warmup + i) % 2]
+        losses.append(training_step(model, opt, x, y, torch.bfloat16, grad_clip=GRAD_CLIP))
+    torch.accelerator.synchronize()
+    dt = time.perf_counter() - t0
+    vals = [float(l.item()) for l in losses]
+    tokens = args.batch * args.block * args.steps
+    return {
+        "tokens_per_s": tokens / dt,
+        "ms_per_step": 1000.0 * dt / args.steps,
+        "params": nparams,
+        "loss_first": vals[0],
+        "loss_last": vals[-1],
+        "losses": [round(v, 5) for v in vals],
+    }
+
+
+def bench_sdpa(iters):
+    """Config 1: causal SDPA fwd+bwd [8,12,1024,64] bf16 through the product path."""
+    from torch_mojo_backend.eager_kernels import aten_fast as F
+
+    B, H, S, D = 8, 12, 1024, 64
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(B, H, S, D, generator=g).bfloat16().to("mojo") for _ in range(4))
+    out, lse = F.fused_flash_attention_forward(q, k, v, True, None)
+    fwd_ms = time_gpu(lambda: F.fused_flash_attention_forward(q, k, v, True, None), iters)
+    bwd_ms = time_gpu(lambda: F.fused_flash_attention_backward(do, q, k, v, out, lse, True, None), iters)
+    fwd_flop = 4.0 * B * H * S * S * D / 2
+    bwd_flop = 2.5 * fwd_flop
+    tot_ms = fwd_ms + bwd_ms
+    achieved = (fwd_flop + bwd_flop) / (tot_ms * 1e-3) / 1e12
+    return {
+        "shape": [B, H, S, D],
+        "fwd_ms": fwd_ms,
+        "bwd_ms": bwd_ms,
+        "fwd_tflops": fwd_flop / (fwd_ms * 1e-3) / 1e12,
+        "bwd_tflops": bwd_flop / (bwd_ms * 1e-3) / 1e12,
+        "fwd_bwd_tflops": achieved,
+        "frac_of_peak": achieved / PEAK_BF16_TFLOPS,
+        "gflop_per_fwd_bwd": (fwd_flop + bwd_flop) / 1e9,
+    }
+
+
+def bench_gemm(iters):
+    """Config 2: bf16 GEMMs at M = 16384 (fwd x W^T + bias, dX = dY W, dW = dY^T X)."""
+    from torch_mojo_backend.eager_kernels import aten_fast as F
+
+    M = 16384
+    g = torch.Generator().manual_seed(0)
+    rows = []
+    for K, N in ((768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 50304)):
+        x = torch.randn(M, K, generator=g).bfloat16().to("mojo")
+        w = (torch.randn(N, K, generator=g) * 0.02).bfloat16().to("mojo")
+        bias = (torch.randn(N, generator=g) * 0.02).bfloat16().to("mojo")
+        dy = torch.randn(M, N, generator=g).bfloat16().to("mojo")
+        flop = 2.0 * M * N * K
+        r = {"K": K, "N": N, "gflop": flop / 1e9}
+        wt = F.fast_aten_t(w)
+        dyt = F.fast_aten_t(dy)
+        for name, fn in (
+            ("fwd", lambda: F.fast_aten_addmm(bias, x, wt)),
+            ("dX", lambda: F.fast_aten_mm(dy, w)),
+            ("dW", lambda: F.fast_aten_mm(dyt, x)),
+        ):
+            ms = time_gpu(fn, iters)
+            r[name + "_tflops"] = flop / (ms * 1e-3) / 1e12
+        rows.append(r)
+        del x, w, bias, dy, wt, dyt
+    return rows
+
+
+def bench_hbm(iters):
+    """HBM-bound kernels at config 3 shapes; GB/s from algorithmic bytes."""
+    import torch.nn.functional as Fn
+
+    from torch_mojo_backend.eager_kernels import aten_fast as F
+
+    g = torch.Generator().manual_seed(0)
+    out = []
+    x = torch.randn(16384, 768, generator=g).to("mojo")
+    w = torch.randn(768, generator=g).to("mojo")
+    b = torch.randn(768, generator=g).to("mojo")
+    ms = time_gpu(lambda: F.fast_aten_native_layer_norm(x, (768,), w, b, 1e-5), iters)
+    nbytes = 16384 * 768 * 4 * 2 + 16384 * 8
+    out.append({"kernel": "layer_norm_fwd f32 [16384,768]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    h = torch.randn(16384, 3072, generator=g).bfloat16().to("mojo")
+    ms = time_gpu(lambda: F.fast_aten_gelu(h), iters)
+    nbytes = 16384 * 3072 * 2 * 2
+    out.append({"kernel": "gelu_fwd bf16 [16384,3072]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    lg = torch.randn(16384, 50257, generator=g).bfloat16().to("mojo")
+    ms = time_gpu(lambda: F.fast_aten__log_softmax(lg, 1, False), max(3, iters // 4))
+    nbytes = 16384 * 50257 * 2 * 2
+    out.append({"kernel": "log_softmax_fwd bf16 [16384,50257]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    del lg
+    n = 124_439_808
+    p_, g_, m_, v_ = (torch.randn(n, generator=g).to("mojo") for _ in range(4))
+    v_ = v_.abs()
+    step = torch.tensor(1.0).to("mojo")
+    ms = time_gpu(lambda: torch._fused_adamw_([p_], [g_], [m_], [v_], [], [step], lr=6e-4, beta1=0.9,
+                                              beta2=0.95, weight_decay=0.1, eps=1e-8, amsgrad=False,
+                                              maximize=False), iters)
+    nbytes = n * 28
+    out.append({"kernel": "fused_adamw f32 124.4M params", "ms": ms, "gbs": nbytes / ms / 1e6})
+    del Fn
+    for r in out:
+        r["frac_of_hbm"] = r["gbs"] / PEAK_HBM_GBS
+    return out
+
+
+def cpu_baseline():
+    """f32 training step on the host cores with stock PyTorch CPU (bounded
+    sample: batch 1 x 1024 tokens, 1 timed step after 1 warmup)."""
+    from torch_mojo_backend.gpt2 import (BETAS, GRAD_CLIP, LEARNING_RATE, WEIGHT_DECAY, GPT, GPTConfig,
+                                         make_batches, training_step)
+
+    torch.manual_seed(1337)
+    model = GPT(GPTConfig())
+    opt = model.configure_optimizers(WEIGHT_DECAY, LEARNING_RATE, BETAS, fused=True)
+    (x, y), = make_batches(1, 1024, 50257, 1, 5, "cpu")
+    training_step(model, opt, x, y, grad_clip=GRAD_CLIP)
+    t0 = time.perf_counter()
+    training_step(model, opt, x, y, grad_clip=GRAD_CLIP)
+    dt = time.perf_counter() - t0
+    return {
+        "value": 1024 / dt,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": "one f32 GPT-2-small train step (fwd+bwd+clip+fused AdamW) on batch 1 x 1024 tokens, "
+                  "stock PyTorch CPU ATen (the reference's oracle), after one warmup step",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--block", type=int, default=1024)
+    ap.add_argument("--only", default="all", choices=["all", "model", "sdpa", "gemm", "hbm"])
+    ap.add_argument("--iters", type=int, default=20, help="launches per kernel timing")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; the data-parallel design is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    from torch_mojo_backend import register_mojo_devices
+
+    register_mojo_devices()
+    res = {}
+    if args.only in ("all", "sdpa"):
+        res["sdpa"] = bench_sdpa(args.iters)
+    if args.only in ("all", "gemm"):
+        res["gemm"] = bench_gemm(max(3, args.iters // 2))
+    if args.only in ("all", "hbm"):
+        res["hbm"] = bench_hbm(args.iters)
+    if args.only in ("all", "model"):
+        res["model"] = bench_model(args)
+    traffic = None
+    tfile = ROOT / "profiles" / "attention_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_fwd_bwd")
+    line = {
+        "metric": METRIC,
+        "value": res["model"]["tokens_per_s"] if "model" in res else None,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["model"]["ms_per_step"] if "model" in res else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform token ids, random N(0,0.02) init)",
+        "config": {"workload": "nanoGPT-124M (GPT-2 small, vocab 50257, bias, tied lm_head) eager train "
+                               "step: bf16 autocast fwd+bwd, clip_grad_norm 1.0, fused AdamW",
+                   "global_batch": args.batch, "seq_len": args.block, "parallelism": "single GPU"},
+    }
+    if "sdpa" in res:
+        s = res["sdpa"]
+        line["roofline"] = {
+            "kernel": "causal flash attention fwd+bwd (attn_fwd + bwd_delta + bwd_dkv + bwd_dq), cfg 1",
+            "bound": "mfma",
+            "achieved": s["fwd_bwd_tflops"],
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": s["frac_of_peak"],
+            "traffic": traffic,
+        }
+    if not args.no_cpu and args.only in ("all", "model"):
+        line["cpu_baseline"] = cpu_baseline()
+    line.update({k: v for k, v in res.items() if k != "model"})
+    if "model" in res:
+        line["model"] = {k: v for k, v in res["model"].items()}
+        line["model"]["mfu"] = (res["model"]["tokens_per_s"] * 13.2e12 / (args.batch * args.block)) / 2.5e15
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

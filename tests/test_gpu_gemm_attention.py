@@ -23,9 +23,11 @@ def randn(*shape):
 
 
 def _gemm(c, a, b, m, n, k, a_rs, a_cs, b_rs, b_cs, dt, bias=None, beta=0, batch=1, a_bs=0, b_bs=0, c_bs=0):
+    ws_n = lib().mi355x_gemm_workspace_bytes(batch, m, n, k, CODE[dt])
+    ws = workspace(ws_n) if ws_n else None
     call("mi355x_gemm", p(c), CODE[c.dtype], n if c.dim() == 2 else c.stride(-2), c_bs,
          p(a), a_rs, a_cs, a_bs, p(b), b_rs, b_cs, b_bs, CODE[dt], p(bias),
-         CODE[bias.dtype] if bias is not None else 0, beta, batch, m, n, k, None, 0, None)
+         CODE[bias.dtype] if bias is not None else 0, beta, batch, m, n, k, p(ws), ws_n, None)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -67,10 +69,26 @@ def test_gemm_accumulate_and_batched(kernels):
     B = randn(bsz, k, n).bfloat16()
     C0 = randn(bsz, m, n)
     ta, tb, tc = dev(A), dev(B), dev(C0)
+    ws_n = lib().mi355x_gemm_workspace_bytes(bsz, m, n, k, 1)
+    ws = workspace(ws_n) if ws_n else None
     call("mi355x_gemm", p(tc), 0, n, m * n, p(ta), k, 1, m * k, p(tb), n, 1, k * n, 1, None, 0, 1,
-         bsz, m, n, k, None, 0, None)
+         bsz, m, n, k, p(ws), ws_n, None)
     exp = C0.double().numpy() + np.einsum("bmk,bkn->bmn", A.double().numpy(), B.double().numpy())
     tol_close(np64(tc), exp, atol=2e-2, rtol=1e-2, what="batched beta=1")
+
+
+def test_gemm_split_k_with_bias_and_beta(kernels):
+    """Small C, long K (the weight-gradient regime) takes the split-K path."""
+    m, n, k = 96, 80, 8192
+    assert lib().mi355x_gemm_workspace_bytes(1, m, n, k, 1) > 0
+    A = randn(k, m).bfloat16()  # stored m-contiguous: A(m, k) = A_store[k, m]
+    B = randn(k, n).bfloat16()
+    bias = randn(n)
+    C0 = randn(m, n)
+    tc = dev(C0)
+    _gemm(tc, dev(A), dev(B), m, n, k, 1, m, n, 1, torch.bfloat16, bias=dev(bias), beta=1)
+    exp = C0.double().numpy() + A.double().numpy().T @ B.double().numpy() + bias.double().numpy()
+    tol_close(np64(tc), exp, atol=0.5, rtol=1e-2, what="split-K")
 
 
 @pytest.mark.parametrize("K,N", [(768, 2304), (3072, 768)])

@@ -398,6 +398,20 @@ __global__ void __launch_bounds__(kThreads) cast_bf16_f32(float* __restrict__ ou
     ((float4*)out)[2 * i + 1] = b;
   }
 }
+// Same-dtype copy of `rows` rows of `row_bytes` (16-byte multiples) between
+// row strides (slices, concatenation): one 64-lane wave per row.
+__global__ void __launch_bounds__(kThreads) copy_rows_b128(uint8_t* __restrict__ dst, int64_t dst_rs,
+                                                           const uint8_t* __restrict__ src, int64_t src_rs,
+                                                           int64_t rows, int64_t row_bytes) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nv = row_bytes / 16;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * 4) {
+    const uint4* s = (const uint4*)(src + r * src_rs);
+    uint4* d = (uint4*)(dst + r * dst_rs);
+    for (int64_t k = lane; k < nv; k += 64) d[k] = s[k];
+  }
+}
+
 // Dense same-dtype copy, 16 bytes per thread-iteration.
 __global__ void __launch_bounds__(kThreads) copy_b128(uint4* __restrict__ out,
                                                       const uint4* __restrict__ in, int64_t n16) {
@@ -494,6 +508,17 @@ extern "C" int mi355x_copy(void* dst, int dst_dtype, const int64_t* dst_strides,
         cast_bf16_f32<<<grid_for(n / 8, 2), kThreads, 0, s>>>((float*)dst, (const bf16*)src, n / 8);
         return check_launch("mi355x_copy");
       }
+    }
+  }
+  if (g.ndim == 2 && dst_dtype == src_dtype && g.st[0][1] == 1 && g.st[1][1] == 1) {
+    const int64_t es = (int64_t)dtype_size(dst_dtype);
+    const int64_t rb = g.shape[1] * es, drs = g.st[0][0] * es, srs = g.st[1][0] * es;
+    if (rb % 16 == 0 && drs % 16 == 0 && srs % 16 == 0 && aligned(dst, 16) && aligned(src, 16)) {
+      int64_t blocks = (g.shape[0] + 3) / 4;
+      if (blocks > 65536) blocks = 65536;
+      copy_rows_b128<<<(unsigned)blocks, kThreads, 0, s>>>((uint8_t*)dst, drs, (const uint8_t*)src, srs,
+                                                            g.shape[0], rb);
+      return check_launch("mi355x_copy");
     }
   }
   MapArgs a{};

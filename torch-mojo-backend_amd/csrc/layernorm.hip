@@ -21,7 +21,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kMaxBwdBlocks = 512;
+constexpr int kMaxBwdBlocks = 256;
 
 template <typename T, int NV>
 __global__ void __launch_bounds__(kThreads)
@@ -236,17 +236,28 @@ __global__ void __launch_bounds__(kThreads)
   part_b[(int64_t)blockIdx.y * cols + c] = b;
 }
 
+// dgamma/dbeta = sum of the block partials: 64 columns x 4 partial lanes
+// per block, combined through LDS in a fixed order.
 template <typename T>
 __global__ void __launch_bounds__(kThreads)
     ln_bwd_params_final(T* __restrict__ dgamma, T* __restrict__ dbeta,
                         const float* __restrict__ part_g, const float* __restrict__ part_b,
                         int nparts, int64_t cols) {
-  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (c >= cols) return;
+  __shared__ float lg[4][64], lb[4][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + tx;
   float g = 0.f, b = 0.f;
-  for (int p = 0; p < nparts; ++p) g += part_g[(int64_t)p * cols + c], b += part_b[(int64_t)p * cols + c];
-  if (dgamma) dgamma[c] = from_f32<T>(g);
-  if (dbeta) dbeta[c] = from_f32<T>(b);
+  if (c < cols)
+    for (int p = ty; p < nparts; p += 4) g += part_g[(int64_t)p * cols + c], b += part_b[(int64_t)p * cols + c];
+  lg[ty][tx] = g;
+  lb[ty][tx] = b;
+  __syncthreads();
+  if (ty == 0 && c < cols) {
+    g = (lg[0][tx] + lg[1][tx]) + (lg[2][tx] + lg[3][tx]);
+    b = (lb[0][tx] + lb[1][tx]) + (lb[2][tx] + lb[3][tx]);
+    if (dgamma) dgamma[c] = from_f32<T>(g);
+    if (dbeta) dbeta[c] = from_f32<T>(b);
+  }
 }
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -319,7 +330,7 @@ int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* m
     }
   }
   if (params)
-    ln_bwd_params_final<T><<<ceil_div(cols, kThreads), kThreads, 0, s>>>(dgamma, dbeta, pg, pb, nb, cols);
+    ln_bwd_params_final<T><<<ceil_div(cols, 64), kThreads, 0, s>>>(dgamma, dbeta, pg, pb, nb, cols);
   return check_launch("mi355x_layer_norm_bwd");
 }
 
