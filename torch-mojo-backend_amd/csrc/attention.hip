@@ -238,6 +238,215 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// forward, head_dim 64/128: direct-to-LDS K/V staging + transposing reads.
+//
+// K and V tiles (64 keys) are copied global -> LDS with global_load_lds
+// (1 KB per wave instruction), double-buffered so the next key block streams
+// in during the current block's math, and stored row-major with the 16-byte
+// chunks of each row XOR-swizzled (conflict-free 16-row fragment reads).
+// The V^T operand of O^T += V^T P^T is read straight from the row-major V
+// tile with ds_read_b64_tr_b16: within a 16-lane group, lane i receives
+// element i%4 of the 4-element pieces supplied by lanes i/4, 4+i/4, 8+i/4 and
+// 12+i/4, so two such reads give each lane the 8 (permuted) keys of its
+// head-dim row.
+// ---------------------------------------------------------------------------
+typedef const void __attribute__((address_space(1)))* gptr_t;
+typedef void __attribute__((address_space(3)))* lptr_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <int D>
+struct KvLayout {
+  static constexpr int ROWB = D * 2;          // bytes per row
+  static constexpr int CH = D / 8;            // 16-byte chunks per row
+  static constexpr int TILE = 64 * ROWB;      // one 64-row tile
+  static constexpr int RPI = 1024 / ROWB;     // rows per 1 KB load instruction
+  static __device__ __forceinline__ int swz(int row) {
+    return D == 64 ? ((row >> 1) & 7) : (row & 15);
+  }
+  // byte offset of element (row, col) in a swizzled tile
+  static __device__ __forceinline__ int off(int row, int col) {
+    return row * ROWB + (((col >> 3) ^ swz(row)) << 4) + ((col & 7) << 1);
+  }
+};
+
+// Issue the direct loads of a 64-row tile (rows row0.., clamped to nrows-1).
+template <int D>
+__device__ __forceinline__ void kv_tile_issue(const char* g, int64_t rs_bytes, int64_t row0,
+                                              int64_t nrows, char* dst) {
+  typedef KvLayout<D> L;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int INSTR = L::TILE / 1024;
+#pragma unroll
+  for (int it = 0; it < INSTR / 4; ++it) {
+    const int blk = it * 4 + wave;
+    const int r = blk * L::RPI + lane / L::CH;
+    const int chunk = (lane % L::CH) ^ L::swz(r);
+    int64_t gr = row0 + r;
+    if (gr >= nrows) gr = nrows - 1;
+    __builtin_amdgcn_global_load_lds((gptr_t)(g + gr * rs_bytes + chunk * 16),
+                                     (lptr_t)(dst + blk * 1024), 16, 0, 0);
+  }
+}
+
+// Fragment of 8 permuted keys for head-dim row `d`: slots 0-3 = keys
+// t0*16+4g+0..3, slots 4-7 = keys t1*16+4g+0..3 (g = lane/16).
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::frag tr_frag(const char* tile, int dt, int t0, int t1) {
+  typedef KvLayout<D> L;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, src = lane & 15;
+  const int col = dt * 16 + 4 * (src & 3);
+  const int r0 = t0 * 16 + 4 * g + (src >> 2), r1 = t1 * 16 + 4 * g + (src >> 2);
+  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + L::off(r0, col)));
+  s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + L::off(r1, col)));
+  typename Mfma<T>::frag f;
+  short* fs = (short*)&f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) fs[e] = a[e], fs[4 + e] = b[e];
+  return f;
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_fwd_v2(AttnArgs p) {
+  typedef typename Mfma<T>::frag frag;
+  typedef KvLayout<D> L;
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int STAGE = 2 * L::TILE;  // K tile + V tile
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const int64_t q0 = qblock * 128;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const T* Q = (const T*)p.q + b * p.q_b + h * p.q_h;
+  const char* K = (const char*)((const T*)p.k + b * p.k_b + h * p.k_h);
+  const char* V = (const char*)((const T*)p.v + b * p.v_b + h * p.v_h);
+  const int64_t ks_b = p.k_s * (int64_t)sizeof(T), vs_b = p.v_s * (int64_t)sizeof(T);
+
+  frag qf[2][KS];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[qt][ks] = qi < p.Sq ? *(const frag*)(Q + qi * p.q_s + ks * 32 + lg * 8) : zero_frag<T>();
+  }
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  f32x4 oacc[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) oacc[dt][0] = oacc[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int64_t kv_end = p.Skv;
+  if (p.causal) kv_end = min(p.Skv, q0 + 128);
+  kv_tile_issue<D>(K, ks_b, 0, p.Skv, lds);
+  kv_tile_issue<D>(V, vs_b, 0, p.Skv, lds + L::TILE);
+  const int sw = L::swz(lr);  // fragment rows kt*16 + lr share the swizzle of lr
+  int buf = 0;
+  for (int64_t kb0 = 0; kb0 < kv_end; kb0 += 64) {
+    __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
+    __syncthreads();
+    if (kb0 + 64 < kv_end) {
+      char* nx = lds + (buf ^ 1) * STAGE;
+      kv_tile_issue<D>(K, ks_b, kb0 + 64, p.Skv, nx);
+      kv_tile_issue<D>(V, vs_b, kb0 + 64, p.Skv, nx + L::TILE);
+    }
+    const char* Kt = lds + buf * STAGE;
+    const char* Vt = Kt + L::TILE;
+
+    f32x4 s[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      frag kf[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        kf[ks] = *(const frag*)(Kt + (kt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4));
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a = Mfma<T>::mma(kf[ks], qf[qt][ks], a);
+        s[kt][qt] = a;
+      }
+    }
+    const bool need_mask = (kb0 + 64 > p.Skv) || (p.causal && kb0 + 64 > q0 + wave * 32);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = s[kt][qt][e] * p.scale_log2;
+          if (need_mask) {
+            const int64_t kj = kb0 + kt * 16 + lg * 4 + e;
+            if (kj >= p.Skv || (p.causal && kj > qi)) v = -INFINITY;
+          }
+          s[kt][qt][e] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m[qt], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m[qt] - m_use);
+      float rs = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pv = exp2f(s[kt][qt][e] - m_use);
+          s[kt][qt][e] = pv;
+          rs += pv;
+        }
+      rs += __shfl_xor(rs, 16, 64);
+      rs += __shfl_xor(rs, 32, 64);
+      l[qt] = l[qt] * alpha + rs;
+      m[qt] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
+    }
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      frag pf[2];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pf[qt][e] = (T)s[2 * ks2][qt][e];
+          pf[qt][4 + e] = (T)s[2 * ks2 + 1][qt][e];
+        }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const frag vf = tr_frag<T, D>(Vt, dt, 2 * ks2, 2 * ks2 + 1);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = Mfma<T>::mma(vf, pf[qt], oacc[dt][qt]);
+      }
+    }
+    buf ^= 1;
+  }
+
+  T* O = (T*)p.o + b * p.o_b + h * p.o_h;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+    if (qi >= p.Sq) continue;
+    const float inv = l[qt] > 0.f ? 1.f / l[qt] : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      V4<T> o4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4.v[e] = (T)(oacc[dt][qt][e] * inv);
+      *(V4<T>*)(O + qi * p.o_s + dt * 16 + lg * 4) = o4;
+    }
+    if (lg == 0)
+      p.lse[(b * p.H + h) * p.Sq + qi] = l[qt] > 0.f ? (m[qt] + log2f(l[qt])) * kLn2 : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // backward
 // ---------------------------------------------------------------------------
 struct AttnBwdArgs {
@@ -455,6 +664,278 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dq(AttnBwdArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// backward, head_dim 64/128: direct-to-LDS staging + transposing reads.
+//
+// dK/dV: a block owns 128 keys (32 per wave, held as MFMA B operands in
+// registers).  Per 64-query block it stages Q, dO, LSE and D (the row terms)
+// into LDS with direct loads, double-buffered, then per pair of 16-query
+// tiles computes S and dP (query tile = MFMA rows, keys = columns), P and dS
+// in registers, and accumulates dV^T += dO^T P and dK^T += Q^T dS with the
+// dO^T / Q^T operands read transposed from the row-major tiles.
+// dQ: a block owns 128 queries (32 per wave); per 64-key block it stages K
+// and V, computes S^T and dP^T (key tile = MFMA rows, queries = columns) and
+// accumulates dQ^T += K^T dS^T with K^T read transposed.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(AttnBwdArgs p) {
+  typedef typename Mfma<T>::frag frag;
+  typedef KvLayout<D> L;
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int STAGE = 2 * L::TILE + 512;  // Q tile, dO tile, LSE[64], D[64]
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+
+  const AttnArgs& f = p.f;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int64_t k0 = (int64_t)blockIdx.x * 128;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const char* Q = (const char*)((const T*)f.q + b * f.q_b + h * f.q_h);
+  const T* K = (const T*)f.k + b * f.k_b + h * f.k_h;
+  const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
+  const char* dO = (const char*)((const T*)p.dout + b * p.do_b + h * p.do_h);
+  const float* LSE = f.lse + (b * f.H + h) * f.Sq;
+  const float* DEL = p.delta + (b * f.H + h) * f.Sq;
+  const int64_t qs_b = f.q_s * (int64_t)sizeof(T), dos_b = p.do_s * (int64_t)sizeof(T);
+
+  const int64_t kw = k0 + wave * 32;
+  frag kf[2][KS], vf[2][KS];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t kj = kw + t * 16 + lr;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kf[t][ks] = kj < f.Skv ? *(const frag*)(K + kj * f.k_s + ks * 32 + lg * 8) : zero_frag<T>();
+      vf[t][ks] = kj < f.Skv ? *(const frag*)(V + kj * f.v_s + ks * 32 + lg * 8) : zero_frag<T>();
+    }
+  }
+  f32x4 dva[DT][2], dka[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    dva[dt][0] = dva[dt][1] = dka[dt][0] = dka[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](int64_t qb0, char* st) {
+    kv_tile_issue<D>(Q, qs_b, qb0, f.Sq, st);
+    kv_tile_issue<D>(dO, dos_b, qb0, f.Sq, st + L::TILE);
+    if (wave < 2) {
+      int64_t qi = qb0 + lane;
+      if (qi >= f.Sq) qi = f.Sq - 1;
+      const float* src = (wave == 0 ? LSE : DEL) + qi;
+      __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(st + 2 * L::TILE + wave * 256), 4, 0, 0);
+    }
+  };
+
+  const int64_t qstart = f.causal ? (k0 / 64) * 64 : 0;
+  const int sw = L::swz(lr);
+  int buf = 0;
+  if (qstart < f.Sq) issue(qstart, lds);
+  for (int64_t qb0 = qstart; qb0 < f.Sq; qb0 += 64) {
+    __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
+    __syncthreads();
+    if (qb0 + 64 < f.Sq) issue(qb0 + 64, lds + (buf ^ 1) * STAGE);
+    const char* Qt = lds + buf * STAGE;
+    const char* dOt = Qt + L::TILE;
+    const float* lse_s = (const float*)(Qt + 2 * L::TILE);
+    const float* del_s = lse_s + 64;
+    buf ^= 1;
+    if (f.causal && kw > qb0 + 63) continue;  // every key of this wave is after every query
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      f32x4 pt[2][2], ds[2][2];  // [query tile in pair][key tile]
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int qt = 2 * qs + u;
+        frag qa[KS], da[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int off = (qt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4);
+          qa[ks] = *(const frag*)(Qt + off);
+          da[ks] = *(const frag*)(dOt + off);
+        }
+        const float4 l4 = *(const float4*)(lse_s + qt * 16 + 4 * lg);
+        const float4 d4 = *(const float4*)(del_s + qt * 16 + 4 * lg);
+        const float lv[4] = {l4.x * kLog2e, l4.y * kLog2e, l4.z * kLog2e, l4.w * kLog2e};
+        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            sa = Mfma<T>::mma(qa[ks], kf[t][ks], sa);
+            pa = Mfma<T>::mma(da[ks], vf[t][ks], pa);
+          }
+          const int64_t kj = kw + t * 16 + lr;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t qi = qb0 + qt * 16 + 4 * lg + e;
+            float pv = exp2f(sa[e] * f.scale_log2 - lv[e]);
+            if (qi >= f.Sq || kj >= f.Skv || (f.causal && kj > qi)) pv = 0.f;
+            pt[u][t][e] = pv;
+            ds[u][t][e] = pv * (pa[e] - dv[e]);
+          }
+        }
+      }
+      frag pb[2], sb[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pb[t][e] = (T)pt[0][t][e];
+          pb[t][4 + e] = (T)pt[1][t][e];
+          sb[t][e] = (T)ds[0][t][e];
+          sb[t][4 + e] = (T)ds[1][t][e];
+        }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const frag dof = tr_frag<T, D>(dOt, dt, 2 * qs, 2 * qs + 1);
+        const frag qtf = tr_frag<T, D>(Qt, dt, 2 * qs, 2 * qs + 1);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          dva[dt][t] = Mfma<T>::mma(dof, pb[t], dva[dt][t]);
+          dka[dt][t] = Mfma<T>::mma(qtf, sb[t], dka[dt][t]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t kj = kw + t * 16 + lr;
+    if (kj >= f.Skv) continue;
+    T* dK = (T*)p.dk + b * p.dk_b + h * p.dk_h + kj * p.dk_s;
+    T* dV = (T*)p.dv + b * p.dv_b + h * p.dv_h + kj * p.dv_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      V4<T> k4, v4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        k4.v[e] = (T)(dka[dt][t][e] * f.scale);
+        v4.v[e] = (T)dva[dt][t][e];
+      }
+      *(V4<T>*)(dK + dt * 16 + lg * 4) = k4;
+      *(V4<T>*)(dV + dt * 16 + lg * 4) = v4;
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(AttnBwdArgs p) {
+  typedef typename Mfma<T>::frag frag;
+  typedef KvLayout<D> L;
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int STAGE = 2 * L::TILE;  // K tile, V tile
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+
+  const AttnArgs& f = p.f;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const int64_t q0 = qblock * 128;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const T* Q = (const T*)f.q + b * f.q_b + h * f.q_h;
+  const char* K = (const char*)((const T*)f.k + b * f.k_b + h * f.k_h);
+  const char* V = (const char*)((const T*)f.v + b * f.v_b + h * f.v_h);
+  const T* dO = (const T*)p.dout + b * p.do_b + h * p.do_h;
+  const int64_t ks_b = f.k_s * (int64_t)sizeof(T), vs_b = f.v_s * (int64_t)sizeof(T);
+
+  const int64_t qw = q0 + wave * 32;
+  frag qf[2][KS], df[2][KS];
+  float lse2[2], dlt[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t qi = qw + u * 16 + lr;
+    const bool ok = qi < f.Sq;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[u][ks] = ok ? *(const frag*)(Q + qi * f.q_s + ks * 32 + lg * 8) : zero_frag<T>();
+      df[u][ks] = ok ? *(const frag*)(dO + qi * p.do_s + ks * 32 + lg * 8) : zero_frag<T>();
+    }
+    lse2[u] = ok ? f.lse[(b * f.H + h) * f.Sq + qi] * kLog2e : 0.f;
+    dlt[u] = ok ? p.delta[(b * f.H + h) * f.Sq + qi] : 0.f;
+  }
+  f32x4 dqa[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dqa[dt][0] = dqa[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int64_t kv_end = f.Skv;
+  if (f.causal) kv_end = min(f.Skv, q0 + 128);
+  const int sw = L::swz(lr);
+  int buf = 0;
+  kv_tile_issue<D>(K, ks_b, 0, f.Skv, lds);
+  kv_tile_issue<D>(V, vs_b, 0, f.Skv, lds + L::TILE);
+  for (int64_t kb0 = 0; kb0 < kv_end; kb0 += 64) {
+    __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
+    __syncthreads();
+    if (kb0 + 64 < kv_end) {
+      char* nx = lds + (buf ^ 1) * STAGE;
+      kv_tile_issue<D>(K, ks_b, kb0 + 64, f.Skv, nx);
+      kv_tile_issue<D>(V, vs_b, kb0 + 64, f.Skv, nx + L::TILE);
+    }
+    const char* Kt = lds + buf * STAGE;
+    const char* Vt = Kt + L::TILE;
+    buf ^= 1;
+    if (f.causal && kb0 > qw + 31) continue;  // every key after every query of this wave
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      f32x4 ds[2][2];  // [key tile in pair][query tile]
+#pragma unroll
+      for (int v2 = 0; v2 < 2; ++v2) {
+        const int kt = 2 * ks2 + v2;
+        frag ka[KS], va[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int off = (kt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4);
+          ka[ks] = *(const frag*)(Kt + off);
+          va[ks] = *(const frag*)(Vt + off);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            sa = Mfma<T>::mma(ka[ks], qf[u][ks], sa);
+            pa = Mfma<T>::mma(va[ks], df[u][ks], pa);
+          }
+          const int64_t qi = qw + u * 16 + lr;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t kj = kb0 + kt * 16 + 4 * lg + e;
+            float pv = exp2f(sa[e] * f.scale_log2 - lse2[u]);
+            if (qi >= f.Sq || kj >= f.Skv || (f.causal && kj > qi)) pv = 0.f;
+            ds[v2][u][e] = pv * (pa[e] - dlt[u]);
+          }
+        }
+      }
+      frag sb[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sb[u][e] = (T)ds[0][u][e];
+          sb[u][4 + e] = (T)ds[1][u][e];
+        }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const frag ktf = tr_frag<T, D>(Kt, dt, 2 * ks2, 2 * ks2 + 1);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) dqa[dt][u] = Mfma<T>::mma(ktf, sb[u], dqa[dt][u]);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t qi = qw + u * 16 + lr;
+    if (qi >= f.Sq) continue;
+    T* dQ = (T*)p.dq + b * p.dq_b + h * p.dq_h + qi * p.dq_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      V4<T> q4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q4.v[e] = (T)(dqa[dt][u][e] * f.scale);
+      *(V4<T>*)(dQ + dt * 16 + lg * 4) = q4;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------
 bool strides_ok(const void* ptr, const int64_t* bhs) {
@@ -474,7 +955,8 @@ int check_common(int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D, int d
 template <typename T, int D>
 int fwd_launch(const AttnArgs& a, hipStream_t s) {
   dim3 grid(ceil_div(a.Sq, 128), (unsigned)a.H, (unsigned)a.B);
-  attn_fwd_kernel<T, D><<<grid, kThreads, 0, s>>>(a);
+  if constexpr (D == 64 || D == 128) attn_fwd_v2<T, D><<<grid, kThreads, 0, s>>>(a);
+  else attn_fwd_kernel<T, D><<<grid, kThreads, 0, s>>>(a);
   return check_launch("mi355x_attn_fwd");
 }
 
@@ -482,10 +964,17 @@ template <typename T, int D>
 int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
   const int64_t rows = a.f.B * a.f.H * a.f.Sq;
   attn_bwd_delta<T, D><<<ceil_div(rows, 4), kThreads, 0, s>>>(a);
-  dim3 gk(ceil_div(a.f.Skv, 64), (unsigned)a.f.H, (unsigned)a.f.B);
-  attn_bwd_dkv<T, D><<<gk, kThreads, 0, s>>>(a);
-  dim3 gq(ceil_div(a.f.Sq, 64), (unsigned)a.f.H, (unsigned)a.f.B);
-  attn_bwd_dq<T, D><<<gq, kThreads, 0, s>>>(a);
+  if constexpr (D == 64 || D == 128) {
+    dim3 gk(ceil_div(a.f.Skv, 128), (unsigned)a.f.H, (unsigned)a.f.B);
+    attn_bwd_dkv_v2<T, D><<<gk, kThreads, 0, s>>>(a);
+    dim3 gq(ceil_div(a.f.Sq, 128), (unsigned)a.f.H, (unsigned)a.f.B);
+    attn_bwd_dq_v2<T, D><<<gq, kThreads, 0, s>>>(a);
+  } else {
+    dim3 gk(ceil_div(a.f.Skv, 64), (unsigned)a.f.H, (unsigned)a.f.B);
+    attn_bwd_dkv<T, D><<<gk, kThreads, 0, s>>>(a);
+    dim3 gq(ceil_div(a.f.Sq, 64), (unsigned)a.f.H, (unsigned)a.f.B);
+    attn_bwd_dq<T, D><<<gq, kThreads, 0, s>>>(a);
+  }
   return check_launch("mi355x_attn_bwd");
 }
 

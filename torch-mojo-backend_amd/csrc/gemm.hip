@@ -29,6 +29,9 @@
 // workspace, summed (with bias/beta and the output cast) by a second pass.
 //
 // f32 inputs use a plain 64x64 register-tiled FMA kernel.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "common.h"
 #include "mfma.h"
 
@@ -583,6 +586,14 @@ Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool fast) {
     const int64_t rounds = (tiles + slots - 1) / slots;
     const double cost = (double)rounds * c.bm * c.bn / (c.per_cu * c.eff);
     if (cost < best_cost - 1e-9) best_cost = cost, best = Plan{c.bm, c.bn, 1, k};
+  }
+  // Tuning override, e.g. MI355X_GEMM_TILE=256x128 (fast path only).
+  static const char* forced = getenv("MI355X_GEMM_TILE");
+  if (fast && forced) {
+    int fm = 0, fn = 0;
+    if (sscanf(forced, "%dx%d", &fm, &fn) == 2 && (fm == 128 || fm == 256) && (fn == 128 || fn == 256) &&
+        !(fm == 256 && fn == 256))
+      best = Plan{fm, fn, 1, k};
   }
   const int64_t tiles = ((m + best.bm - 1) / best.bm) * ((n + best.bn - 1) / best.bn) * batch;
   if (tiles < kCUs && k >= 2048) {
