@@ -340,8 +340,13 @@ int mi355x_foreach_apply(int op, void* const* a, const void* const* b,
  * ab_dtype: F32, BF16 or F16 (A and B share it); c_dtype and bias_dtype:
  * F32/BF16/F16.  Accumulates in f32; bf16/f16 use MFMA.  beta == 1 adds the
  * existing C (accumulate), beta == 0 overwrites. */
-int64_t mi355x_gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n,
-                                    int64_t k, int ab_dtype);
+/* Workspace for the call with these operands (split-K partials, and packed
+ * copies of operands that cannot be read in place). */
+int64_t mi355x_gemm_workspace_bytes(const void* a, int64_t a_rs, int64_t a_cs,
+                                    int64_t a_bs, const void* b, int64_t b_rs,
+                                    int64_t b_cs, int64_t b_bs, int ab_dtype,
+                                    int64_t batch, int64_t m, int64_t n,
+                                    int64_t k);
 int mi355x_gemm(void* c, int c_dtype, int64_t c_rs, int64_t c_bs,
                 const void* a, int64_t a_rs, int64_t a_cs, int64_t a_bs,
                 const void* b, int64_t b_rs, int64_t b_cs, int64_t b_bs,

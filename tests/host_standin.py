@@ -410,7 +410,7 @@ class HostStandIn:
         return 0
 
     # ---- gemm / attention ----
-    def mi355x_gemm_workspace_bytes(self, batch, m, n, k, dt):
+    def mi355x_gemm_workspace_bytes(self, a, ars, acs, abs_, b, brs, bcs, bbs, dt, batch, m, n, k):
         return 0
 
     def mi355x_gemm(self, c, cdt, crs, cbs, a, ars, acs, abs_, b, brs, bcs, bbs, abdt, bias, bdt,

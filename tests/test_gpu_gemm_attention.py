@@ -23,7 +23,8 @@ def randn(*shape):
 
 
 def _gemm(c, a, b, m, n, k, a_rs, a_cs, b_rs, b_cs, dt, bias=None, beta=0, batch=1, a_bs=0, b_bs=0, c_bs=0):
-    ws_n = lib().mi355x_gemm_workspace_bytes(batch, m, n, k, CODE[dt])
+    ws_n = lib().mi355x_gemm_workspace_bytes(p(a), a_rs, a_cs, a_bs, p(b), b_rs, b_cs, b_bs, CODE[dt],
+                                             batch, m, n, k)
     ws = workspace(ws_n) if ws_n else None
     call("mi355x_gemm", p(c), CODE[c.dtype], n if c.dim() == 2 else c.stride(-2), c_bs,
          p(a), a_rs, a_cs, a_bs, p(b), b_rs, b_cs, b_bs, CODE[dt], p(bias),
@@ -69,7 +70,7 @@ def test_gemm_accumulate_and_batched(kernels):
     B = randn(bsz, k, n).bfloat16()
     C0 = randn(bsz, m, n)
     ta, tb, tc = dev(A), dev(B), dev(C0)
-    ws_n = lib().mi355x_gemm_workspace_bytes(bsz, m, n, k, 1)
+    ws_n = lib().mi355x_gemm_workspace_bytes(p(ta), k, 1, m * k, p(tb), n, 1, k * n, 1, bsz, m, n, k)
     ws = workspace(ws_n) if ws_n else None
     call("mi355x_gemm", p(tc), 0, n, m * n, p(ta), k, 1, m * k, p(tb), n, 1, k * n, 1, None, 0, 1,
          bsz, m, n, k, p(ws), ws_n, None)
@@ -80,7 +81,7 @@ def test_gemm_accumulate_and_batched(kernels):
 def test_gemm_split_k_with_bias_and_beta(kernels):
     """Small C, long K (the weight-gradient regime) takes the split-K path."""
     m, n, k = 96, 80, 8192
-    assert lib().mi355x_gemm_workspace_bytes(1, m, n, k, 1) > 0
+    assert lib().mi355x_gemm_workspace_bytes(None, 1, m, 0, None, n, 1, 0, 1, 1, m, n, k) > 0
     A = randn(k, m).bfloat16()  # stored m-contiguous: A(m, k) = A_store[k, m]
     B = randn(k, n).bfloat16()
     bias = randn(n)

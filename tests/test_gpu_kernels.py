@@ -102,6 +102,20 @@ def test_reduce_sum_matches_oracle(kernels, shape, axis):
     tol_close(np64(out), expect, atol=1e-3, rtol=1e-5, what="sum")
 
 
+@pytest.mark.parametrize("rows,cols", [(16384, 2304), (7, 72), (1000, 50304)])
+def test_bias_grad_column_sum_bf16(kernels, rows, cols):
+    """sum(dY, 0) over a bf16 [rows, cols] gradient (the vectorised column-sum
+    path), accumulated in f32, rounded once to bf16."""
+    x = randn(rows, cols).bfloat16()
+    tx = dev(x)
+    out = torch.empty(cols, dtype=torch.bfloat16, device="cuda")
+    ws_n = lib().mi355x_reduce_workspace_bytes(1, rows, cols)
+    ws = workspace(ws_n)
+    call("mi355x_reduce", 0, p(out), 1, p(tx), 1, 1, rows, cols, rows * cols, cols, 1, p(ws), ws_n, None)
+    expect = x.double().numpy().sum(0)
+    tol_close(np64(out), expect, atol=2e-2 * math.sqrt(rows / 64), rtol=1e-2, what="colsum")
+
+
 def test_reduce_max_norm_mean(kernels):
     x = randn(37, 1000)
     x[3, 5] = float("nan")

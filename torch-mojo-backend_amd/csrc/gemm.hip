@@ -359,7 +359,91 @@ struct TileLoad {
   }
 };
 
-template <typename T, int BM, int BN>
+// m/n-contiguous operand tile: 64 k-rows of ROWS elements, 16-byte chunks
+// XOR-swizzled by s(k) = (k & 3) | ((k >> 1) & 12), a bijection on the 16
+// k-rows one transposing fragment read touches.
+__device__ __forceinline__ int kswz(int k) { return (k & 3) | ((k >> 1) & 12); }
+
+template <int ROWS, int NT>
+struct TileLoadT {
+  static constexpr int ROWB = ROWS * 2;
+  static constexpr int CPR = ROWS / 8;     // chunks per k-row
+  static constexpr int KPI = 1024 / ROWB;  // k-rows per 1 KB instruction
+  static constexpr int WAVES = NT / 64;
+  static constexpr int ITERS = 64 / KPI / WAVES;
+  const char* base;
+  int64_t ld;  // bytes between k-rows
+  int64_t row0, rows;
+  int krow_l, phys;
+
+  __device__ __forceinline__ void init(const char* b, int64_t ld_bytes, int64_t r0, int64_t nrows) {
+    const int lane = threadIdx.x & 63;
+    base = b;
+    ld = ld_bytes;
+    row0 = r0;
+    rows = nrows;
+    krow_l = lane / CPR;
+    phys = lane % CPR;
+  }
+  __device__ __forceinline__ void issue(int64_t k0, char* dst, bool full) const {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int blk = it * WAVES + wave;
+      const int kr = blk * KPI + krow_l;
+      const int chunk = phys ^ kswz(kr);
+      int64_t m = row0 + chunk * 8;
+      if (!full && m + 8 > rows) m = rows - 8;
+      const char* src = base + (k0 + kr) * ld + m * 2;
+      __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(dst + blk * 1024), 16, 0, 0);
+    }
+  }
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// MFMA fragment (rows r0..r0+15, k = ks*32 + 8g + 0..7) from an m/n-
+// contiguous tile with two transposing reads: within a 16-lane group, lane i
+// receives element i%4 of the 4-element pieces of lanes i/4, 4+i/4, 8+i/4,
+// 12+i/4, so source lane 4e+q supplies k-row (.. + e), columns r0+4q..+3.
+template <typename T, int ROWS>
+__device__ __forceinline__ typename Mfma<T>::frag mn_frag(const char* tile, int r0, int ks) {
+  constexpr int ROWB = ROWS * 2;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, src = lane & 15;
+  const int m = r0 + 4 * (src & 3);
+  const int k1 = ks * 32 + 8 * g + (src >> 2), k2 = k1 + 4;
+  const int o1 = k1 * ROWB + (((m >> 3) ^ kswz(k1)) << 4) + ((m & 7) << 1);
+  const int o2 = k2 * ROWB + (((m >> 3) ^ kswz(k2)) << 4) + ((m & 7) << 1);
+  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + o1));
+  s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + o2));
+  typename Mfma<T>::frag f;
+  short* fs = (short*)&f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) fs[e] = a[e], fs[4 + e] = b[e];
+  return f;
+}
+
+template <int ROWS, int NT, bool K_CONTIG>
+struct OperandLoad;
+template <int ROWS, int NT>
+struct OperandLoad<ROWS, NT, true> {
+  TileLoad<ROWS, NT> t;
+  int64_t rows;
+  __device__ __forceinline__ void init(const char* b, int64_t ld, int64_t r0, int64_t n) { t.init(b, ld, r0); rows = n; }
+  __device__ __forceinline__ void issue(int64_t k0_elems, char* dst, bool full) const {
+    t.issue(k0_elems * 2, dst, rows, full);
+  }
+};
+template <int ROWS, int NT>
+struct OperandLoad<ROWS, NT, false> {
+  TileLoadT<ROWS, NT> t;
+  __device__ __forceinline__ void init(const char* b, int64_t ld, int64_t r0, int64_t n) { t.init(b, ld, r0, n); }
+  __device__ __forceinline__ void issue(int64_t k0_elems, char* dst, bool full) const { t.issue(k0_elems, dst, full); }
+};
+
+template <typename T, int BM, int BN, bool A_K, bool B_K>
 __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, int tiles_n) {
   typedef typename Mfma<T>::frag frag;
   constexpr int NT = 256;
@@ -388,7 +472,9 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, 
 
   const char* A = (const char*)g.a + bidx * g.a_bs * (int64_t)sizeof(T);
   const char* B = (const char*)g.b + bidx * g.b_bs * (int64_t)sizeof(T);
-  const int64_t a_ldb = g.a_rs * (int64_t)sizeof(T), b_ldb = g.b_cs * (int64_t)sizeof(T);
+  // A_K: bytes between rows; else bytes between k-rows.  Same for B.
+  const int64_t a_ldb = (A_K ? g.a_rs : g.a_cs) * (int64_t)sizeof(T);
+  const int64_t b_ldb = (B_K ? g.b_cs : g.b_rs) * (int64_t)sizeof(T);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -400,14 +486,14 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, 
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  TileLoad<BM, NT> la;
-  TileLoad<BN, NT> lb;
-  la.init(A, a_ldb, m0);
-  lb.init(B, b_ldb, n0);
+  OperandLoad<BM, NT, A_K> la;
+  OperandLoad<BN, NT, B_K> lb;
+  la.init(A, a_ldb, m0, g.m);
+  lb.init(B, b_ldb, n0, g.n);
   const bool full_a = m0 + BM <= g.m, full_b = n0 + BN <= g.n;
-  la.issue(kbeg * (int64_t)sizeof(T), lds, g.m, full_a);
-  lb.issue(kbeg * (int64_t)sizeof(T), lds + A_BYTES, g.n, full_b);
-  // fragment reads: row wm*WM + i*16 + lr has swizzle (lr >> 1) & 7
+  la.issue(kbeg, lds, full_a);
+  lb.issue(kbeg, lds + A_BYTES, full_b);
+  // k-contiguous fragment rows wm*WM + i*16 + lr share the swizzle of lr
   const int sw = (lr >> 1) & 7;
 
   int cur = 0;
@@ -416,20 +502,25 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, 
     __syncthreads();
     if (k0 + 64 < kend) {
       char* nxt = lds + (cur ^ 1) * STAGE;
-      la.issue((k0 + 64) * (int64_t)sizeof(T), nxt, g.m, full_a);
-      lb.issue((k0 + 64) * (int64_t)sizeof(T), nxt + A_BYTES, g.n, full_b);
+      la.issue(k0 + 64, nxt, full_a);
+      lb.issue(k0 + 64, nxt + A_BYTES, full_b);
     }
-    const char* as = lds + cur * STAGE + (wm * WM + lr) * 128;
-    const char* bs = lds + cur * STAGE + A_BYTES + (wn * WN + lr) * 128;
+    const char* at = lds + cur * STAGE;
+    const char* bt = at + A_BYTES;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int coff = ((ks * 4 + lg) ^ sw) * 16;
       frag bfr[TN];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bfr[j] = *(const frag*)(bs + j * 2048 + coff);
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (B_K) bfr[j] = *(const frag*)(bt + (wn * WN + lr) * 128 + j * 2048 + coff);
+        else bfr[j] = mn_frag<T, BN>(bt, wn * WN + j * 16, ks);
+      }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const frag af = *(const frag*)(as + i * 2048 + coff);
+        frag af;
+        if constexpr (A_K) af = *(const frag*)(at + (wm * WM + lr) * 128 + i * 2048 + coff);
+        else af = mn_frag<T, BM>(at, wm * WM + i * 16, ks);
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af, bfr[j], acc[i][j]);
       }
@@ -629,7 +720,11 @@ int launch_fast_cfg(const GemmArgs& g, int64_t batch, int splits, hipStream_t s)
   const int tm = (int)ceil_div(g.m, BM), tn = (int)ceil_div(g.n, BN);
   const int64_t blocks = (int64_t)tm * tn * batch * splits;
   const size_t lds = 2 * (BM + BN) * 128;
-  gemm_nt_fast<T, BM, BN><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
+  const bool ak = g.a_cs == 1, bk = g.b_rs == 1;
+  if (ak && bk) gemm_nt_fast<T, BM, BN, true, true><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
+  else if (ak) gemm_nt_fast<T, BM, BN, true, false><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
+  else if (bk) gemm_nt_fast<T, BM, BN, false, true><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
+  else gemm_nt_fast<T, BM, BN, false, false><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
   return check_launch("mi355x_gemm");
 }
 
@@ -679,8 +774,21 @@ WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int64_t k, const void* a
   WsLayout w{};
   w.kp = (k + 63) / 64 * 64;
   const bool k64 = k % 64 == 0;
-  w.pack_a = !(k64 && a_cs == 1 && a_rs % 8 == 0 && a_bs % 8 == 0 && (a == nullptr || aligned16(a)));
-  w.pack_b = !(k64 && b_rs == 1 && b_cs % 8 == 0 && b_bs % 8 == 0 && (b == nullptr || aligned16(b)));
+  // In place when K tiles are whole and every 16-byte load is aligned:
+  // k-contiguous operands need an 8-element row stride, m/n-contiguous ones
+  // an 8-element k stride and a row count that is a multiple of 8.
+  auto in_place = [&](const void* p, int64_t rs, int64_t cs, int64_t bs, int64_t nrows) {
+    if (!k64 || bs % 8 != 0 || (p != nullptr && !aligned16(p))) return false;
+    if (cs == 1) return rs % 8 == 0;
+    return cs % 8 == 0 && nrows % 8 == 0 && nrows >= 8;
+  };
+  // An m/n-contiguous operand that is small next to the product (a weight in
+  // dX = dY W) is still packed: the copy costs under ~3% of the GEMM and the
+  // k-contiguous fragment reads are cheaper than transposing ones.
+  const double small_rows = 2e-4 * (double)m * (double)n;
+  w.pack_a = !in_place(a, a_rs, a_cs, a_bs, m) || (a_cs != 1 && (double)m < small_rows);
+  // B as [n rows][k]: row stride b_cs, k stride b_rs
+  w.pack_b = !in_place(b, b_cs, b_rs, b_bs, n) || (b_rs != 1 && (double)n < small_rows);
   w.plan = plan_gemm(batch, m, n, w.kp, true);
   auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
   w.part_bytes = w.plan.splits > 1 ? up((int64_t)w.plan.splits * batch * m * n * 4) : 0;
@@ -707,12 +815,12 @@ int pack(uint16_t* dst, const void* src, int64_t batch, int64_t rows, int64_t kd
 
 using namespace mi;
 
-extern "C" int64_t mi355x_gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k,
-                                               int ab_dtype) {
+extern "C" int64_t mi355x_gemm_workspace_bytes(const void* a, int64_t a_rs, int64_t a_cs,
+                                               int64_t a_bs, const void* b, int64_t b_rs,
+                                               int64_t b_cs, int64_t b_bs, int ab_dtype,
+                                               int64_t batch, int64_t m, int64_t n, int64_t k) {
   if (ab_dtype == MI355X_F32 || m <= 0 || n <= 0 || k <= 0) return 0;
-  // Worst case over operand layouts: both operands packed.
-  WsLayout w = ws_layout(batch, m, n, k, nullptr, 1, 3, 1, nullptr, 3, 1, 1);
-  return w.total;
+  return ws_layout(batch, m, n, k, a, a_rs, a_cs, a_bs, b, b_rs, b_cs, b_bs).total;
 }
 
 extern "C" int mi355x_gemm(void* c, int c_dtype, int64_t c_rs, int64_t c_bs, const void* a,

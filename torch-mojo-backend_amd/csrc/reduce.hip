@@ -171,6 +171,41 @@ __global__ void __launch_bounds__(kThreads) reduce_cols(RedArgs a) {
   }
 }
 
+// Sum over rows of a dense [r, inner] f32/bf16/f16 matrix (the bias gradient
+// sum(dY, 0)): a thread owns 8 consecutive columns (one 16-byte load per row
+// for 16-bit types, two for f32); 32 column groups x 8 row lanes per block,
+// row lanes combined through LDS in a fixed order.
+template <typename T>
+__global__ void __launch_bounds__(kThreads) colsum8(RedArgs a) {
+  __shared__ float red[8][32][9];
+  const int cg = threadIdx.x & 31, rl = threadIdx.x >> 5;
+  const int64_t c0 = ((int64_t)blockIdx.x * 32 + cg) * 8;
+  const int split = blockIdx.y;
+  const int64_t r0 = (int64_t)split * a.chunk;
+  const int64_t r1 = min(a.r, r0 + a.chunk);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (c0 < a.inner) {
+    const T* base = (const T*)a.in + c0;
+    for (int64_t r = r0 + rl; r < r1; r += 8) {
+      struct alignas(16) P { T v[8]; } p = *(const P*)(base + r * a.inner);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += to_f32(p.v[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[rl][cg][e] = acc[e];
+  __syncthreads();
+  if (rl == 0 && c0 < a.inner) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float t = red[0][cg][e];
+      for (int w = 1; w < 8; ++w) t += red[w][cg][e];
+      if (a.part) ((float*)a.part)[(int64_t)split * a.inner + c0 + e] = t;
+      else store_as<float>(a.out, a.out_dt, c0 + e, t);
+    }
+  }
+}
+
 template <typename A>
 __global__ void __launch_bounds__(kThreads) reduce_combine(RedArgs a, int splits) {
   const RedOp<A> R{a.op};
@@ -319,6 +354,23 @@ extern "C" int mi355x_reduce(int op, void* out, int out_dtype, const void* in, i
   }
   RedArgs a{op, in, in_dtype, out, out_dtype, workspace, outer, r, inner, s_o, s_r, s_i, chunk};
   hipStream_t s = (hipStream_t)stream;
+  // Dense column sums (bias gradients): vectorised kernel, same split plan.
+  const size_t es = dtype_size(in_dtype);
+  if (op == MI355X_RED_SUM && outer == 1 && inner > 1 && inner % 8 == 0 && s_i == 1 &&
+      s_r == inner && ((uintptr_t)in % 16) == 0 &&
+      (in_dtype == MI355X_F32 || in_dtype == MI355X_BF16 || in_dtype == MI355X_F16)) {
+    (void)es;
+    if (splits <= 1) a.part = nullptr;
+    dim3 grid(ceil_div(inner, 256), splits);
+    if (in_dtype == MI355X_F32) colsum8<float><<<grid, kThreads, 0, s>>>(a);
+    else if (in_dtype == MI355X_BF16) colsum8<bf16><<<grid, kThreads, 0, s>>>(a);
+    else colsum8<f16><<<grid, kThreads, 0, s>>>(a);
+    if (splits > 1) {
+      int64_t g = (inner + kThreads - 1) / kThreads;
+      reduce_combine<float><<<(unsigned)g, kThreads, 0, s>>>(a, splits);
+    }
+    return check_launch("mi355x_reduce");
+  }
   switch (acc_kind(op, in_dtype)) {
     case 1: return run<double>(a, splits, s);
     case 2: return run<int64_t>(a, splits, s);

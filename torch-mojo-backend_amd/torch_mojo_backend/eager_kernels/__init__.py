@@ -122,7 +122,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_int, P_vp, P_vp, P_vp, P_double, P_i64, c_int, c_int, c_double, c_vp, c_vp],
     ),
-    "mi355x_gemm_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_int]),
+    "mi355x_gemm_workspace_bytes": (
+        c_i64, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64, c_i64, c_int, c_i64, c_i64, c_i64, c_i64],
+    ),
     "mi355x_gemm": (
         c_int,
         [

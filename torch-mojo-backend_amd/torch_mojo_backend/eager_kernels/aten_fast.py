@@ -1226,7 +1226,8 @@ def _gemm(out: MT, a: MT, b: MT, bias=None, beta=0, batch=1):
     b, brs, bcs, bbs = _gemm_operand(b, rank)
     c_rs = out._strides[-2] if m > 1 else n
     c_bs = out._strides[0] if rank == 3 else 0
-    ws = lib().mi355x_gemm_workspace_bytes(batch, m, n, k, _code(a._dtype))
+    ws = lib().mi355x_gemm_workspace_bytes(a._ptr, ars, acs, abs_, b._ptr, brs, bcs, bbs,
+                                           _code(a._dtype), batch, m, n, k)
     hold, wptr = _workspace(ws, a._device)
     check(
         "mi355x_gemm",
