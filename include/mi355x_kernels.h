@@ -283,6 +283,28 @@ int mi355x_nll_bwd(void* grad_input, const void* grad_out,
                    int reduction, int64_t ignore_index, int dtype,
                    mi355x_stream_t stream);
 
+/* ---- fused cross-entropy (the log_softmax -> nll_loss chain of the step:
+ *      fast_aten__log_softmax aten_fast.py:5792-5825, nll_loss_forward/
+ *      backward aten_fast.py:5974-6130, log_softmax backward :5828-5971) -- */
+/* out: f32 scalar (reduction mean/sum) or f32 [n] (none); total_weight: f32
+ * scalar (non-ignored rows); lse: f32 [n] natural-log row log-sum-exp, kept
+ * for the backward.  logits rows at logits + i*ld. */
+int64_t mi355x_cross_entropy_workspace_bytes(int64_t n);
+int mi355x_cross_entropy_fwd(void* out, float* total_weight, float* lse,
+                             const void* logits, int dtype, int64_t ld,
+                             const int64_t* target, int64_t n, int64_t c,
+                             int reduction, int64_t ignore_index,
+                             int32_t* err_flag, void* workspace,
+                             int64_t ws_bytes, mi355x_stream_t stream);
+/* dx[i, :] = g_i * (softmax(x_i) - onehot(t_i)) with rows at dx + i*ld_dx;
+ * columns [c, ld_dx) are written as zero.  grad_out: f32 scalar or [n]. */
+int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx,
+                             const void* logits, int dtype, int64_t ld,
+                             const float* lse, const int64_t* target,
+                             const float* grad_out, int reduction,
+                             const float* total_weight, int64_t n, int64_t c,
+                             int64_t ignore_index, mi355x_stream_t stream);
+
 /* ---- optimizer (enqueue_fused_adamw_f32 optimizer_kernels.mojo:339-454,
  *      AdamWDesc optimizer_contract.mojo:11-56;
  *      foreach_l2_norm_f32_* foreach_clip_kernels.mojo:64,101;

@@ -347,6 +347,44 @@ class HostStandIn:
         dense(_val(gi), DT[dt], (n, c)).copy_(G)
         return 0
 
+    def mi355x_cross_entropy_workspace_bytes(self, n):
+        return 8 * n + 256
+
+    def mi355x_cross_entropy_fwd(self, out, tw, lse, x, dt, ld, tgt, n, c, red, ign, err, ws, wsb, stream):
+        X = view(_val(x), DT[dt], (n, c), (ld, 1)).float()
+        T = dense(_val(tgt), torch.int64, (n,))
+        L = torch.logsumexp(X, 1)
+        dense(_val(lse), torch.float32, (n,)).copy_(L)
+        valid = T != ign
+        if ((T[valid] < 0) | (T[valid] >= c)).any() and err:
+            dense(_val(err), torch.int32, (1,)).fill_(1)
+        Tc = torch.where(valid, T, torch.zeros_like(T)).clamp(0, c - 1)
+        rows = (L - X.gather(1, Tc[:, None])[:, 0]) * valid.float()
+        w = valid.float().sum()
+        if red == 0:
+            dense(_val(out), torch.float32, (n,)).copy_(rows)
+        else:
+            dense(_val(out), torch.float32, ()).copy_(rows.sum() / w if red == 1 else rows.sum())
+        dense(_val(tw), torch.float32, ()).copy_(w)
+        return 0
+
+    def mi355x_cross_entropy_bwd(self, dx, dxdt, lddx, x, dt, ld, lse, tgt, g, red, tw, n, c, ign, stream):
+        X = view(_val(x), DT[dt], (n, c), (ld, 1)).float()
+        T = dense(_val(tgt), torch.int64, (n,))
+        L = dense(_val(lse), torch.float32, (n,))
+        G = dense(_val(g), torch.float32, (n,) if red == 0 else ()).expand(n).clone()
+        if red == 1:
+            G = G / dense(_val(tw), torch.float32, ()).item()
+        valid = (T != ign) & (T >= 0) & (T < c)
+        G = G * valid.float()
+        P = torch.exp(X - L[:, None])
+        Tc = torch.where(valid, T, torch.zeros_like(T))
+        P[torch.arange(n), Tc] -= valid.float()
+        D = view(_val(dx), DT[dxdt], (n, lddx), (lddx, 1))
+        D.zero_()
+        D[:, :c].copy_(P * G[:, None])
+        return 0
+
     # ---- optimizer ----
     def mi355x_fused_adamw(self, descs, n, lr, lr_ptr, b1, b2, wd, eps, flags, gs, fi, stream):
         if fi and dense(_val(fi), torch.float32, ()).item() != 0:

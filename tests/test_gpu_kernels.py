@@ -275,6 +275,45 @@ def test_nll_fwd_bwd(kernels, reduction):
     assert host(err).item() == 1
 
 
+@pytest.mark.parametrize("reduction", [0, 1, 2])
+@pytest.mark.parametrize("dtype,n,c", [(torch.bfloat16, 257, 50257), (torch.float32, 64, 1000)])
+def test_fused_cross_entropy_matches_log_softmax_nll_chain(kernels, reduction, dtype, n, c):
+    """The fused kernels against the oracle of the chain they replace:
+    nll_loss(log_softmax(x)) forward, log_softmax_backward(nll_backward)
+    backward (reduction none/mean/sum, ignore_index rows, odd row stride)."""
+    x = (randn(n, c + 3) * 4).to(dtype)[:, :c]  # rows with a gap: stride c + 3
+    tgt = torch.randint(0, c, (n,), generator=G)
+    tgt[::5] = -100
+    tx, tt = dev(x.contiguous()), dev(tgt)
+    xs = torch.empty(n, c + 3, dtype=dtype, device="cuda")[:, :c]
+    xs.copy_(tx)
+    ld = c + 3
+    out = torch.empty(n if reduction == 0 else (), device="cuda")
+    lse = torch.empty(n, device="cuda")
+    tw = torch.empty((), device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws_n = lib().mi355x_cross_entropy_workspace_bytes(n)
+    ws = workspace(ws_n)
+    call("mi355x_cross_entropy_fwd", p(out), p(tw), p(lse), p(xs), CODE[dtype], ld, p(tt), n, c,
+         reduction, -100, p(err), p(ws), ws_n, None)
+    red = {0: "none", 1: "mean", 2: "sum"}[reduction]
+    logp = O.log_softmax(x.double().numpy())
+    eo, etw = O.nll_loss(logp, tgt.numpy(), None, red, -100)
+    tol_close(np64(out), eo, atol=1e-4, rtol=1e-5, what="ce loss")
+    assert host(tw).item() == etw and host(err).item() == 0
+    g = randn(n) if reduction == 0 else torch.tensor(1.3)
+    tg = dev(g)
+    ld_dx = (c + 7) // 8 * 8
+    dx = torch.full((n, ld_dx), 7.0, dtype=dtype, device="cuda")
+    call("mi355x_cross_entropy_bwd", p(dx), CODE[dtype], ld_dx, p(xs), CODE[dtype], ld, p(lse), p(tt),
+         p(tg), reduction, p(tw), n, c, -100, None)
+    dnll = O.nll_loss_backward(g.double().numpy(), (n, c), tgt.numpy(), None, red, -100, etw)
+    edx = O.log_softmax_backward(dnll, logp)
+    tol = 1e-6 if dtype == torch.float32 else 2e-2
+    tol_close(np64(dx)[:, :c], edx, atol=tol * 1e-2 + 1e-7, rtol=tol, what="ce dx")
+    assert (host(dx)[:, c:] == 0).all()
+
+
 # ---------------------------------------------------------------------------
 # optimizer
 # ---------------------------------------------------------------------------

@@ -106,6 +106,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_int, c_i64, c_int, c_vp],
     ),
+    "mi355x_cross_entropy_workspace_bytes": (c_i64, [c_i64]),
+    "mi355x_cross_entropy_fwd": (
+        c_int,
+        [c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_vp, c_i64, c_i64, c_int, c_i64, c_vp, c_vp, c_i64, c_vp],
+    ),
+    "mi355x_cross_entropy_bwd": (
+        c_int,
+        [c_vp, c_int, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_vp],
+    ),
     "mi355x_fused_adamw": (
         c_int,
         [

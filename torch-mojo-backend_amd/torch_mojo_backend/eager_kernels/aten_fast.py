@@ -1898,3 +1898,62 @@ def fast_aten__foreach_norm(self, ord=2, dtype=None):
         ),
     )
     return outs
+
+
+# ---------------------------------------------------------------------------
+# fused cross-entropy (the log_softmax + nll_loss chain, aten_fast.py:5792-6130)
+# ---------------------------------------------------------------------------
+_REDUCTION = {0: 0, 1: 1, 2: 2}
+
+
+def fused_cross_entropy_inputs(input, target, weight, reduction, ignore_index, label_smoothing):
+    """(logits, target) when the fused kernels serve the call, else None."""
+    x, t = _t(input), _t(target)
+    if (
+        x is None or t is None or weight is not None or float(label_smoothing) != 0.0
+        or reduction not in _REDUCTION or x._dtype not in _FLOAT_DTYPES
+        or len(x._shape) != 2 or t._dtype != torch.int64 or len(t._shape) != 1
+        or t._shape[0] != x._shape[0] or x._strides[1] != 1 or x._shape[1] == 0
+    ):
+        return None
+    return x, t
+
+
+def fused_cross_entropy_forward(x: MT, t: MT, reduction, ignore_index):
+    """(loss f32, lse f32 [n], total_weight f32 scalar)."""
+    n, c = x._shape
+    ld = x._strides[0] if n > 1 else c
+    tgt = _contig(t)
+    out = _alloc((n,) if reduction == 0 else (), torch.float32, x._device)
+    lse = _alloc((n,), torch.float32, x._device)
+    total = _alloc((), torch.float32, x._device)
+    ws = lib().mi355x_cross_entropy_workspace_bytes(n)
+    hold, wptr = _workspace(ws, x._device)
+    err, eptr = _error_flag(x._device)
+    check(
+        "mi355x_cross_entropy_fwd",
+        lib().mi355x_cross_entropy_fwd(out._ptr, total._ptr, lse._ptr, x._ptr, _code(x._dtype), ld,
+                                       tgt._ptr, n, c, int(reduction), int(ignore_index), eptr, wptr,
+                                       ws, _STREAM),
+    )
+    _raise_if_flagged(err, "Target is out of bounds")
+    return out, lse, total
+
+
+def fused_cross_entropy_backward(grad, x: MT, t: MT, lse: MT, total: MT, reduction, ignore_index):
+    """dlogits in x's dtype, stored with rows padded to a multiple of 8
+    elements (16-byte aligned rows for the lm_head GEMMs that consume it)."""
+    n, c = x._shape
+    ld = x._strides[0] if n > 1 else c
+    g = _require(grad)
+    g = _contig(g) if g._dtype == torch.float32 else materialize_contiguous(g, torch.float32)
+    ld_dx = (c + 7) // 8 * 8
+    dense = _alloc((n, ld_dx), x._dtype, x._device)
+    dx = MT._view_of(dense, (n, c), (ld_dx, 1), 0, ld_dx == c)
+    check(
+        "mi355x_cross_entropy_bwd",
+        lib().mi355x_cross_entropy_bwd(dx._ptr, _code(x._dtype), ld_dx, x._ptr, _code(x._dtype), ld,
+                                       lse._ptr, _contig(t)._ptr, g._ptr, int(reduction), total._ptr,
+                                       n, c, int(ignore_index), _STREAM),
+    )
+    return dx

@@ -56,4 +56,50 @@ def register_autograd_ops() -> None:
         return
     _library = torch.library.Library("aten", "IMPL", "AutogradPrivateUse1")
     _library.impl("scaled_dot_product_attention", _scaled_dot_product_attention_autograd)
+    _library.impl("cross_entropy_loss", _cross_entropy_loss_autograd)
     _registered = True
+
+
+class _FusedCrossEntropy(torch.autograd.Function):
+    """Softmax cross-entropy with saved row log-sum-exp: the forward reads the
+    logits once, the backward writes dlogits = (softmax - onehot) * g once,
+    instead of the log_softmax -> nll_loss chain's log-probabilities and
+    dense one-hot gradient."""
+
+    @staticmethod
+    def forward(ctx, logits, target, reduction, ignore_index, out_dtype):
+        loss, lse, total = aten_fast.fused_cross_entropy_forward(logits, target, reduction, ignore_index)
+        ctx.save_for_backward(logits, target, lse, total)
+        ctx.reduction = reduction
+        ctx.ignore_index = ignore_index
+        ctx.loss_dtype = loss.dtype
+        if out_dtype != loss.dtype:
+            loss = loss.to(out_dtype)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad):
+        logits, target, lse, total = ctx.saved_tensors
+        dx = aten_fast.fused_cross_entropy_backward(grad, logits, target, lse, total, ctx.reduction,
+                                                    ctx.ignore_index)
+        return dx, None, None, None, None
+
+
+def _cross_entropy_loss_autograd(input, target, weight=None, reduction=1, ignore_index=-100,
+                                 label_smoothing=0.0):
+    if aten_fast.fused_cross_entropy_inputs(input, target, weight, reduction, ignore_index,
+                                            label_smoothing) is not None:
+        low = input.dtype in (torch.bfloat16, torch.float16)
+        out_dtype = torch.float32 if (low and torch.is_autocast_enabled("mojo")) else input.dtype
+        return _FusedCrossEntropy.apply(input, target, reduction, ignore_index, out_dtype)
+    if float(label_smoothing) != 0.0:
+        raise NotImplementedError(
+            "cross_entropy with label_smoothing is not supported by the mojo eager device"
+        )
+    # other regimes (class weights, N-d inputs): the log_softmax -> nll_loss
+    # decomposition on the device
+    logp = torch.log_softmax(input, dim=1 if input.dim() > 1 else 0)
+    return torch.nn.functional.nll_loss(
+        logp, target, weight, reduction={0: "none", 1: "mean", 2: "sum"}[reduction],
+        ignore_index=ignore_index,
+    )
