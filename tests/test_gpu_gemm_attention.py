@@ -64,6 +64,37 @@ def test_gemm_layouts_and_shapes(kernels, dtype, layout, mnk):
     tol_close(np64(c), exp, atol=tol, rtol=2e-2 if dtype != torch.float32 else 1e-4, what=f"{layout}{mnk}")
 
 
+@pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
+def test_gemm_k_tail_on_padded_rows_in_place(kernels, layout):
+    """K not a multiple of 64 and row counts not a multiple of 8, with rows
+    padded to 8 elements (the lm_head backward's dlogits layout): operands are
+    read in place and the K tail is masked."""
+    m, n, k = 250, 196, 1001
+    pad = lambda v: (v + 7) // 8 * 8  # noqa: E731
+    A = randn(m, k).bfloat16()
+    B = (randn(k, n) * 0.1).bfloat16()
+    if layout[0] == "N":  # A stored [m][pad(k)]
+        store = torch.zeros(m, pad(k), dtype=torch.bfloat16)
+        store[:, :k] = A
+        ta, a_rs, a_cs = dev(store), pad(k), 1
+    else:  # A stored [k][pad(m)]
+        store = torch.zeros(k, pad(m), dtype=torch.bfloat16)
+        store[:, :m] = A.t()
+        ta, a_rs, a_cs = dev(store), 1, pad(m)
+    if layout[1] == "N":  # B stored [k][pad(n)]
+        store = torch.zeros(k, pad(n), dtype=torch.bfloat16)
+        store[:, :n] = B
+        tb, b_rs, b_cs = dev(store), pad(n), 1
+    else:  # B stored [n][pad(k)]
+        store = torch.zeros(n, pad(k), dtype=torch.bfloat16)
+        store[:, :k] = B.t()
+        tb, b_rs, b_cs = dev(store), 1, pad(k)
+    c = torch.empty(m, n, dtype=torch.float32, device="cuda")
+    _gemm(c, ta, tb, m, n, k, a_rs, a_cs, b_rs, b_cs, torch.bfloat16)
+    exp = A.double().numpy() @ B.double().numpy()
+    tol_close(np64(c), exp, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what=f"tail {layout}")
+
+
 def test_gemm_accumulate_and_batched(kernels):
     bsz, m, n, k = 3, 100, 72, 96
     A = randn(bsz, m, k).bfloat16()

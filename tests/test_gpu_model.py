@@ -74,3 +74,28 @@ def test_bounds_errors_surface(mojo):
     with pytest.raises(IndexError):
         F.embedding(torch.tensor([1, 10]).to("mojo"), w)
     assert aten_fast is not None
+
+
+def test_nanogpt_loss_curve_matches_cpu_f32_fixture(mojo):
+    """The headline run (GPT-2 124M, batch 16 x 1024, bf16 autocast, fused
+    AdamW, clip 1.0, 50 steps, 2 batches cycled) tracks the stock-PyTorch f32
+    CPU loss curve committed in tests/golden: within 1% relative every step."""
+    import json
+    from pathlib import Path
+
+    fx = json.loads((Path(__file__).parent / "golden" / "loss_curve_b16_t1024_f32cpu.json").read_text())
+    c = fx["config"]
+    torch.manual_seed(c["seed"])
+    model = GPT(GPTConfig()).to("mojo")
+    opt = model.configure_optimizers(WEIGHT_DECAY, LEARNING_RATE, BETAS, fused=True)
+    batches = [(x.to("mojo"), y.to("mojo"))
+               for x, y in make_batches(c["batch"], c["block"], c["vocab"], c["batches_cycled"],
+                                        c["data_seed"], "cpu")]
+    worst = 0.0
+    for step, ref in enumerate(fx["losses"]):
+        x, y = batches[step % len(batches)]
+        loss = training_step(model, opt, x, y, autocast_dtype=torch.bfloat16).item()
+        rel = abs(loss - ref) / abs(ref)
+        worst = max(worst, rel)
+        assert rel <= 1e-2, (step, loss, ref)
+    print(f"worst relative loss deviation over {len(fx['losses'])} steps: {worst:.2e}")

@@ -330,26 +330,31 @@ struct TileLoad {
   static constexpr int WAVES = NT / 64;
   static constexpr int ITERS = ROWS / (8 * WAVES);
   static_assert(WAVES % 2 == 0, "swizzle invariance needs an even wave count");
-  const char* src;    // thread's source for it = 0 at k = 0
+  const char* src;    // thread's source for it = 0 at k = 0 (without its chunk)
   int64_t row_step;   // bytes between it and it+1
   int64_t first_row;  // row of it = 0 (for clamping)
   int64_t ld;
+  int chunk;          // 16-byte chunk of the 64-element k slab this lane loads
 
   __device__ __forceinline__ void init(const char* base, int64_t ld_bytes, int64_t row0) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = wave * 8 + (lane >> 3);
-    const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+    chunk = (lane & 7) ^ ((r >> 1) & 7);
     first_row = row0 + r;
     ld = ld_bytes;
-    src = base + first_row * ld_bytes + chunk * 16;
+    src = base + first_row * ld_bytes;
     row_step = (int64_t)8 * WAVES * ld_bytes;
   }
-  // k0_bytes: byte offset along k; dst: LDS tile; rows: valid row count.
-  __device__ __forceinline__ void issue(int64_t k0_bytes, char* dst, int64_t rows, bool full) const {
+  // k0_bytes: byte offset along k; dst: LDS tile; rows: valid row count;
+  // kend_bytes: end of the valid k range (a chunk starting past it reloads
+  // chunk 0: its values are masked out of the MFMAs, the address stays valid).
+  __device__ __forceinline__ void issue(int64_t k0_bytes, char* dst, int64_t rows, bool full,
+                                        int64_t kend_bytes) const {
     const int wave = threadIdx.x >> 6;
+    const int64_t coff = (k0_bytes + chunk * 16 < kend_bytes) ? k0_bytes + chunk * 16 : k0_bytes;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-      const char* p = src + it * row_step + k0_bytes;
+      const char* p = src + it * row_step + coff;
       if (!full) {
         const int64_t row = first_row + it * 8 * WAVES;
         if (row >= rows) p -= (row - (rows - 1)) * ld;
@@ -385,16 +390,22 @@ struct TileLoadT {
     krow_l = lane / CPR;
     phys = lane % CPR;
   }
-  __device__ __forceinline__ void issue(int64_t k0, char* dst, bool full) const {
+  // k-rows past kend reload row kend-1 (masked out of the MFMAs); a last
+  // partial chunk of rows reads into the row padding (k stride >= rows
+  // rounded up to 8, checked by the caller).
+  __device__ __forceinline__ void issue(int64_t k0, char* dst, bool full, int64_t kend) const {
     const int wave = threadIdx.x >> 6;
+    const int64_t last_chunk = ((rows - 1) >> 3) << 3;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       const int blk = it * WAVES + wave;
       const int kr = blk * KPI + krow_l;
       const int chunk = phys ^ kswz(kr);
       int64_t m = row0 + chunk * 8;
-      if (!full && m + 8 > rows) m = rows - 8;
-      const char* src = base + (k0 + kr) * ld + m * 2;
+      if (!full && m > last_chunk) m = last_chunk;
+      int64_t k = k0 + kr;
+      if (k >= kend) k = kend - 1;
+      const char* src = base + k * ld + m * 2;
       __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(dst + blk * 1024), 16, 0, 0);
     }
   }
@@ -432,16 +443,27 @@ struct OperandLoad<ROWS, NT, true> {
   TileLoad<ROWS, NT> t;
   int64_t rows;
   __device__ __forceinline__ void init(const char* b, int64_t ld, int64_t r0, int64_t n) { t.init(b, ld, r0); rows = n; }
-  __device__ __forceinline__ void issue(int64_t k0_elems, char* dst, bool full) const {
-    t.issue(k0_elems * 2, dst, rows, full);
+  __device__ __forceinline__ void issue(int64_t k0_elems, char* dst, bool full, int64_t kend) const {
+    t.issue(k0_elems * 2, dst, rows, full, kend * 2);
   }
 };
 template <int ROWS, int NT>
 struct OperandLoad<ROWS, NT, false> {
   TileLoadT<ROWS, NT> t;
   __device__ __forceinline__ void init(const char* b, int64_t ld, int64_t r0, int64_t n) { t.init(b, ld, r0, n); }
-  __device__ __forceinline__ void issue(int64_t k0_elems, char* dst, bool full) const { t.issue(k0_elems, dst, full); }
+  __device__ __forceinline__ void issue(int64_t k0_elems, char* dst, bool full, int64_t kend) const {
+    t.issue(k0_elems, dst, full, kend);
+  }
 };
+
+// Zero the fragment slots whose k index (k0 + ks*32 + 8*g + slot) is >= kend.
+template <typename F>
+__device__ __forceinline__ void mask_k(F& f, int64_t kbase, int64_t kend) {
+  short* fs = (short*)&f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (kbase + e >= kend) fs[e] = 0;
+}
 
 template <typename T, int BM, int BN, bool A_K, bool B_K>
 __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, int tiles_n) {
@@ -491,8 +513,8 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, 
   la.init(A, a_ldb, m0, g.m);
   lb.init(B, b_ldb, n0, g.n);
   const bool full_a = m0 + BM <= g.m, full_b = n0 + BN <= g.n;
-  la.issue(kbeg, lds, full_a);
-  lb.issue(kbeg, lds + A_BYTES, full_b);
+  la.issue(kbeg, lds, full_a, kend);
+  lb.issue(kbeg, lds + A_BYTES, full_b, kend);
   // k-contiguous fragment rows wm*WM + i*16 + lr share the swizzle of lr
   const int sw = (lr >> 1) & 7;
 
@@ -502,25 +524,29 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, 
     __syncthreads();
     if (k0 + 64 < kend) {
       char* nxt = lds + (cur ^ 1) * STAGE;
-      la.issue(k0 + 64, nxt, full_a);
-      lb.issue(k0 + 64, nxt + A_BYTES, full_b);
+      la.issue(k0 + 64, nxt, full_a, kend);
+      lb.issue(k0 + 64, nxt + A_BYTES, full_b, kend);
     }
     const char* at = lds + cur * STAGE;
     const char* bt = at + A_BYTES;
+    const bool tail = k0 + 64 > kend;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int coff = ((ks * 4 + lg) ^ sw) * 16;
+      const int64_t kfrag = k0 + ks * 32 + lg * 8;
       frag bfr[TN];
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         if constexpr (B_K) bfr[j] = *(const frag*)(bt + (wn * WN + lr) * 128 + j * 2048 + coff);
         else bfr[j] = mn_frag<T, BN>(bt, wn * WN + j * 16, ks);
+        if (tail) mask_k(bfr[j], kfrag, kend);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         frag af;
         if constexpr (A_K) af = *(const frag*)(at + (wm * WM + lr) * 128 + i * 2048 + coff);
         else af = mn_frag<T, BM>(at, wm * WM + i * 16, ks);
+        if (tail) mask_k(af, kfrag, kend);
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af, bfr[j], acc[i][j]);
       }
@@ -773,14 +799,16 @@ WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int64_t k, const void* a
                    int64_t b_bs) {
   WsLayout w{};
   w.kp = (k + 63) / 64 * 64;
-  const bool k64 = k % 64 == 0;
   // In place when K tiles are whole and every 16-byte load is aligned:
   // k-contiguous operands need an 8-element row stride, m/n-contiguous ones
   // an 8-element k stride and a row count that is a multiple of 8.
+  // K tails are masked in the kernel; a last partial 8-element chunk may
+  // read into row padding, so the contiguous extent must be padded to 8.
+  auto up8 = [](int64_t v) { return (v + 7) / 8 * 8; };
   auto in_place = [&](const void* p, int64_t rs, int64_t cs, int64_t bs, int64_t nrows) {
-    if (!k64 || bs % 8 != 0 || (p != nullptr && !aligned16(p))) return false;
-    if (cs == 1) return rs % 8 == 0;
-    return cs % 8 == 0 && nrows % 8 == 0 && nrows >= 8;
+    if (bs % 8 != 0 || (p != nullptr && !aligned16(p))) return false;
+    if (cs == 1) return rs % 8 == 0 && rs >= up8(k);
+    return cs % 8 == 0 && cs >= up8(nrows);
   };
   // An m/n-contiguous operand that is small next to the product (a weight in
   // dX = dY W) is still packed: the copy costs under ~3% of the GEMM and the
@@ -865,7 +893,7 @@ extern "C" int mi355x_gemm(void* c, int c_dtype, int64_t c_rs, int64_t c_bs, con
     if (rc) return rc;
     g.b = pb; g.b_rs = 1; g.b_cs = w.kp; g.b_bs = b_bs == 0 ? 0 : n * w.kp;
   }
-  g.k = w.kp;
+  // packed operands are zero-padded to kp; the kernel masks k >= K
   if (w.plan.splits > 1) {
     g.part = (float*)ws;
     g.kchunk = w.plan.kchunk;
