@@ -330,7 +330,7 @@ struct TileLoad {
   static constexpr int WAVES = NT / 64;
   static constexpr int ITERS = ROWS / (8 * WAVES);
   static_assert(WAVES % 2 == 0, "swizzle invariance needs an even wave count");
-  const char* src;    // thread's source for it = 0 at k = 0 (without its chunk)
+  const char* src;    // thread's source for it = 0 at k = 0 (its chunk included)
   int64_t row_step;   // bytes between it and it+1
   int64_t first_row;  // row of it = 0 (for clamping)
   int64_t ld;
@@ -342,16 +342,18 @@ struct TileLoad {
     chunk = (lane & 7) ^ ((r >> 1) & 7);
     first_row = row0 + r;
     ld = ld_bytes;
-    src = base + first_row * ld_bytes;
+    src = base + first_row * ld_bytes + chunk * 16;
     row_step = (int64_t)8 * WAVES * ld_bytes;
   }
   // k0_bytes: byte offset along k; dst: LDS tile; rows: valid row count;
   // kend_bytes: end of the valid k range (a chunk starting past it reloads
   // chunk 0: its values are masked out of the MFMAs, the address stays valid).
+  // KT = false: K is a multiple of 64 and no clamp is needed.
+  template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0_bytes, char* dst, int64_t rows, bool full,
                                         int64_t kend_bytes) const {
     const int wave = threadIdx.x >> 6;
-    const int64_t coff = (k0_bytes + chunk * 16 < kend_bytes) ? k0_bytes + chunk * 16 : k0_bytes;
+    const int64_t coff = (KT && k0_bytes + chunk * 16 >= kend_bytes) ? k0_bytes - chunk * 16 : k0_bytes;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       const char* p = src + it * row_step + coff;
@@ -393,6 +395,7 @@ struct TileLoadT {
   // k-rows past kend reload row kend-1 (masked out of the MFMAs); a last
   // partial chunk of rows reads into the row padding (k stride >= rows
   // rounded up to 8, checked by the caller).
+  template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0, char* dst, bool full, int64_t kend) const {
     const int wave = threadIdx.x >> 6;
     const int64_t last_chunk = ((rows - 1) >> 3) << 3;
@@ -404,7 +407,7 @@ struct TileLoadT {
       int64_t m = row0 + chunk * 8;
       if (!full && m > last_chunk) m = last_chunk;
       int64_t k = k0 + kr;
-      if (k >= kend) k = kend - 1;
+      if (KT && k >= kend) k = kend - 1;
       const char* src = base + k * ld + m * 2;
       __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(dst + blk * 1024), 16, 0, 0);
     }
@@ -443,16 +446,18 @@ struct OperandLoad<ROWS, NT, true> {
   TileLoad<ROWS, NT> t;
   int64_t rows;
   __device__ __forceinline__ void init(const char* b, int64_t ld, int64_t r0, int64_t n) { t.init(b, ld, r0); rows = n; }
+  template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0_elems, char* dst, bool full, int64_t kend) const {
-    t.issue(k0_elems * 2, dst, rows, full, kend * 2);
+    t.template issue<KT>(k0_elems * 2, dst, rows, full, kend * 2);
   }
 };
 template <int ROWS, int NT>
 struct OperandLoad<ROWS, NT, false> {
   TileLoadT<ROWS, NT> t;
   __device__ __forceinline__ void init(const char* b, int64_t ld, int64_t r0, int64_t n) { t.init(b, ld, r0, n); }
+  template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0_elems, char* dst, bool full, int64_t kend) const {
-    t.issue(k0_elems, dst, full, kend);
+    t.template issue<KT>(k0_elems, dst, full, kend);
   }
 };
 
@@ -465,7 +470,9 @@ __device__ __forceinline__ void mask_k(F& f, int64_t kbase, int64_t kend) {
     if (kbase + e >= kend) fs[e] = 0;
 }
 
-template <typename T, int BM, int BN, bool A_K, bool B_K>
+// KT: K is not a multiple of 64, so the last k step clamps its loads and
+// masks the fragments past K.
+template <typename T, int BM, int BN, bool A_K, bool B_K, bool KT>
 __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, int tiles_n) {
   typedef typename Mfma<T>::frag frag;
   constexpr int NT = 256;
@@ -513,8 +520,8 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, 
   la.init(A, a_ldb, m0, g.m);
   lb.init(B, b_ldb, n0, g.n);
   const bool full_a = m0 + BM <= g.m, full_b = n0 + BN <= g.n;
-  la.issue(kbeg, lds, full_a, kend);
-  lb.issue(kbeg, lds + A_BYTES, full_b, kend);
+  la.template issue<KT>(kbeg, lds, full_a, kend);
+  lb.template issue<KT>(kbeg, lds + A_BYTES, full_b, kend);
   // k-contiguous fragment rows wm*WM + i*16 + lr share the swizzle of lr
   const int sw = (lr >> 1) & 7;
 
@@ -524,12 +531,12 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_fast(GemmArgs g, int tiles_m, 
     __syncthreads();
     if (k0 + 64 < kend) {
       char* nxt = lds + (cur ^ 1) * STAGE;
-      la.issue(k0 + 64, nxt, full_a, kend);
-      lb.issue(k0 + 64, nxt + A_BYTES, full_b, kend);
+      la.template issue<KT>(k0 + 64, nxt, full_a, kend);
+      lb.template issue<KT>(k0 + 64, nxt + A_BYTES, full_b, kend);
     }
     const char* at = lds + cur * STAGE;
     const char* bt = at + A_BYTES;
-    const bool tail = k0 + 64 > kend;
+    const bool tail = KT && k0 + 64 > kend;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int coff = ((ks * 4 + lg) ^ sw) * 16;
@@ -741,17 +748,23 @@ int launch_cfg(const GemmArgs& g, int64_t batch, int splits, hipStream_t s) {
   return check_launch("mi355x_gemm");
 }
 
+template <typename T, int BM, int BN, bool KT>
+int launch_fast_kt(const GemmArgs& g, int64_t blocks, size_t lds, int tm, int tn, hipStream_t s) {
+  const bool ak = g.a_cs == 1, bk = g.b_rs == 1;
+  if (ak && bk) gemm_nt_fast<T, BM, BN, true, true, KT><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
+  else if (ak) gemm_nt_fast<T, BM, BN, true, false, KT><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
+  else if (bk) gemm_nt_fast<T, BM, BN, false, true, KT><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
+  else gemm_nt_fast<T, BM, BN, false, false, KT><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
+  return check_launch("mi355x_gemm");
+}
+
 template <typename T, int BM, int BN>
 int launch_fast_cfg(const GemmArgs& g, int64_t batch, int splits, hipStream_t s) {
   const int tm = (int)ceil_div(g.m, BM), tn = (int)ceil_div(g.n, BN);
   const int64_t blocks = (int64_t)tm * tn * batch * splits;
   const size_t lds = 2 * (BM + BN) * 128;
-  const bool ak = g.a_cs == 1, bk = g.b_rs == 1;
-  if (ak && bk) gemm_nt_fast<T, BM, BN, true, true><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
-  else if (ak) gemm_nt_fast<T, BM, BN, true, false><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
-  else if (bk) gemm_nt_fast<T, BM, BN, false, true><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
-  else gemm_nt_fast<T, BM, BN, false, false><<<(unsigned)blocks, 256, lds, s>>>(g, tm, tn);
-  return check_launch("mi355x_gemm");
+  if (g.k % 64) return launch_fast_kt<T, BM, BN, true>(g, blocks, lds, tm, tn, s);
+  return launch_fast_kt<T, BM, BN, false>(g, blocks, lds, tm, tn, s);
 }
 
 int splitk_finish(const GemmArgs& g, int64_t batch, int splits, hipStream_t s) {
