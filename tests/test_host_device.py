@@ -1,0 +1,146 @@
+"""The mojo device's host layer on the CPU (no GPU): dispatch, views,
+autograd and autocast routing, argument packing, error behaviour.
+
+The device runs over the host stand-in of the kernel library here
+(tests/host_standin.py), so these tests check the Python side and the ABI
+contract it relies on, not the gfx950 kernels (the `gpu` tests do that).
+The reference's own device tests follow the same pattern: build on the
+device, compare with stock PyTorch CPU (torch_mojo_backend/testing.py:
+186-229).
+"""
+
+from __future__ import annotations
+
+import subprocess
+import sys
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import HAS_GPU, ROOT
+
+pytestmark = pytest.mark.skipif(HAS_GPU, reason="host stand-in tests run where there is no GPU")
+
+
+def test_device_identity_and_copies(mojo):
+    x = torch.randn(4, 8)
+    xm = x.to("mojo")
+    assert xm.device.type == "mojo" and xm.device.index == 0
+    assert torch.device("mojo:0") == xm.device
+    assert torch.equal(xm.cpu(), x)
+    assert torch.equal(torch.empty(3, device="mojo").fill_(2.5).cpu(), torch.full((3,), 2.5))
+    assert torch.equal(torch.arange(7, device="mojo").cpu(), torch.arange(7))
+
+
+def test_views_share_storage_and_strides(mojo):
+    x = torch.randn(6, 10)
+    xm = x.to("mojo")
+    for f in (lambda t: t.t(), lambda t: t[1:5, ::3], lambda t: t.view(2, 3, 10).transpose(0, 2),
+              lambda t: t.narrow(1, 2, 5), lambda t: t.unsqueeze(0).expand(3, 6, 10)):
+        v = f(xm)
+        assert v.shape == f(x).shape and v.stride() == f(x).stride()
+        assert torch.equal(v.cpu(), f(x))
+    v = xm[2]
+    v.mul_(0)
+    assert (xm.cpu()[2] == 0).all()
+
+
+def test_elementwise_reduction_and_indexing(mojo):
+    g = torch.Generator().manual_seed(1)
+    a, b = torch.randn(5, 7, generator=g), torch.randn(5, 7, generator=g)
+    am, bm = a.to("mojo"), b.to("mojo")
+    assert torch.allclose((am * bm + am / (bm.abs() + 1)).cpu(), a * b + a / (b.abs() + 1))
+    assert torch.allclose(am.sum(1).cpu(), a.sum(1), atol=1e-6)
+    assert torch.equal(am.argmax(1).cpu(), a.argmax(1))
+    idx = torch.tensor([4, 0, 4, 2])
+    assert torch.equal(am.index_select(0, idx.to("mojo")).cpu(), a.index_select(0, idx))
+    assert torch.equal(torch.cat([am, bm], 1).cpu(), torch.cat([a, b], 1))
+
+
+def test_sdpa_autograd_routes_to_the_flash_pair(mojo):
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(2, 2, 32, 64, generator=g).bfloat16() for _ in range(3))
+    qm, km, vm = (t.to("mojo").requires_grad_() for t in (q, k, v))
+    out = F.scaled_dot_product_attention(qm, km, vm, is_causal=True)
+    assert type(out.grad_fn).__name__ == "ScaledDotProductFlashAttentionBackward0"
+    out.float().sum().backward()
+    qc, kc, vc = (t.float().requires_grad_() for t in (q, k, v))
+    ref = F.scaled_dot_product_attention(qc, kc, vc, is_causal=True)
+    ref.sum().backward()
+    assert torch.allclose(out.float().cpu(), ref, atol=2e-2, rtol=2e-2)
+    for a, b in ((qm, qc), (km, kc), (vm, vc)):
+        assert torch.allclose(a.grad.float().cpu(), b.grad, atol=5e-2, rtol=5e-2)
+
+
+def test_sdpa_with_mask_uses_the_math_route(mojo):
+    q = torch.randn(1, 2, 8, 16).to("mojo").requires_grad_()
+    mask = torch.ones(8, 8, dtype=torch.bool).tril().to("mojo")
+    out = F.scaled_dot_product_attention(q, q, q, attn_mask=mask)
+    assert "Flash" not in type(out.grad_fn).__name__
+    ref = F.scaled_dot_product_attention(q.detach().cpu(), q.detach().cpu(), q.detach().cpu(),
+                                         attn_mask=mask.cpu())
+    assert torch.allclose(out.detach().cpu(), ref, atol=1e-5)
+
+
+def test_autocast_policy(mojo):
+    a, b = torch.randn(4, 8).to("mojo"), torch.randn(8, 3).to("mojo")
+    x = torch.randn(4, 8).to("mojo")
+    with torch.autocast("mojo", dtype=torch.bfloat16):
+        assert (a @ b).dtype == torch.bfloat16
+        assert F.layer_norm(x.bfloat16(), (8,)).dtype == torch.float32
+        assert (a + 1).dtype == torch.float32  # everything else falls through
+
+
+def test_fused_cross_entropy_matches_cpu(mojo):
+    g = torch.Generator().manual_seed(3)
+    logits, tgt = torch.randn(6, 37, generator=g), torch.tensor([1, 36, -100, 0, 5, 5])
+    lm = logits.to("mojo").requires_grad_()
+    loss = F.cross_entropy(lm, tgt.to("mojo"), ignore_index=-100)
+    loss.backward()
+    lc = logits.clone().requires_grad_()
+    ref = F.cross_entropy(lc, tgt, ignore_index=-100)
+    ref.backward()
+    assert torch.allclose(loss.cpu(), ref, atol=1e-6)
+    assert torch.allclose(lm.grad.cpu(), lc.grad, atol=1e-6)
+    with pytest.raises(NotImplementedError):
+        F.cross_entropy(lm, tgt.to("mojo"), label_smoothing=0.1)
+
+
+def test_gpt_step_matches_cpu(mojo):
+    from torch_mojo_backend.gpt2 import BETAS, LEARNING_RATE, WEIGHT_DECAY, GPT, GPTConfig, make_batches, training_step
+
+    cfg = GPTConfig(block_size=64, vocab_size=97, n_layer=2, n_head=2, n_embd=32)
+    torch.manual_seed(0)
+    ref = GPT(cfg)
+    model = GPT(cfg)
+    model.load_state_dict(ref.state_dict())
+    model.to("mojo")
+    assert model.lm_head.weight is model.transformer.wte.weight
+    opt = model.configure_optimizers(WEIGHT_DECAY, LEARNING_RATE, BETAS, fused=True)
+    ropt = ref.configure_optimizers(WEIGHT_DECAY, LEARNING_RATE, BETAS, fused=True)
+    for x, y in make_batches(2, 64, cfg.vocab_size, 3, 5, "cpu"):
+        lr_ = training_step(ref, ropt, x, y).item()
+        lm = training_step(model, opt, x.to("mojo"), y.to("mojo")).item()
+        assert abs(lm - lr_) <= 1e-4 * abs(lr_)
+    for (name, p_ref), p in zip(ref.named_parameters(), model.parameters()):
+        assert torch.allclose(p.detach().cpu(), p_ref.detach(), atol=1e-5, rtol=1e-4), name
+
+
+def test_embedding_out_of_range_raises(mojo):
+    w = torch.randn(10, 4).to("mojo")
+    with pytest.raises(IndexError):
+        F.embedding(torch.tensor([1, 10]).to("mojo"), w)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """No kernel library -> KernelLibraryError naming the build command; there
+    is no CPU fallback."""
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "from torch_mojo_backend import eager_kernels as ek\n"
+        "try:\n    ek.lib()\nexcept ek.KernelLibraryError as e:\n    print('RAISED', e)\n"
+    ) % str(ROOT / "torch-mojo-backend_amd")
+    env = {"MI355X_KERNELS_LIB": str(tmp_path / "absent.so"), "PATH": "/usr/bin:/bin"}
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert "RAISED" in r.stdout and "build" in r.stdout, r.stdout + r.stderr
