@@ -297,7 +297,9 @@ int mi355x_cross_entropy_fwd(void* out, float* total_weight, float* lse,
                              int32_t* err_flag, void* workspace,
                              int64_t ws_bytes, mi355x_stream_t stream);
 /* dx[i, :] = g_i * (softmax(x_i) - onehot(t_i)) with rows at dx + i*ld_dx;
- * columns [c, ld_dx) are written as zero.  grad_out: f32 scalar or [n]. */
+ * columns [c, ld_dx) are written as zero.  grad_out: f32 scalar or [n].
+ * dx has the logits' dtype, a 16-byte aligned base and ld_dx a multiple of
+ * 16 bytes' worth of elements (8 for bf16/f16, 4 for f32). */
 int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx,
                              const void* logits, int dtype, int64_t ld,
                              const float* lse, const int64_t* target,

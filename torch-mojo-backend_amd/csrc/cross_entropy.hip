@@ -2,13 +2,24 @@
 // targets: the log_softmax -> nll_loss chain of the training step without
 // materialising log-probabilities or a dense one-hot gradient.
 //
-// Forward, one 512-thread block per row: an online (max, sum-of-exp) pass
-// gives lse_i; row loss = lse_i - x_i[t_i] (0 for ignore_index).  A second
-// one-block kernel reduces the row losses in a fixed order into the mean or
-// sum and writes total_weight (the count of non-ignored rows).
+// Rows are visited as aligned 16-byte chunks.  A row of the [16384, 50257]
+// logits starts at any 2-byte boundary (phase p = its start's offset inside
+// a 16-byte granule, uniform per row): aligned chunk j covers elements
+// [V*j - p, V*j - p + V) (V = 16 / sizeof(T)); elements outside [0, c) are
+// masked.  A chunk never leaves the 16-byte granules the row touches, so no
+// load crosses into memory the row does not own a byte of.
+//
+// Forward, one 256-thread block per row: an online (max, sum) in the exp2
+// domain with one rescale per chunk (max of the chunk first), four chunks in
+// flight per thread; lse_i = ln(sum) + max.  Row loss = lse_i - x_i[t_i] (0
+// for ignore_index).  A one-block kernel reduces the row losses in a fixed
+// order into the mean or sum and writes total_weight.
 // Backward, one block per row: dx_i = g_i * (exp(x_i - lse_i) - onehot(t_i)),
 // g_i = grad (per row for reduction none, else the scalar, / total_weight
-// for mean), zero for ignored rows; columns [c, ld_dx) of dx are zero-filled.
+// for mean), zero for ignored rows and for the padding columns [c, ld_dx).
+// dx rows are 16-byte aligned (ld_dx a multiple of V), so each thread writes
+// whole 16-byte dx chunks; the V logits one needs come from two aligned
+// chunks shifted by the row's phase (v_alignbyte).
 // HBM traffic: forward reads the logits once; backward reads them once and
 // writes dx once.
 #include <math.h>
@@ -18,67 +29,114 @@
 namespace mi {
 namespace {
 
-constexpr int kRowThreads = 512;
+constexpr int kRowThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
-struct MS {
-  float m, s;
+template <typename T>
+struct Chunk {
+  static constexpr int V = 16 / sizeof(T);
+  uint4 w;
+  __device__ __forceinline__ float get(int e) const {
+    if constexpr (sizeof(T) == 4) return __uint_as_float((&w.x)[e]);
+    else {
+      const uint32_t u = (&w.x)[e >> 1];
+      const unsigned short h = (e & 1) ? (unsigned short)(u >> 16) : (unsigned short)(u & 0xffff);
+      return to_f32(__builtin_bit_cast(T, h));
+    }
+  }
 };
-__device__ __forceinline__ MS ms_fold(MS a, float x) {
-  if (x == -INFINITY) return a;
-  if (x != x) return MS{x, a.s};
-  if (x > a.m) {
-    const float s = (a.m == -INFINITY) ? 0.f : a.s * expf(a.m - x);
-    return MS{x, s + 1.f};
-  }
-  return MS{a.m, a.s + expf(x - a.m)};
-}
-__device__ __forceinline__ MS ms_merge(MS a, MS b) {
-  if (a.m != a.m || b.m != b.m) return MS{a.m != a.m ? a.m : b.m, 0.f};
-  if (a.m == -INFINITY) return b;
-  if (b.m == -INFINITY) return a;
-  const float m = fmaxf(a.m, b.m);
-  return MS{m, a.s * expf(a.m - m) + b.s * expf(b.m - m)};
-}
 
-// Visit x[0..c) of one row with 16-byte loads where aligned.
-template <typename T, typename F>
-__device__ __forceinline__ void for_row(const T* r, int64_t c, F&& f) {
-  constexpr int V = 16 / sizeof(T);
-  int64_t head = (int64_t)(((16 - ((uintptr_t)r & 15)) & 15) / sizeof(T));
-  if (((uintptr_t)r % sizeof(T)) != 0) head = c;
-  if (head > c) head = c;
-  for (int64_t k = threadIdx.x; k < head; k += kRowThreads) f(k, to_f32(r[k]));
-  const int64_t nv = (c - head) / V;
-  const T* body = r + head;
-  for (int64_t q = threadIdx.x; q < nv; q += kRowThreads) {
-    struct alignas(16) P { T v[V]; } p = ((const P*)body)[q];
-#pragma unroll
-    for (int e = 0; e < V; ++e) f(head + q * V + e, to_f32(p.v[e]));
+// Row geometry: aligned base, phase and the number of aligned chunks that
+// hold elements of [0, c).
+template <typename T>
+struct RowGeo {
+  static constexpr int V = 16 / sizeof(T);
+  const uint4* base;
+  int p;
+  int64_t nch;
+  __device__ __forceinline__ RowGeo(const T* r, int64_t c) {
+    const uintptr_t a = (uintptr_t)r & ~(uintptr_t)15;
+    base = (const uint4*)a;
+    p = (int)(((uintptr_t)r - a) / sizeof(T));
+    nch = (c + p + V - 1) / V;
   }
-  for (int64_t k = head + nv * V + threadIdx.x; k < c; k += kRowThreads) f(k, to_f32(r[k]));
-}
+};
 
 template <typename T>
 __global__ void __launch_bounds__(kRowThreads)
     ce_fwd_rows(float* __restrict__ row_loss, float* __restrict__ row_valid, float* __restrict__ lse,
                 const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ target, int64_t n,
                 int64_t c, int64_t ignore_index, int32_t* err) {
-  __shared__ MS red[kRowThreads / 64];
+  constexpr int V = Chunk<T>::V, U = 4;
+  __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64];
+  __shared__ int red_nan[kRowThreads / 64];
   const int64_t row = blockIdx.x;
   const T* r = x + row * ld;
-  MS acc{-INFINITY, 0.f};
-  for_row(r, c, [&](int64_t, float v) { acc = ms_fold(acc, v); });
+  const RowGeo<T> geo(r, c);
+  float m = -INFINITY, sum = 0.f;  // max and sum of exp2((x - m) * log2e)
+  bool nan = false;
+  for (int64_t j0 = threadIdx.x; j0 < geo.nch; j0 += (int64_t)kRowThreads * U) {
+    Chunk<T> ch[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + (int64_t)u * kRowThreads;
+      if (j < geo.nch) ch[u].w = geo.base[j];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + (int64_t)u * kRowThreads;
+      if (j >= geo.nch) break;
+      const int64_t k0 = j * V - geo.p;
+      float v[V];
+      float cm = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const int64_t k = k0 + e;
+        v[e] = (k >= 0 && k < c) ? ch[u].get(e) : -INFINITY;
+        nan |= v[e] != v[e];
+        cm = fmaxf(cm, v[e]);
+      }
+      if (cm == -INFINITY) continue;
+      if (cm > m) {
+        sum = (m == -INFINITY) ? 0.f : sum * exp2f((m - cm) * kLog2e);
+        m = cm;
+      }
+#pragma unroll
+      for (int e = 0; e < V; ++e) sum += exp2f((v[e] - m) * kLog2e);
+    }
+  }
+  // wave then block merge of (m, sum)
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    MS o{__shfl_xor(acc.m, off, 64), __shfl_xor(acc.s, off, 64)};
-    acc = ms_merge(acc, o);
+    const float om = __shfl_xor(m, off, 64), os = __shfl_xor(sum, off, 64);
+    nan |= __shfl_xor((int)nan, off, 64) != 0;
+    const float nm = fmaxf(m, om);
+    if (nm != -INFINITY) {
+      sum = (m == -INFINITY ? 0.f : sum * exp2f((m - nm) * kLog2e)) +
+            (om == -INFINITY ? 0.f : os * exp2f((om - nm) * kLog2e));
+      m = nm;
+    }
   }
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  if ((threadIdx.x & 63) == 0) {
+    red_m[threadIdx.x >> 6] = m;
+    red_s[threadIdx.x >> 6] = sum;
+    red_nan[threadIdx.x >> 6] = nan;
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
-    MS t = red[0];
-    for (int w = 1; w < kRowThreads / 64; ++w) t = ms_merge(t, red[w]);
-    const float l = t.m + logf(t.s);
+    float tm = -INFINITY, ts = 0.f;
+    bool tn = false;
+    for (int w = 0; w < kRowThreads / 64; ++w) {
+      tn |= red_nan[w] != 0;
+      const float om = red_m[w], os = red_s[w];
+      const float nm = fmaxf(tm, om);
+      if (nm == -INFINITY) continue;
+      ts = (tm == -INFINITY ? 0.f : ts * exp2f((tm - nm) * kLog2e)) +
+           (om == -INFINITY ? 0.f : os * exp2f((om - nm) * kLog2e));
+      tm = nm;
+    }
+    const float l = tn ? __int_as_float(0x7fc00000) : tm + log2f(ts) * kLn2;
     lse[row] = l;
     const int64_t tg = target[row];
     float loss = 0.f, valid = 0.f;
@@ -110,30 +168,65 @@ __global__ void __launch_bounds__(1024) ce_fwd_reduce(float* __restrict__ out, f
   }
 }
 
-template <typename TX, typename TD>
+// The V elements of x starting at element V*t of the row: aligned chunks t
+// and t+1 shifted right by the row phase (bytes b = p * sizeof(T)).
+__device__ __forceinline__ uint4 shift_pair(uint4 lo, uint4 hi, int bytes) {
+  const uint32_t W[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  const int r = bytes & 3;
+  uint4 o;
+  uint32_t* ow = &o.x;
+  switch (bytes >> 2) {  // uniform per row
+#define CE_SHIFT(Q)                                                                            \
+  case Q:                                                                                      \
+    for (int i = 0; i < 4; ++i) ow[i] = __builtin_amdgcn_alignbyte(W[i + Q + 1], W[i + Q], r); \
+    break;
+    CE_SHIFT(0)
+    CE_SHIFT(1)
+    CE_SHIFT(2)
+    CE_SHIFT(3)
+#undef CE_SHIFT
+  }
+  return o;
+}
+
+template <typename T, typename TD>
 __global__ void __launch_bounds__(kRowThreads)
-    ce_bwd_rows(TD* __restrict__ dx, int64_t ld_dx, const TX* __restrict__ x, int64_t ld,
+    ce_bwd_rows(TD* __restrict__ dx, int64_t ld_dx, const T* __restrict__ x, int64_t ld,
                 const float* __restrict__ lse, const int64_t* __restrict__ target,
                 const float* __restrict__ grad, int grad_per_row, const float* __restrict__ total,
                 int64_t n, int64_t c, int64_t ignore_index) {
+  constexpr int V = Chunk<T>::V;
+  static_assert(sizeof(TD) == sizeof(T), "dx chunks follow the logits chunks");
   const int64_t row = blockIdx.x;
   const int64_t tg = target[row];
   float g = grad[grad_per_row ? row : 0];
   if (!grad_per_row && total) g /= total[0];
   const bool valid = tg != ignore_index && tg >= 0 && tg < c;
-  const float l = lse[row];
-  TD* o = dx + row * ld_dx;
-  const TX* r = x + row * ld;
-  constexpr int V = 16 / sizeof(TD);
-  // x is read element-wise through for_row; dx rows are written in the same
-  // index order (each thread owns the indices it reads).
   if (!valid) g = 0.f;
-  for_row(r, c, [&](int64_t k, float v) {
-    float p = expf(v - l);
-    o[k] = from_f32<TD>(g * (p - (k == tg ? 1.f : 0.f)));
-  });
-  (void)V;
-  for (int64_t k = c + threadIdx.x; k < ld_dx; k += kRowThreads) o[k] = from_f32<TD>(0.f);
+  const float l = lse[row];
+  const T* r = x + row * ld;
+  const RowGeo<T> geo(r, c);
+  const int bytes = geo.p * (int)sizeof(T);
+  uint4* o = (uint4*)(dx + row * ld_dx);
+  const int64_t nout = ld_dx / V;
+  for (int64_t t = threadIdx.x; t < nout; t += kRowThreads) {
+    const int64_t k0 = t * V;
+    Chunk<T> ch;
+    if (k0 < c) {
+      const uint4 lo = geo.base[t];
+      const uint4 hi = (bytes && t + 1 < geo.nch) ? geo.base[t + 1] : make_uint4(0, 0, 0, 0);
+      ch.w = bytes ? shift_pair(lo, hi, bytes) : lo;
+    }
+    struct alignas(16) Out { TD v[V]; } out;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int64_t k = k0 + e;
+      float d = 0.f;
+      if (k < c) d = g * (exp2f((ch.get(e) - l) * kLog2e) - (k == tg ? 1.f : 0.f));
+      out.v[e] = from_f32<TD>(d);
+    }
+    o[t] = *(const uint4*)&out;
+  }
 }
 
 }  // namespace
@@ -150,6 +243,8 @@ extern "C" int mi355x_cross_entropy_fwd(void* out, float* total_weight, float* l
                                         mi355x_stream_t stream) {
   MI_REQUIRE(n >= 0 && c > 0 && ld >= c, "mi355x_cross_entropy_fwd: bad shape");
   MI_REQUIRE(reduction >= 0 && reduction <= 2, "mi355x_cross_entropy_fwd: bad reduction");
+  MI_REQUIRE(dtype_size(dtype) == 0 || ((uintptr_t)logits % dtype_size(dtype)) == 0,
+             "mi355x_cross_entropy_fwd: misaligned logits");
   if (n == 0) return MI355X_OK;
   MI_REQUIRE(n < (1ll << 31), "mi355x_cross_entropy_fwd: too many rows");
   const int64_t need = mi355x_cross_entropy_workspace_bytes(n);
@@ -176,6 +271,10 @@ extern "C" int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx, c
                                         int reduction, const float* total_weight, int64_t n,
                                         int64_t c, int64_t ignore_index, mi355x_stream_t stream) {
   MI_REQUIRE(n >= 0 && c > 0 && ld >= c && ld_dx >= c, "mi355x_cross_entropy_bwd: bad shape");
+  const int64_t v = 16 / (int64_t)dtype_size(dx_dtype);
+  MI_REQUIRE(ld_dx % v == 0 && ((uintptr_t)dx % 16) == 0,
+             "mi355x_cross_entropy_bwd: dx rows must be 16-byte aligned (ld_dx a multiple of %lld)", (long long)v);
+  MI_REQUIRE(((uintptr_t)logits % dtype_size(dtype)) == 0, "mi355x_cross_entropy_bwd: misaligned logits");
   if (n == 0) return MI355X_OK;
   hipStream_t s = (hipStream_t)stream;
   const int per_row = reduction == 0;
@@ -187,7 +286,6 @@ extern "C" int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx, c
   if (dtype == MI355X_BF16 && dx_dtype == MI355X_BF16) CE_BWD(bf16, bf16);
   else if (dtype == MI355X_F32 && dx_dtype == MI355X_F32) CE_BWD(float, float);
   else if (dtype == MI355X_F16 && dx_dtype == MI355X_F16) CE_BWD(f16, f16);
-  else if (dtype == MI355X_BF16 && dx_dtype == MI355X_F32) CE_BWD(bf16, float);
   else return fail(MI355X_EUNSUPPORTED, "mi355x_cross_entropy_bwd: unsupported dtypes %d/%d", dtype, dx_dtype);
 #undef CE_BWD
   return check_launch("mi355x_cross_entropy_bwd");

@@ -347,16 +347,26 @@ __global__ void __launch_bounds__(kThreads) map_dense(MapArgs a, int64_t n) {
   }
 }
 
-// Vectorised dense binary add/sub/mul/div over f32 (residual adds, grad
-// accumulation): 4 elements per 128-bit access.
-__global__ void __launch_bounds__(kThreads) binary_f32x4(int op, float* __restrict__ out,
-                                                         const float* __restrict__ x,
-                                                         const float* __restrict__ y,
-                                                         float alpha, int64_t n4) {
+// Vectorised dense binary add/sub/mul/div with an f32 output and f32 or
+// bf16 inputs (residual adds of a bf16 branch into the f32 stream, grad
+// accumulation): 4 elements per access, the bf16 side widened exactly.
+template <typename TX, typename TY>
+__device__ __forceinline__ float4 ld4(const TX* p, int64_t i);
+template <>
+__device__ __forceinline__ float4 ld4<float, float>(const float* p, int64_t i) { return ((const float4*)p)[i]; }
+template <>
+__device__ __forceinline__ float4 ld4<bf16, float>(const bf16* p, int64_t i) {
+  bf16x4 v = ((const bf16x4*)p)[i];
+  return float4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+
+template <typename TX, typename TY>
+__global__ void __launch_bounds__(kThreads) binary_x4(int op, float* __restrict__ out, const TX* __restrict__ x,
+                                                      const TY* __restrict__ y, float alpha, int64_t n4) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4;
        i += (int64_t)gridDim.x * kThreads) {
-    float4 a = ((const float4*)x)[i];
-    float4 b = ((const float4*)y)[i];
+    const float4 a = ld4<TX, float>(x, i);
+    const float4 b = ld4<TY, float>(y, i);
     float4 r;
     if (op == MI355X_OP_ADD) {
       r.x = a.x + alpha * b.x; r.y = a.y + alpha * b.y; r.z = a.z + alpha * b.z; r.w = a.w + alpha * b.w;
@@ -597,12 +607,20 @@ extern "C" int mi355x_map(int op, void* out, int out_dtype, int nin, const void*
         return fail(MI355X_EUNSUPPORTED, "mi355x_map: op %d needs a floating output", op);
     }
   }
+  const auto f32_or_bf16 = [](int d) { return d == MI355X_F32 || d == MI355X_BF16; };
   if (g.ndim == 1 && geo_dense(g) && nin == 2 && ins[0] && ins[1] && out_dtype == MI355X_F32 &&
-      in_dtypes[0] == MI355X_F32 && in_dtypes[1] == MI355X_F32 && n % 4 == 0 &&
-      aligned(out, 16) && aligned(ins[0], 16) && aligned(ins[1], 16) &&
+      f32_or_bf16(in_dtypes[0]) && f32_or_bf16(in_dtypes[1]) && n % 4 == 0 && aligned(out, 16) &&
+      aligned(ins[0], 8) && aligned(ins[1], 8) &&
+      (in_dtypes[0] == MI355X_BF16 || aligned(ins[0], 16)) && (in_dtypes[1] == MI355X_BF16 || aligned(ins[1], 16)) &&
       (op == MI355X_OP_ADD || op == MI355X_OP_SUB || op == MI355X_OP_MUL || op == MI355X_OP_DIV)) {
-    binary_f32x4<<<grid_for(n / 4, 2), kThreads, 0, s>>>(op, (float*)out, (const float*)ins[0],
-                                                          (const float*)ins[1], (float)s0, n / 4);
+    const unsigned grid = grid_for(n / 4, 2);
+    const float al = (float)s0;
+    float* o = (float*)out;
+    const bool xb = in_dtypes[0] == MI355X_BF16, yb = in_dtypes[1] == MI355X_BF16;
+    if (!xb && !yb) binary_x4<float, float><<<grid, kThreads, 0, s>>>(op, o, (const float*)ins[0], (const float*)ins[1], al, n / 4);
+    else if (!xb) binary_x4<float, bf16><<<grid, kThreads, 0, s>>>(op, o, (const float*)ins[0], (const bf16*)ins[1], al, n / 4);
+    else if (!yb) binary_x4<bf16, float><<<grid, kThreads, 0, s>>>(op, o, (const bf16*)ins[0], (const float*)ins[1], al, n / 4);
+    else binary_x4<bf16, bf16><<<grid, kThreads, 0, s>>>(op, o, (const bf16*)ins[0], (const bf16*)ins[1], al, n / 4);
     return check_launch("mi355x_map");
   }
   MapArgs a{};

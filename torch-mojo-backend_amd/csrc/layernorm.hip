@@ -21,7 +21,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kMaxBwdBlocks = 256;
+constexpr int kMaxBwdBlocks = 1024;
 
 template <typename T, int NV>
 __global__ void __launch_bounds__(kThreads)
@@ -132,31 +132,22 @@ __global__ void __launch_bounds__(kThreads)
   const float inv_n = 1.f / (float)cols;
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
   const int64_t r1 = min(rows, r0 + rows_per_block);
-  for (int64_t row = r0 + wid; row < r1; row += kWaves) {
+  // One row's dx and its contribution to this lane's dgamma/dbeta columns.
+  auto process = [&](int64_t row, const float (&xv)[NV][4], const float (&dv)[NV][4]) {
     const float mu = mean[row], rs = rstd[row];
     float xh[NV][4], gy[NV][4];
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int c = (j * 64 + lane) * 4;
-      if (c < cols) {
-        float xv[4], dv[4];
-        Vec4<T>::load(x + row * cols + c, xv);
-        Vec4<T>::load(dy + row * cols + c, dv);
+    for (int j = 0; j < NV; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          xh[j][e] = (xv[e] - mu) * rs;
-          gy[j][e] = dv[e] * gm[j][e];
-          s1 += gy[j][e];
-          s2 += gy[j][e] * xh[j][e];
-          pg[j][e] += dv[e] * xh[j][e];
-          pb[j][e] += dv[e];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xh[j][e] = gy[j][e] = 0.f;
+      for (int e = 0; e < 4; ++e) {
+        xh[j][e] = (xv[j][e] - mu) * rs;
+        gy[j][e] = dv[j][e] * gm[j][e];
+        s1 += gy[j][e];
+        s2 += gy[j][e] * xh[j][e];
+        pg[j][e] += dv[j][e] * xh[j][e];
+        pb[j][e] += dv[j][e];
       }
-    }
     if (dx) {
       const float m1 = wave_sum(s1) * inv_n;
       const float m2 = wave_sum(s2) * inv_n;
@@ -171,6 +162,28 @@ __global__ void __launch_bounds__(kThreads)
         }
       }
     }
+  };
+  auto load = [&](int64_t row, float (&xv)[NV][4], float (&dv)[NV][4]) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (j * 64 + lane) * 4;
+      if (c < cols) {
+        Vec4<T>::load(x + row * cols + c, xv[j]);
+        Vec4<T>::load(dy + row * cols + c, dv[j]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[j][e] = dv[j][e] = 0.f;
+      }
+    }
+  };
+  // Two rows per iteration, both rows' loads issued before either is used.
+  for (int64_t row = r0 + wid; row < r1; row += 2 * kWaves) {
+    const int64_t row2 = row + kWaves;
+    float xa[NV][4], da[NV][4], xb[NV][4], db[NV][4];
+    load(row, xa, da);
+    if (row2 < r1) load(row2, xb, db);
+    process(row, xa, da);
+    if (row2 < r1) process(row2, xb, db);
   }
   if (!want_params) return;
 #pragma unroll
@@ -236,27 +249,35 @@ __global__ void __launch_bounds__(kThreads)
   part_b[(int64_t)blockIdx.y * cols + c] = b;
 }
 
-// dgamma/dbeta = sum of the block partials: 64 columns x 4 partial lanes
-// per block, combined through LDS in a fixed order.
+// dgamma/dbeta = sum of the block partials: 16 columns x 16 partial lanes
+// per block, each lane keeping four independent sums (partials lane + 16u,
+// u = 0..3, then every 64th) so several loads are in flight; lanes and sums
+// are combined in a fixed order, so the result is deterministic.
 template <typename T>
 __global__ void __launch_bounds__(kThreads)
     ln_bwd_params_final(T* __restrict__ dgamma, T* __restrict__ dbeta,
                         const float* __restrict__ part_g, const float* __restrict__ part_b,
                         int nparts, int64_t cols) {
-  __shared__ float lg[4][64], lb[4][64];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int64_t c = (int64_t)blockIdx.x * 64 + tx;
-  float g = 0.f, b = 0.f;
+  __shared__ float lg[16][17], lb[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t c = (int64_t)blockIdx.x * 16 + tx;
+  float g[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
   if (c < cols)
-    for (int p = ty; p < nparts; p += 4) g += part_g[(int64_t)p * cols + c], b += part_b[(int64_t)p * cols + c];
-  lg[ty][tx] = g;
-  lb[ty][tx] = b;
+    for (int p = ty; p < nparts; p += 64) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int q = p + 16 * u;
+        if (q < nparts) g[u] += part_g[(int64_t)q * cols + c], b[u] += part_b[(int64_t)q * cols + c];
+      }
+    }
+  lg[ty][tx] = (g[0] + g[1]) + (g[2] + g[3]);
+  lb[ty][tx] = (b[0] + b[1]) + (b[2] + b[3]);
   __syncthreads();
   if (ty == 0 && c < cols) {
-    g = (lg[0][tx] + lg[1][tx]) + (lg[2][tx] + lg[3][tx]);
-    b = (lb[0][tx] + lb[1][tx]) + (lb[2][tx] + lb[3][tx]);
-    if (dgamma) dgamma[c] = from_f32<T>(g);
-    if (dbeta) dbeta[c] = from_f32<T>(b);
+    float sg = 0.f, sb = 0.f;
+    for (int w = 0; w < 16; ++w) sg += lg[w][tx], sb += lb[w][tx];
+    if (dgamma) dgamma[c] = from_f32<T>(sg);
+    if (dbeta) dbeta[c] = from_f32<T>(sb);
   }
 }
 
@@ -330,7 +351,7 @@ int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* m
     }
   }
   if (params)
-    ln_bwd_params_final<T><<<ceil_div(cols, 64), kThreads, 0, s>>>(dgamma, dbeta, pg, pb, nb, cols);
+    ln_bwd_params_final<T><<<ceil_div(cols, 16), kThreads, 0, s>>>(dgamma, dbeta, pg, pb, nb, cols);
   return check_launch("mi355x_layer_norm_bwd");
 }
 

@@ -206,6 +206,24 @@ __global__ void __launch_bounds__(kThreads) colsum8(RedArgs a) {
   }
 }
 
+// Sum colsum8's per-split partials [splits][inner]: 32 columns x 8 split
+// lanes per block; lane l adds splits l, l+8, ... and the lanes are combined
+// in a fixed order, so the result does not depend on scheduling.
+__global__ void __launch_bounds__(kThreads) colsum_combine(RedArgs a, int splits) {
+  __shared__ float red[8][33];
+  const int cx = threadIdx.x & 31, sl = threadIdx.x >> 5;
+  const int64_t c = (int64_t)blockIdx.x * 32 + cx;
+  float t = 0.f;
+  if (c < a.inner)
+    for (int sp = sl; sp < splits; sp += 8) t += ((const float*)a.part)[(int64_t)sp * a.inner + c];
+  red[sl][cx] = t;
+  __syncthreads();
+  if (sl == 0 && c < a.inner) {
+    for (int w = 1; w < 8; ++w) t += red[w][cx];
+    store_as<float>(a.out, a.out_dt, c, t);
+  }
+}
+
 template <typename A>
 __global__ void __launch_bounds__(kThreads) reduce_combine(RedArgs a, int splits) {
   const RedOp<A> R{a.op};
@@ -236,6 +254,21 @@ void plan(int64_t outer, int64_t r, int64_t inner, int* splits, int64_t* chunk) 
     if (s > max_s) s = max_s;
     if (s > 1024) s = 1024;
   }
+  if (s < 1) s = 1;
+  int64_t c = (r + s - 1) / s;
+  if (c < 1) c = 1;
+  *splits = (int)((r + c - 1) / c);
+  if (*splits < 1) *splits = 1;
+  *chunk = c;
+}
+
+// Dense column sums: about 1024 blocks of 256 columns x (chunk) rows, at
+// least 32 rows per block.
+void colsum_plan(int64_t r, int64_t inner, int* splits, int64_t* chunk) {
+  const int64_t gx = (inner + 255) / 256;
+  int64_t s = (1024 + gx - 1) / gx;
+  const int64_t max_s = (r + 31) / 32;
+  if (s > max_s) s = max_s;
   if (s < 1) s = 1;
   int64_t c = (r + s - 1) / s;
   if (c < 1) c = 1;
@@ -331,8 +364,12 @@ extern "C" int64_t mi355x_reduce_workspace_bytes(int64_t outer, int64_t r, int64
   int splits;
   int64_t chunk;
   plan(outer, r, inner, &splits, &chunk);
-  if (splits <= 1) return 0;
-  return (int64_t)splits * outer * inner * 8;
+  int64_t need = splits <= 1 ? 0 : (int64_t)splits * outer * inner * 8;
+  if (outer == 1 && inner > 1) {  // the dense column-sum path may split further
+    colsum_plan(r, inner, &splits, &chunk);
+    if (splits > 1 && (int64_t)splits * inner * 4 > need) need = (int64_t)splits * inner * 4;
+  }
+  return need;
 }
 
 extern "C" int mi355x_reduce(int op, void* out, int out_dtype, const void* in, int in_dtype,
@@ -354,21 +391,25 @@ extern "C" int mi355x_reduce(int op, void* out, int out_dtype, const void* in, i
   }
   RedArgs a{op, in, in_dtype, out, out_dtype, workspace, outer, r, inner, s_o, s_r, s_i, chunk};
   hipStream_t s = (hipStream_t)stream;
-  // Dense column sums (bias gradients): vectorised kernel, same split plan.
-  const size_t es = dtype_size(in_dtype);
+  // Dense column sums (bias gradients): vectorised kernel, own split plan.
   if (op == MI355X_RED_SUM && outer == 1 && inner > 1 && inner % 8 == 0 && s_i == 1 &&
       s_r == inner && ((uintptr_t)in % 16) == 0 &&
       (in_dtype == MI355X_F32 || in_dtype == MI355X_BF16 || in_dtype == MI355X_F16)) {
-    (void)es;
-    if (splits <= 1) a.part = nullptr;
+    colsum_plan(r, inner, &splits, &chunk);
+    a.chunk = chunk;
+    if (splits > 1) {
+      const int64_t need = mi355x_reduce_workspace_bytes(outer, r, inner);
+      if (!workspace || ws_bytes < need)
+        return fail(MI355X_EWORKSPACE, "mi355x_reduce: workspace %lld < %lld", (long long)ws_bytes,
+                    (long long)need);
+    } else {
+      a.part = nullptr;
+    }
     dim3 grid(ceil_div(inner, 256), splits);
     if (in_dtype == MI355X_F32) colsum8<float><<<grid, kThreads, 0, s>>>(a);
     else if (in_dtype == MI355X_BF16) colsum8<bf16><<<grid, kThreads, 0, s>>>(a);
     else colsum8<f16><<<grid, kThreads, 0, s>>>(a);
-    if (splits > 1) {
-      int64_t g = (inner + kThreads - 1) / kThreads;
-      reduce_combine<float><<<(unsigned)g, kThreads, 0, s>>>(a, splits);
-    }
+    if (splits > 1) colsum_combine<<<ceil_div(inner, 32), kThreads, 0, s>>>(a, splits);
     return check_launch("mi355x_reduce");
   }
   switch (acc_kind(op, in_dtype)) {
