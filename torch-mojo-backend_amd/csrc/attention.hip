@@ -103,10 +103,49 @@ __device__ __forceinline__ typename Mfma<T>::frag perm_frag(const T* tr, int row
   return f;
 }
 
+// XCD-aware block coordinates over a (tiles, H, B) grid: the hardware deals
+// workgroups to the 8 XCDs round-robin by linear id, so the ids are
+// renumbered to give each XCD a contiguous range of (b, h) pairs; all tiles
+// of one pair then share one L2 and its K/V (or Q/dO) are fetched from HBM
+// once instead of once per XCD.
+struct BlockCoord {
+  int64_t x, h, b;
+};
+__device__ __forceinline__ BlockCoord block_coord() {
+  const uint32_t nx = gridDim.x, ny = gridDim.y, n = nx * ny * gridDim.z;
+  uint32_t l = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+  if ((n & 7) == 0) l = (l & 7) * (n >> 3) + (l >> 3);
+  BlockCoord c;
+  c.x = l % nx;
+  const uint32_t r = l / nx;
+  c.h = r % ny;
+  c.b = r / ny;
+  return c;
+}
+
+// Reductions over the four 16-lane groups of a wave (the key rows of an
+// S^T tile): v_permlane16_swap / v_permlane32_swap with both operands = x
+// leave x's partner row (lane +-16, then +-32) in the second result.
+__device__ __forceinline__ float group_max(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float group_sum(float x) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// 2^x on the transcendental unit (results below 2^-126 flush to zero, which
+// softmax weights never miss).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool POS>
 __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnArgs p) {
   typedef typename Mfma<T>::frag frag;
   constexpr int KS = D / 32;  // MFMA k-steps over the head dim
@@ -116,9 +155,10 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnArgs p) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const BlockCoord bc = block_coord();
+  const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
   const int64_t q0 = qblock * 128;
-  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t b = bc.b, h = bc.h;
   const T* Q = (const T*)p.q + b * p.q_b + h * p.q_h;
   const T* K = (const T*)p.k + b * p.k_b + h * p.k_h;
   const T* V = (const T*)p.v + b * p.v_b + h * p.v_h;
@@ -159,46 +199,52 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnArgs p) {
         s[kt][qt] = a;
       }
     }
-    // masking + online softmax (per query = per lane column)
+    // Online softmax in the exp2 domain.  With a positive scale the row max
+    // is taken on the raw scores and p = 2^(s*c - m) is one FMA + one exp;
+    // each lane keeps a partial row sum (its 16 keys per tile) under the
+    // shared max, summed across the four lane groups once at the end.  O is
+    // rescaled only when some row's max grew.
     const bool need_mask = (kb0 + 64 > p.Skv) || (p.causal && kb0 + 64 > q0 + wave * 32);
+    const float c = p.scale_log2;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+      int lim = 63;  // keys kb0 + 0..lim are visible to this lane's query
+      if (need_mask) {
+        const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+        int64_t lm = p.Skv - 1 - kb0;
+        if (p.causal && qi - kb0 < lm) lm = qi - kb0;
+        lim = (int)max((int64_t)-1, min((int64_t)63, lm));
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = s[kt][qt][e] * p.scale_log2;
-          if (need_mask) {
-            const int64_t kj = kb0 + kt * 16 + lg * 4 + e;
-            if (kj >= p.Skv || (p.causal && kj > qi)) v = -INFINITY;
-          }
+          float v = POS ? s[kt][qt][e] : s[kt][qt][e] * c;
+          if (need_mask && kt * 16 + lg * 4 + e > lim) v = -INFINITY;
           s[kt][qt][e] = v;
           mx = fmaxf(mx, v);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m[qt], mx);
+      mx = group_max(mx);
+      const float m_new = fmaxf(m[qt], POS ? mx * c : mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m[qt] - m_use);
       float rs = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pv = exp2f(s[kt][qt][e] - m_use);
+          const float pv = fast_exp2(POS ? fmaf(s[kt][qt][e], c, -m_use) : s[kt][qt][e] - m_use);
           s[kt][qt][e] = pv;
           rs += pv;
         }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
+      const float alpha = fast_exp2(m[qt] - m_use);
       l[qt] = l[qt] * alpha + rs;
       m[qt] = m_new;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
+      }
     }
-    // O^T += V^T P^T over two 32-key k-steps
 #pragma unroll
     for (int ks2 = 0; ks2 < 2; ++ks2) {
       frag pf[2];
@@ -220,6 +266,8 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnArgs p) {
 
   // epilogue: lane holds O[query lr][d = dt*16 + 4*lg + e]
   T* O = (T*)p.o + b * p.o_b + h * p.o_h;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) l[qt] = group_sum(l[qt]);
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
@@ -307,7 +355,7 @@ __device__ __forceinline__ typename Mfma<T>::frag tr_frag(const char* tile, int 
   return f;
 }
 
-template <typename T, int D>
+template <typename T, int D, bool POS>
 __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_fwd_v2(AttnArgs p) {
   typedef typename Mfma<T>::frag frag;
   typedef KvLayout<D> L;
@@ -317,9 +365,10 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_fwd_v2(AttnArg
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const BlockCoord bc = block_coord();
+  const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
   const int64_t q0 = qblock * 128;
-  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t b = bc.b, h = bc.h;
   const T* Q = (const T*)p.q + b * p.q_b + h * p.q_h;
   const char* K = (const char*)((const T*)p.k + b * p.k_b + h * p.k_h);
   const char* V = (const char*)((const T*)p.v + b * p.v_b + h * p.v_h);
@@ -370,43 +419,51 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_fwd_v2(AttnArg
         s[kt][qt] = a;
       }
     }
+    // Online softmax in the exp2 domain.  With a positive scale the row max
+    // is taken on the raw scores and p = 2^(s*c - m) is one FMA + one exp;
+    // each lane keeps a partial row sum (its 16 keys per tile) under the
+    // shared max, summed across the four lane groups once at the end.  O is
+    // rescaled only when some row's max grew.
     const bool need_mask = (kb0 + 64 > p.Skv) || (p.causal && kb0 + 64 > q0 + wave * 32);
+    const float c = p.scale_log2;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+      int lim = 63;  // keys kb0 + 0..lim are visible to this lane's query
+      if (need_mask) {
+        const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+        int64_t lm = p.Skv - 1 - kb0;
+        if (p.causal && qi - kb0 < lm) lm = qi - kb0;
+        lim = (int)max((int64_t)-1, min((int64_t)63, lm));
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = s[kt][qt][e] * p.scale_log2;
-          if (need_mask) {
-            const int64_t kj = kb0 + kt * 16 + lg * 4 + e;
-            if (kj >= p.Skv || (p.causal && kj > qi)) v = -INFINITY;
-          }
+          float v = POS ? s[kt][qt][e] : s[kt][qt][e] * c;
+          if (need_mask && kt * 16 + lg * 4 + e > lim) v = -INFINITY;
           s[kt][qt][e] = v;
           mx = fmaxf(mx, v);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m[qt], mx);
+      mx = group_max(mx);
+      const float m_new = fmaxf(m[qt], POS ? mx * c : mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m[qt] - m_use);
       float rs = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pv = exp2f(s[kt][qt][e] - m_use);
+          const float pv = fast_exp2(POS ? fmaf(s[kt][qt][e], c, -m_use) : s[kt][qt][e] - m_use);
           s[kt][qt][e] = pv;
           rs += pv;
         }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
+      const float alpha = fast_exp2(m[qt] - m_use);
       l[qt] = l[qt] * alpha + rs;
       m[qt] = m_new;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
+      }
     }
 #pragma unroll
     for (int ks2 = 0; ks2 < 2; ++ks2) {
@@ -429,6 +486,8 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_fwd_v2(AttnArg
   }
 
   T* O = (T*)p.o + b * p.o_b + h * p.o_h;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) l[qt] = group_sum(l[qt]);
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
@@ -488,8 +547,9 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dkv(AttnBwdArgs p) {
   const AttnArgs& f = p.f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int64_t k0 = (int64_t)blockIdx.x * 64;
-  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const BlockCoord bc = block_coord();
+  const int64_t k0 = bc.x * 64;
+  const int64_t b = bc.b, h = bc.h;
   const T* Q = (const T*)f.q + b * f.q_b + h * f.q_h;
   const T* K = (const T*)f.k + b * f.k_b + h * f.k_h;
   const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
@@ -589,9 +649,10 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dq(AttnBwdArgs p) {
   const AttnArgs& f = p.f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const BlockCoord bc = block_coord();
+  const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
   const int64_t q0 = qblock * 64;
-  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t b = bc.b, h = bc.h;
   const T* Q = (const T*)f.q + b * f.q_b + h * f.q_h;
   const T* K = (const T*)f.k + b * f.k_b + h * f.k_h;
   const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
@@ -687,8 +748,9 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
   const AttnArgs& f = p.f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int64_t k0 = (int64_t)blockIdx.x * 128;
-  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const BlockCoord bc = block_coord();
+  const int64_t k0 = bc.x * 128;
+  const int64_t b = bc.b, h = bc.h;
   const char* Q = (const char*)((const T*)f.q + b * f.q_b + h * f.q_h);
   const T* K = (const T*)f.k + b * f.k_b + h * f.k_h;
   const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
@@ -827,9 +889,10 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
   const AttnArgs& f = p.f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
-  const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const BlockCoord bc = block_coord();
+  const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
   const int64_t q0 = qblock * 128;
-  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t b = bc.b, h = bc.h;
   const T* Q = (const T*)f.q + b * f.q_b + h * f.q_h;
   const char* K = (const char*)((const T*)f.k + b * f.k_b + h * f.k_h);
   const char* V = (const char*)((const T*)f.v + b * f.v_b + h * f.v_h);
@@ -955,8 +1018,12 @@ int check_common(int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D, int d
 template <typename T, int D>
 int fwd_launch(const AttnArgs& a, hipStream_t s) {
   dim3 grid(ceil_div(a.Sq, 128), (unsigned)a.H, (unsigned)a.B);
-  if constexpr (D == 64 || D == 128) attn_fwd_v2<T, D><<<grid, kThreads, 0, s>>>(a);
-  else attn_fwd_kernel<T, D><<<grid, kThreads, 0, s>>>(a);
+  if constexpr (D == 64 || D == 128) {
+    if (a.scale_log2 > 0.f) attn_fwd_v2<T, D, true><<<grid, kThreads, 0, s>>>(a);
+    else attn_fwd_v2<T, D, false><<<grid, kThreads, 0, s>>>(a);
+  }
+  else if (a.scale_log2 > 0.f) attn_fwd_kernel<T, D, true><<<grid, kThreads, 0, s>>>(a);
+  else attn_fwd_kernel<T, D, false><<<grid, kThreads, 0, s>>>(a);
   return check_launch("mi355x_attn_fwd");
 }
 
