@@ -517,22 +517,29 @@ struct AttnBwdArgs {
   float* delta;  // [B, H, Sq]
 };
 
-// D_i = sum_d dO[i, d] * O[i, d]; one wave per row.
+// D_i = sum_d dO[i, d] * O[i, d]: D/8 lanes per row, one 16-byte load of
+// each operand per lane, reduced across the row's lanes.
 template <typename T, int D>
 __global__ void __launch_bounds__(kThreads) attn_bwd_delta(AttnBwdArgs p) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // over B*H*Sq
+  constexpr int CPR = D / 8;              // lanes per row
+  constexpr int RPB = kThreads / CPR;     // rows per block
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / CPR;  // over B*H*Sq
+  const int ch = threadIdx.x % CPR;
   const int64_t total = p.f.B * p.f.H * p.f.Sq;
-  if (row >= total) return;
-  const int64_t i = row % p.f.Sq, bh = row / p.f.Sq;
-  const int64_t h = bh % p.f.H, b = bh / p.f.H;
-  const T* O = (const T*)p.f.o + b * p.f.o_b + h * p.f.o_h + i * p.f.o_s;
-  const T* dO = (const T*)p.dout + b * p.do_b + h * p.do_h + i * p.do_s;
   float acc = 0.f;
-  for (int d = lane; d < D; d += 64) acc += to_f32(O[d]) * to_f32(dO[d]);
-  acc = wave_sum(acc);
-  if (lane == 0) p.delta[row] = acc;
+  if (row < total) {
+    const int64_t i = row % p.f.Sq, bh = row / p.f.Sq;
+    const int64_t h = bh % p.f.H, b = bh / p.f.H;
+    const V8<T> o = *(const V8<T>*)((const T*)p.f.o + b * p.f.o_b + h * p.f.o_h + i * p.f.o_s + ch * 8);
+    const V8<T> d = *(const V8<T>*)((const T*)p.dout + b * p.do_b + h * p.do_h + i * p.do_s + ch * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += to_f32(o.v[e]) * to_f32(d.v[e]);
+  }
+#pragma unroll
+  for (int off = CPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (row < total && ch == 0) p.delta[row] = acc;
 }
+
 
 template <typename T, int D>
 __global__ void __launch_bounds__(kThreads) attn_bwd_dkv(AttnBwdArgs p) {
@@ -800,6 +807,13 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
     const float* del_s = lse_s + 64;
     buf ^= 1;
     if (f.causal && kw > qb0 + 63) continue;  // every key of this wave is after every query
+    // Masks only where the tile crosses the causal diagonal or an edge; then
+    // in 32-bit indices relative to the tile.
+    const bool need_mask = (qb0 + 64 > f.Sq) || (kw + 32 > f.Skv) || (f.causal && kw + 31 > qb0);
+    const int q_lim = (int)min((int64_t)64, f.Sq - qb0);   // query rows < q_lim exist
+    const int k_lim = (int)min((int64_t)32, f.Skv - kw);   // key rows < k_lim exist
+    const int kq = (int)max((int64_t)-128, min((int64_t)128, kw - qb0));  // key row 0 minus query row 0
+    const float c = f.scale_log2;
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       f32x4 pt[2][2], ds[2][2];  // [query tile in pair][key tile]
@@ -825,12 +839,14 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
             sa = Mfma<T>::mma(qa[ks], kf[t][ks], sa);
             pa = Mfma<T>::mma(da[ks], vf[t][ks], pa);
           }
-          const int64_t kj = kw + t * 16 + lr;
+          const int kr = t * 16 + lr;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int64_t qi = qb0 + qt * 16 + 4 * lg + e;
-            float pv = exp2f(sa[e] * f.scale_log2 - lv[e]);
-            if (qi >= f.Sq || kj >= f.Skv || (f.causal && kj > qi)) pv = 0.f;
+            float pv = fast_exp2(fmaf(sa[e], c, -lv[e]));
+            if (need_mask) {
+              const int qr = qt * 16 + 4 * lg + e;
+              if (qr >= q_lim || kr >= k_lim || (f.causal && kq + kr > qr)) pv = 0.f;
+            }
             pt[u][t][e] = pv;
             ds[u][t][e] = pv * (pa[e] - dv[e]);
           }
@@ -936,6 +952,11 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
     const char* Vt = Kt + L::TILE;
     buf ^= 1;
     if (f.causal && kb0 > qw + 31) continue;  // every key after every query of this wave
+    const bool need_mask = (kb0 + 64 > f.Skv) || (qw + 32 > f.Sq) || (f.causal && kb0 + 63 > qw);
+    const int q_lim = (int)min((int64_t)32, f.Sq - qw);    // query rows < q_lim exist
+    const int k_lim = (int)min((int64_t)64, f.Skv - kb0);  // key rows < k_lim exist
+    const int qk = (int)max((int64_t)-128, min((int64_t)128, qw - kb0));  // query row 0 minus key row 0
+    const float c = f.scale_log2;
 #pragma unroll
     for (int ks2 = 0; ks2 < 2; ++ks2) {
       f32x4 ds[2][2];  // [key tile in pair][query tile]
@@ -957,12 +978,14 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
             sa = Mfma<T>::mma(ka[ks], qf[u][ks], sa);
             pa = Mfma<T>::mma(va[ks], df[u][ks], pa);
           }
-          const int64_t qi = qw + u * 16 + lr;
+          const int qr = u * 16 + lr;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int64_t kj = kb0 + kt * 16 + 4 * lg + e;
-            float pv = exp2f(sa[e] * f.scale_log2 - lse2[u]);
-            if (qi >= f.Sq || kj >= f.Skv || (f.causal && kj > qi)) pv = 0.f;
+            float pv = fast_exp2(fmaf(sa[e], c, -lse2[u]));
+            if (need_mask) {
+              const int kr = kt * 16 + 4 * lg + e;
+              if (qr >= q_lim || kr >= k_lim || (f.causal && kr > qk + qr)) pv = 0.f;
+            }
             ds[v2][u][e] = pv * (pa[e] - dlt[u]);
           }
         }
@@ -1030,7 +1053,7 @@ int fwd_launch(const AttnArgs& a, hipStream_t s) {
 template <typename T, int D>
 int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
   const int64_t rows = a.f.B * a.f.H * a.f.Sq;
-  attn_bwd_delta<T, D><<<ceil_div(rows, 4), kThreads, 0, s>>>(a);
+  attn_bwd_delta<T, D><<<ceil_div(rows, kThreads / (D / 8)), kThreads, 0, s>>>(a);
   if constexpr (D == 64 || D == 128) {
     dim3 gk(ceil_div(a.f.Skv, 128), (unsigned)a.f.H, (unsigned)a.f.B);
     attn_bwd_dkv_v2<T, D><<<gk, kThreads, 0, s>>>(a);
@@ -1096,8 +1119,8 @@ extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const 
   int rc = check_common(batch, heads, sq, skv, d, dtype);
   if (rc) return rc;
   MI_REQUIRE(strides_ok(q, q_bhs) && strides_ok(k, k_bhs) && strides_ok(v, v_bhs) &&
-                 strides_ok(dout, do_bhs),
-             "mi355x_attn_bwd: q/k/v/dout need 16-byte aligned bases and strides that are multiples of 8");
+                 strides_ok(dout, do_bhs) && strides_ok(o, o_bhs),
+             "mi355x_attn_bwd: q/k/v/o/dout need 16-byte aligned bases and strides that are multiples of 8");
   for (const int64_t* s : {dq_bhs, dk_bhs, dv_bhs})
     MI_REQUIRE(s[0] % 4 == 0 && s[1] % 4 == 0 && s[2] % 4 == 0, "mi355x_attn_bwd: grads need 8-byte aligned rows");
   const int64_t need = mi355x_attn_bwd_workspace_bytes(batch, heads, sq, skv, d);
