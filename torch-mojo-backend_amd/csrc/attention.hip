@@ -103,23 +103,35 @@ __device__ __forceinline__ typename Mfma<T>::frag perm_frag(const T* tr, int row
   return f;
 }
 
-// XCD-aware block coordinates over a (tiles, H, B) grid: the hardware deals
-// workgroups to the 8 XCDs round-robin by linear id, so the ids are
-// renumbered to give each XCD a contiguous range of (b, h) pairs; all tiles
-// of one pair then share one L2 and its K/V (or Q/dO) are fetched from HBM
-// once instead of once per XCD.
+// XCD-aware, heaviest-first block coordinates over a (tiles, H, B) grid.
+// The hardware deals workgroups to the 8 XCDs round-robin by linear id, so
+// ids are renumbered to give each XCD a contiguous range of (b, h) pairs:
+// all tiles of one pair share one L2, and its K/V (or Q/dO) come from HBM
+// once instead of once per XCD.  Inside an XCD's range the tile index
+// varies slowest, so the heaviest causal tiles (tile 0 after the kernels'
+// own reversal for query tiles; key tile 0 for dK/dV) of all its pairs are
+// dispatched first and spread over the CUs, and the light ones fill in
+// behind them instead of several heavy tiles landing on one CU.
 struct BlockCoord {
   int64_t x, h, b;
 };
 __device__ __forceinline__ BlockCoord block_coord() {
   const uint32_t nx = gridDim.x, ny = gridDim.y, n = nx * ny * gridDim.z;
-  uint32_t l = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
-  if ((n & 7) == 0) l = (l & 7) * (n >> 3) + (l >> 3);
+  const uint32_t l = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
   BlockCoord c;
-  c.x = l % nx;
-  const uint32_t r = l / nx;
-  c.h = r % ny;
-  c.b = r / ny;
+  if ((n & 7) == 0 && ((n >> 3) % nx) == 0) {
+    const uint32_t pairs = (n >> 3) / nx;  // (b, h) pairs per XCD
+    const uint32_t i = l >> 3;
+    c.x = i / pairs;
+    const uint32_t pair = (l & 7) * pairs + (i - (uint32_t)c.x * pairs);
+    c.h = pair % ny;
+    c.b = pair / ny;
+  } else {
+    c.x = l % nx;
+    const uint32_t r = l / nx;
+    c.h = r % ny;
+    c.b = r / ny;
+  }
   return c;
 }
 
