@@ -321,8 +321,15 @@ struct KvLayout {
   static constexpr int CH = D / 8;            // 16-byte chunks per row
   static constexpr int TILE = 64 * ROWB;      // one 64-row tile
   static constexpr int RPI = 1024 / ROWB;     // rows per 1 KB load instruction
+  // Chunk swizzle of row r, chosen from LDS bank-conflict counter
+  // measurements of the two read patterns: 16-byte fragment reads (16
+  // consecutive rows at one chunk) and ds_read_b64_tr_b16 reads (rows
+  // 4g + j, adjacent chunks c, c ^ 1).  Both run without bank conflicts.
+  //   D = 64 (128-byte rows):  r & 7
+  //   D = 128 (256-byte rows): bit 0 = r3, bits 1-2 = r0-r1, bit 3 = r2 ^ r3
   static __device__ __forceinline__ int swz(int row) {
-    return D == 64 ? ((row >> 1) & 7) : (row & 15);
+    return D == 64 ? (row & 7)
+                   : (((row >> 3) & 1) | ((row & 3) << 1) | ((((row >> 2) ^ (row >> 3)) & 1) << 3));
   }
   // byte offset of element (row, col) in a swizzled tile
   static __device__ __forceinline__ int off(int row, int col) {

@@ -136,9 +136,11 @@ struct TileLoad {
 };
 
 // m/n-contiguous operand tile: 64 k-rows of ROWS elements, 16-byte chunks
-// XOR-swizzled by s(k) = (k & 3) | ((k >> 1) & 12), a bijection on the 16
-// k-rows one transposing fragment read touches.
-__device__ __forceinline__ int kswz(int k) { return (k & 3) | ((k >> 1) & 12); }
+// XOR-swizzled by s(k) = 2 * ((k & 3) | ((k >> 1) & 4)).  A transposing
+// fragment read serves each half-wave from 8 k-rows x 2 adjacent chunks
+// (c, c ^ 1); s takes 8 distinct even values on those k-rows, so the 16
+// (k-row, chunk) pairs land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int kswz(int k) { return 2 * ((k & 3) | ((k >> 1) & 4)); }
 
 template <int ROWS, int NT>
 struct TileLoadT {
