@@ -17,9 +17,11 @@
 // A lane's global source address is chosen so that its fixed LDS slot
 // receives the swizzled chunk, so staging costs no registers.
 //
-// Two block configurations (waves arranged WGM x WGN, each wave owning a
+// Three block configurations (waves arranged WGM x WGN, each wave owning a
 // (BM/WGM) x (BN/WGN) sub-tile of 16x16 MFMA tiles):
 //   C128: 128x128, 4 waves of 64x64, 64 KB LDS, two blocks per CU;
+//   C192: 128x192, 4 waves of 64x96, 80 KB LDS, two blocks per CU (B
+//         k-contiguous only); N = 768, 2304, 3072 split into whole rounds;
 //   C256: 256x256, 8 waves of 128x64, 128 KB LDS, one block per CU (fewer
 //         LDS bytes per flop; preferred when its tiles fill the CUs evenly).
 // The block -> tile map is XCD-aware (the hardware deals workgroups to the 8
@@ -249,6 +251,10 @@ struct TileCfg<0> {  // C128
 template <>
 struct TileCfg<1> {  // C256
   static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 4, MIN_BLOCKS = 1;
+};
+template <>
+struct TileCfg<2> {  // C192: 128x192, waves of 64x96, 80 KB LDS, two blocks per CU (k-contiguous B only)
+  static constexpr int BM = 128, BN = 192, WGM = 2, WGN = 2, MIN_BLOCKS = 2;
 };
 
 // Write one wave's accumulators to C (pointing at the wave tile's first
@@ -487,14 +493,14 @@ __global__ void __launch_bounds__(256) gemm_f32(GemmArgs g) {
 // planning
 // ---------------------------------------------------------------------------
 struct Plan {
-  int cfg;  // 0 = C128, 1 = C256
+  int cfg;  // 0 = C128, 1 = C256, 2 = C192
   int splits;
   int64_t kchunk;
 };
 
 int64_t tiles_of(int cfg, int64_t batch, int64_t m, int64_t n) {
-  const int64_t t = cfg ? 256 : 128;
-  return ((m + t - 1) / t) * ((n + t - 1) / t) * batch;
+  const int64_t bm = cfg == 1 ? 256 : 128, bn = cfg == 1 ? 256 : (cfg == 2 ? 192 : 128);
+  return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch;
 }
 
 // Pick the configuration that finishes in the least time: whole rounds of
@@ -502,17 +508,26 @@ int64_t tiles_of(int cfg, int64_t batch, int64_t m, int64_t n) {
 // per-round time measured on gfx950 at K = 768..3072 (a C256 round does
 // twice a C128 round's work in 1.82x its time).  Then split K when the
 // output alone cannot fill the chip.
-Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k) {
+Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool b_kcontig) {
   Plan best{0, 1, k};
-  const int64_t t128 = tiles_of(0, batch, m, n), t256 = tiles_of(1, batch, m, n);
+  const int64_t t128 = tiles_of(0, batch, m, n), t256 = tiles_of(1, batch, m, n), t192 = tiles_of(2, batch, m, n);
   const double c128 = (double)((t128 + 2 * kCUs - 1) / (2 * kCUs));
   const double c256 = 1.82 * (double)((t256 + kCUs - 1) / kCUs);
-  if (t256 >= kCUs && c256 < c128) best.cfg = 1;
-  static const char* forced = getenv("MI355X_GEMM_TILE");  // tuning override: "128" or "256"
-  if (forced) best.cfg = atoi(forced) == 256 ? 1 : 0;
+  const double c192 = 1.5 * (double)((t192 + 2 * kCUs - 1) / (2 * kCUs));
+  double cbest = c128;
+  if (t256 >= kCUs && c256 < cbest) best.cfg = 1, cbest = c256;
+  if (b_kcontig && t192 >= kCUs && c192 < cbest) best.cfg = 2, cbest = c192;
+  static const char* forced = getenv("MI355X_GEMM_TILE");  // tuning override: "128", "192" or "256"
+  if (forced) {
+    const int f = atoi(forced);
+    best.cfg = f == 256 ? 1 : (f == 192 && b_kcontig ? 2 : 0);
+  }
   const int64_t tiles = tiles_of(best.cfg, batch, m, n);
   if (tiles < kCUs && k >= 2048) {
-    int64_t s = (2 * kCUs + tiles - 1) / tiles;
+    // as many K splits as keep every block in the first round of block
+    // slots: a second, partly filled round would double the time
+    const int64_t slots = best.cfg == 1 ? kCUs : 2 * kCUs;  // block slots of the chosen config
+    int64_t s = slots / tiles;
     const int64_t max_s = k / 512;
     if (s > max_s) s = max_s;
     if (s > 64) s = 64;
@@ -526,31 +541,42 @@ Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k) {
   return best;
 }
 
+// Launch one kernel instantiation; the first launch of each opts it into
+// more than 64 KB of dynamic LDS when it needs that.
+template <typename T, int CFG, bool A_K, bool B_K, bool KT>
+int launch_kernel(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  typedef TileCfg<CFG> C;
+  constexpr int NT = 64 * C::WGM * C::WGN;
+  constexpr size_t lds = 2 * (size_t)(C::BM + C::BN) * 128;
+  static bool attr = false;
+  if (lds > 65536 && !attr) {
+    if (hipFuncSetAttribute((const void*)gemm_tile<T, CFG, A_K, B_K, KT>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+      return fail(MI355X_ELAUNCH, "mi355x_gemm: cannot reserve %zu bytes of LDS", lds);
+    attr = true;
+  }
+  gemm_tile<T, CFG, A_K, B_K, KT><<<grid, NT, lds, s>>>(g);
+  return check_launch("mi355x_gemm");
+}
+
 template <typename T, int CFG, bool KT>
 int launch_tile(GemmArgs g, int64_t batch, int splits, hipStream_t s) {
   typedef TileCfg<CFG> C;
-  constexpr int NT = 64 * C::WGM * C::WGN;
   const int tm = (int)ceil_div(g.m, C::BM), tn = (int)ceil_div(g.n, C::BN);
   g.tiles_n = tn;
   g.batch = (int)batch;
   dim3 grid((unsigned)(tm * tn), (unsigned)(batch * splits));
-  const size_t lds = 2 * (size_t)(C::BM + C::BN) * 128;
   const bool ak = g.a_cs == 1, bk = g.b_rs == 1;
-  auto go = [&](auto kern) {
-    static bool attr = false;  // one-time opt-in to more than 64 KB of dynamic LDS
-    if (!attr && lds > 65536) {
-      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-          hipSuccess)
-        return fail(MI355X_ELAUNCH, "mi355x_gemm: cannot reserve %zu bytes of LDS", lds);
-      attr = true;
-    }
-    kern<<<grid, NT, lds, s>>>(g);
-    return check_launch("mi355x_gemm");
-  };
-  if (ak && bk) return go(gemm_tile<T, CFG, true, true, KT>);
-  if (ak) return go(gemm_tile<T, CFG, true, false, KT>);
-  if (bk) return go(gemm_tile<T, CFG, false, true, KT>);
-  return go(gemm_tile<T, CFG, false, false, KT>);
+  if constexpr (CFG == 2) {  // 192-wide B tiles are only loaded k-contiguous
+    if (!bk) return fail(MI355X_EINVAL, "mi355x_gemm: 128x192 tiles need a k-contiguous B");
+    if (ak) return launch_kernel<T, CFG, true, true, KT>(g, grid, s);
+    return launch_kernel<T, CFG, false, true, KT>(g, grid, s);
+  } else {
+    if (ak && bk) return launch_kernel<T, CFG, true, true, KT>(g, grid, s);
+    if (ak) return launch_kernel<T, CFG, true, false, KT>(g, grid, s);
+    if (bk) return launch_kernel<T, CFG, false, true, KT>(g, grid, s);
+    return launch_kernel<T, CFG, false, false, KT>(g, grid, s);
+  }
 }
 
 int splitk_finish(const GemmArgs& g, int64_t batch, int splits, hipStream_t s) {
@@ -566,6 +592,7 @@ int launch_mfma(GemmArgs g, int64_t batch, const Plan& p, hipStream_t s) {
   const bool kt = g.k % 64 != 0;
   int rc;
   if (p.cfg == 1) rc = kt ? launch_tile<T, 1, true>(g, batch, p.splits, s) : launch_tile<T, 1, false>(g, batch, p.splits, s);
+  else if (p.cfg == 2) rc = kt ? launch_tile<T, 2, true>(g, batch, p.splits, s) : launch_tile<T, 2, false>(g, batch, p.splits, s);
   else rc = kt ? launch_tile<T, 0, true>(g, batch, p.splits, s) : launch_tile<T, 0, false>(g, batch, p.splits, s);
   if (rc || !g.part) return rc;
   return splitk_finish(g, batch, p.splits, s);
@@ -605,7 +632,7 @@ WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int64_t k, const void* a
   w.pack_a = !in_place(a, a_rs, a_cs, a_bs, m) || (a_cs != 1 && (double)m < small_rows);
   // B as [n rows][k]: row stride b_cs, k stride b_rs
   w.pack_b = !in_place(b, b_cs, b_rs, b_bs, n) || (b_rs != 1 && (double)n < small_rows);
-  w.plan = plan_gemm(batch, m, n, k);
+  w.plan = plan_gemm(batch, m, n, k, w.pack_b || b_rs == 1);
   auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
   w.part_bytes = w.plan.splits > 1 ? up((int64_t)w.plan.splits * batch * m * n * 4) : 0;
   const int64_t ab = a_bs == 0 ? 1 : batch, bb = b_bs == 0 ? 1 : batch;
