@@ -127,3 +127,33 @@ def test_nanogpt_loss_curve_bf16_autocast_tracks_cpu_fixture(mojo):
     assert all(math.isfinite(v) for v in got)
     assert max(rel[:5]) <= 1e-3, max(enumerate(rel[:5]), key=lambda t: t[1])
     assert max(rel) <= 5e-2, max(enumerate(rel), key=lambda t: t[1])
+
+
+@pytest.mark.parametrize("shape,bias,strided", [((96, 200), True, False), ((3, 70, 200), True, False),
+                                                 ((3, 70, 200), False, True)])
+def test_fused_linear_under_autocast_gpu(mojo, shape, bias, strided):
+    """Autocast linear on the device (one fused autograd Function) against
+    torch CPU with autocast's rounding points (bf16 operands, f32
+    accumulation, bf16 results widened to f32 gradients)."""
+    from test_host_device import _linear_autocast_reference
+
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(*shape, generator=g)
+    if strided:
+        x = torch.randn(*shape[:-1], 232, generator=g)[..., 16:216]
+    w = torch.randn(136, 200, generator=g) * 0.1
+    b = torch.randn(136, generator=g) if bias else None
+    dy = torch.randn(*shape[:-1], 136, generator=g)
+    xm = x.to("mojo").requires_grad_()
+    wm = w.to("mojo").requires_grad_()
+    bm = b.to("mojo").requires_grad_() if bias else None
+    with torch.autocast("mojo", dtype=torch.bfloat16):
+        out = F.linear(xm, wm, bm)
+    assert type(out.grad_fn).__name__ == "_FusedLinearBackward"
+    out.backward(dy.bfloat16().to("mojo"))
+    eo, edx, edw, edb = _linear_autocast_reference(x, w, b, dy)
+    assert torch.allclose(out.float().cpu(), eo.float(), atol=2e-2, rtol=2e-2)
+    assert torch.allclose(xm.grad.cpu(), edx, atol=2e-2, rtol=2e-2)
+    assert torch.allclose(wm.grad.cpu(), edw, atol=5e-2, rtol=2e-2)
+    if bias:
+        assert torch.allclose(bm.grad.cpu(), edb, atol=5e-2, rtol=2e-2)

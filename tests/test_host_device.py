@@ -144,3 +144,46 @@ def test_missing_library_fails_loudly(tmp_path):
     env = {"MI355X_KERNELS_LIB": str(tmp_path / "absent.so"), "PATH": "/usr/bin:/bin"}
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
     assert "RAISED" in r.stdout and "build" in r.stdout, r.stdout + r.stderr
+
+
+def _linear_autocast_reference(x, w, b, dy):
+    """torch CPU f32 restatement of autocast linear: operands rounded to
+    bf16, f32 accumulation, output rounded to bf16; gradients computed from
+    the rounded operands, rounded to bf16, then widened to f32."""
+    xl, wl = x.bfloat16().float(), w.bfloat16().float()
+    out = xl @ wl.t()
+    if b is not None:
+        out = out + b.bfloat16().float()
+    out = out.bfloat16()
+    dyf = dy.bfloat16().float()
+    dx = (dyf @ wl).bfloat16().float()
+    dw = (dyf.reshape(-1, dyf.shape[-1]).t() @ xl.reshape(-1, xl.shape[-1])).bfloat16().float()
+    db = dyf.reshape(-1, dyf.shape[-1]).sum(0).bfloat16().float() if b is not None else None
+    return out, dx, dw, db
+
+
+@pytest.mark.parametrize("shape,bias,strided", [((6, 40), True, False), ((2, 5, 40), True, False),
+                                                 ((2, 5, 40), False, True)])
+def test_fused_linear_under_autocast(mojo, shape, bias, strided):
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(*shape, generator=g)
+    if strided:  # a [.., 40] slice of a wider buffer
+        x = torch.randn(*shape[:-1], 56, generator=g)[..., 8:48]
+    w = torch.randn(24, 40, generator=g) * 0.2
+    b = torch.randn(24, generator=g) if bias else None
+    dy = torch.randn(*shape[:-1], 24, generator=g)
+    xm = x.to("mojo").requires_grad_()
+    wm = w.to("mojo").requires_grad_()
+    bm = b.to("mojo").requires_grad_() if bias else None
+    with torch.autocast("mojo", dtype=torch.bfloat16):
+        out = F.linear(xm, wm, bm)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == tuple(shape[:-1]) + (24,)
+    assert type(out.grad_fn).__name__ == "_FusedLinearBackward"
+    out.backward(dy.bfloat16().to("mojo"))
+    eo, edx, edw, edb = _linear_autocast_reference(x, w, b, dy)
+    assert torch.allclose(out.float().cpu(), eo.float(), atol=2e-2, rtol=2e-2)
+    assert xm.grad.dtype == torch.float32 and wm.grad.dtype == torch.float32
+    assert torch.allclose(xm.grad.cpu(), edx, atol=2e-2, rtol=2e-2)
+    assert torch.allclose(wm.grad.cpu(), edw, atol=2e-2, rtol=2e-2)
+    if bias:
+        assert torch.allclose(bm.grad.cpu(), edb, atol=2e-2, rtol=2e-2)

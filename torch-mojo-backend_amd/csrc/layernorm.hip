@@ -249,36 +249,44 @@ __global__ void __launch_bounds__(kThreads)
   part_b[(int64_t)blockIdx.y * cols + c] = b;
 }
 
-// dgamma/dbeta = sum of the block partials: 16 columns x 16 partial lanes
-// per block, each lane keeping four independent sums (partials lane + 16u,
-// u = 0..3, then every 64th) so several loads are in flight; lanes and sums
-// are combined in a fixed order, so the result is deterministic.
-template <typename T>
+// dgamma/dbeta = sum of the block partials, in two fixed-order passes so
+// the result is deterministic and each pass has enough blocks in flight:
+//   mid:   group y of kGroups sums partials [y*per, (y+1)*per) for 64
+//          columns per block (4 lanes per column, combined through LDS);
+//   final: one thread per column sums the kGroups group sums in order.
+constexpr int kGroups = 16;
+
 __global__ void __launch_bounds__(kThreads)
-    ln_bwd_params_final(T* __restrict__ dgamma, T* __restrict__ dbeta,
-                        const float* __restrict__ part_g, const float* __restrict__ part_b,
-                        int nparts, int64_t cols) {
-  __shared__ float lg[16][17], lb[16][17];
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-  const int64_t c = (int64_t)blockIdx.x * 16 + tx;
-  float g[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+    ln_bwd_params_mid(float* __restrict__ mid_g, float* __restrict__ mid_b, const float* __restrict__ part_g,
+                      const float* __restrict__ part_b, int nparts, int64_t cols) {
+  __shared__ float lg[4][65], lb[4][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + tx;
+  const int per = (nparts + kGroups - 1) / kGroups;
+  const int p0 = blockIdx.y * per, p1 = min(nparts, p0 + per);
+  float g = 0.f, b = 0.f;
   if (c < cols)
-    for (int p = ty; p < nparts; p += 64) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int q = p + 16 * u;
-        if (q < nparts) g[u] += part_g[(int64_t)q * cols + c], b[u] += part_b[(int64_t)q * cols + c];
-      }
-    }
-  lg[ty][tx] = (g[0] + g[1]) + (g[2] + g[3]);
-  lb[ty][tx] = (b[0] + b[1]) + (b[2] + b[3]);
+    for (int q = p0 + ty; q < p1; q += 4) g += part_g[(int64_t)q * cols + c], b += part_b[(int64_t)q * cols + c];
+  lg[ty][tx] = g;
+  lb[ty][tx] = b;
   __syncthreads();
   if (ty == 0 && c < cols) {
-    float sg = 0.f, sb = 0.f;
-    for (int w = 0; w < 16; ++w) sg += lg[w][tx], sb += lb[w][tx];
-    if (dgamma) dgamma[c] = from_f32<T>(sg);
-    if (dbeta) dbeta[c] = from_f32<T>(sb);
+    mid_g[(int64_t)blockIdx.y * cols + c] = (lg[0][tx] + lg[1][tx]) + (lg[2][tx] + lg[3][tx]);
+    mid_b[(int64_t)blockIdx.y * cols + c] = (lb[0][tx] + lb[1][tx]) + (lb[2][tx] + lb[3][tx]);
   }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+    ln_bwd_params_final(T* __restrict__ dgamma, T* __restrict__ dbeta, const float* __restrict__ mid_g,
+                        const float* __restrict__ mid_b, int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= cols) return;
+  float g = 0.f, b = 0.f;
+#pragma unroll
+  for (int y = 0; y < kGroups; ++y) g += mid_g[(int64_t)y * cols + c], b += mid_b[(int64_t)y * cols + c];
+  if (dgamma) dgamma[c] = from_f32<T>(g);
+  if (dbeta) dbeta[c] = from_f32<T>(b);
 }
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -350,8 +358,12 @@ int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* m
       ln_bwd_params_cols<T><<<grid, kThreads, 0, s>>>(pg, pb, dy, x, mean, rstd, rows, cols, rpb);
     }
   }
-  if (params)
-    ln_bwd_params_final<T><<<ceil_div(cols, 16), kThreads, 0, s>>>(dgamma, dbeta, pg, pb, nb, cols);
+  if (params) {
+    float* mg = ws + 2 * (int64_t)nb * cols;
+    float* mb = mg + (int64_t)kGroups * cols;
+    ln_bwd_params_mid<<<dim3(ceil_div(cols, 64), kGroups), kThreads, 0, s>>>(mg, mb, pg, pb, nb, cols);
+    ln_bwd_params_final<T><<<ceil_div(cols, kThreads), kThreads, 0, s>>>(dgamma, dbeta, mg, mb, cols);
+  }
   return check_launch("mi355x_layer_norm_bwd");
 }
 
@@ -383,7 +395,7 @@ extern "C" int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const vo
 }
 
 extern "C" int64_t mi355x_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
-  return 2 * (int64_t)bwd_blocks(rows) * cols * (int64_t)sizeof(float);
+  return 2 * ((int64_t)bwd_blocks(rows) + kGroups) * cols * (int64_t)sizeof(float);
 }
 
 extern "C" int mi355x_layer_norm_bwd(void* dx, void* dgamma, void* dbeta, const void* dy,

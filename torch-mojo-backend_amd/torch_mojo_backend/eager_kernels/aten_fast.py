@@ -1247,6 +1247,79 @@ def ws_ptr_or_none(p):
     return p if p else None
 
 
+# ---------------------------------------------------------------------------
+# fused linear (the autocast linear path: casts, GEMMs and the bias
+# gradient as direct kernel calls, without per-view dispatches)
+# ---------------------------------------------------------------------------
+def cast_to(t: MT, dtype) -> MT:
+    """t in `dtype` (t itself when it already is)."""
+    if t._dtype == dtype:
+        return t
+    out = _alloc(t._shape, dtype, t._device)
+    return copy_into(out, t)
+
+
+def _rows_view(t: MT) -> MT:
+    """[..., K] as a 2-D [M, K] view (materialised when the leading dims
+    do not collapse)."""
+    if len(t._shape) == 2:
+        return t
+    k = t._shape[-1]
+    m = t._numel // k if k else 0
+    if t._is_contiguous:
+        return MT._view_of(t, (m, k), (k, 1), t._offset, True)
+    lead_ok = t._strides[-1] == 1 or k == 1
+    if lead_ok:
+        # leading dims collapse when each stride equals the next one times its size
+        st = t._strides[-2] if len(t._shape) >= 2 else k
+        ok = True
+        for i in range(len(t._shape) - 2):
+            if t._shape[i] != 1 and t._strides[i] != t._strides[i + 1] * t._shape[i + 1]:
+                ok = False
+                break
+        if ok:
+            return MT._view_of(t, (m, k), (st, 1), t._offset)
+    c = materialize_contiguous(t)
+    return MT._view_of(c, (m, k), (k, 1), c._offset, True)
+
+
+def linear_forward(x: MT, w: MT, b) -> MT:
+    """out[..., N] = x[..., K] @ w[N, K]^T (+ b), one GEMM with the bias
+    in its epilogue (aten_fast.py:8755-8812 counterpart)."""
+    n, k = w._shape
+    x2 = _rows_view(x)
+    out = _alloc(tuple(x._shape[:-1]) + (n,), x._dtype, x._device)
+    o2 = MT._view_of(out, (x2._shape[0], n), (n, 1), 0, True)
+    wt = MT._view_of(w, (k, n), (w._strides[1], w._strides[0]), w._offset)
+    if b is not None and b._strides[-1] == 1:
+        _gemm(o2, x2, wt, bias=b)
+    else:
+        _gemm(o2, x2, wt)
+        if b is not None:
+            _map_call(OP["add"], o2, [(o2, o2._dtype), (b, b._dtype)], 1.0, 0.0)
+    return out
+
+
+def linear_backward(dy: MT, x: MT, w: MT, need_x: bool, need_w: bool, need_b: bool):
+    """(dx, dw, db) of linear_forward, each in the forward's compute dtype:
+    dx = dy w, dw = dy^T x, db = sum(dy, 0) (aten_fast.py:8815-8907)."""
+    n, k = w._shape
+    d2 = _rows_view(dy)
+    m = d2._shape[0]
+    dx = dw = db = None
+    if need_x:
+        dx = _alloc(tuple(dy._shape[:-1]) + (k,), dy._dtype, dy._device)
+        _gemm(MT._view_of(dx, (m, k), (k, 1), 0, True), d2, w)
+    if need_w:
+        x2 = _rows_view(x)
+        dw = _alloc((n, k), dy._dtype, dy._device)
+        dyt = MT._view_of(d2, (n, m), (d2._strides[1], d2._strides[0]), d2._offset)
+        _gemm(dw, dyt, x2)
+    if need_b:
+        db = _reduce(RED["sum"], d2, [0], False, dy._dtype)
+    return dx, dw, db
+
+
 def fast_aten_mm(self, mat2):
     a, b = _require(self), _require(mat2)
     if len(a._shape) != 2 or len(b._shape) != 2:

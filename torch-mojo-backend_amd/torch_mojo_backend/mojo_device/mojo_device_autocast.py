@@ -3,7 +3,9 @@
 Same policy table as the reference (torch_mojo_backend/mojo_device/
 mojo_device_autocast.py:537-567): matmul and attention run in the active
 lower precision; layer_norm and NLL run in f32; everything else falls
-through.  Casts are ordinary ``_to_copy`` ops on the device.
+through.  Casts are ordinary ``_to_copy`` ops on the device, except for
+``linear``, whose casts and GEMMs run inside one fused autograd Function
+(mojo_device_autograd._FusedLinear) with the same numerics.
 """
 
 from __future__ import annotations
@@ -59,7 +61,6 @@ def register_autocast_ops() -> None:
     lower = (
         torch.ops.aten.addmm.default,
         torch.ops.aten.bmm.default,
-        torch.ops.aten.linear.default,
         torch.ops.aten.matmul.default,
         torch.ops.aten.mm.default,
         torch.ops.aten.scaled_dot_product_attention.default,
@@ -77,4 +78,16 @@ def register_autocast_ops() -> None:
         )
     for op in fp32:
         _aten_library.impl(op._schema.name, _policy_wrapper(op, lambda: torch.float32))
+    _aten_library.impl("linear", _linear_autocast)
     _registered = True
+
+
+def _linear_autocast(input, weight, bias=None):
+    from .mojo_device_autograd import fused_linear, fused_linear_inputs
+
+    with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYSET):
+        dt = torch.get_autocast_dtype("mojo")
+        if fused_linear_inputs(input, weight, bias, dt):
+            return fused_linear(input, weight, bias, dt)
+        args = _cast_mojo_floating((input, weight, bias), dt)
+        return torch.ops.aten.linear.default(*args)

@@ -1,4 +1,8 @@
-"""AutogradPrivateUse1 implementation of ``aten::scaled_dot_product_attention``.
+"""Autograd kernels of the mojo device: ``aten::scaled_dot_product_attention``
+and ``aten::cross_entropy_loss`` (AutogradPrivateUse1), and the fused
+linear used by the autocast ``linear`` policy.
+
+SDPA:
 
 Routing follows the reference (torch_mojo_backend/mojo_device/
 mojo_device_autograd.py:565-643), re-targeted at gfx950:
@@ -13,6 +17,19 @@ mojo_device_autograd.py:565-643), re-targeted at gfx950:
   ops, differentiated through its pieces.
 
 There is no queue to drain before these routes: kernels are issued directly.
+
+Cross-entropy: one fused softmax-cross-entropy Function (row LSE saved,
+dlogits written once) where the inputs allow it, else the log_softmax ->
+nll_loss decomposition.
+
+Linear under autocast (mojo_device_autocast.py:547-561 puts linear in the
+lower-precision list): ``_FusedLinear`` casts x, w and b to the autocast
+dtype and runs one GEMM with the bias in its epilogue; its backward runs
+the dX and dW GEMMs and the bias column sum, each rounded to the autocast
+dtype and then widened to the dtype of the input it is the gradient of,
+exactly what the autocast casts' own backward passes produce.  It replaces
+the per-op chain (three casts, t, view, addmm, view and their autograd
+nodes) with one Python call in each direction.
 """
 
 from __future__ import annotations
@@ -20,6 +37,7 @@ from __future__ import annotations
 import torch
 
 from ..eager_kernels import aten_fast
+from .torch_mojo_tensor import TorchMojoTensor
 
 _registered = False
 _library = None
@@ -58,6 +76,52 @@ def register_autograd_ops() -> None:
     _library.impl("scaled_dot_product_attention", _scaled_dot_product_attention_autograd)
     _library.impl("cross_entropy_loss", _cross_entropy_loss_autograd)
     _registered = True
+
+
+class _FusedLinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, b, dt):
+        xl = aten_fast.cast_to(x, dt)
+        wl = aten_fast.cast_to(w, dt)
+        bl = aten_fast.cast_to(b, dt) if b is not None else None
+        ctx.save_for_backward(xl, wl)
+        ctx.dtypes = (x.dtype, w.dtype, b.dtype if b is not None else None)
+        return aten_fast.linear_forward(xl, wl, bl)
+
+    @staticmethod
+    def backward(ctx, grad):
+        xl, wl = ctx.saved_tensors
+        nx, nw, nb = ctx.needs_input_grad[:3]
+        nb = nb and ctx.dtypes[2] is not None
+        g = grad if grad.dtype == xl.dtype else aten_fast.cast_to(grad, xl.dtype)
+        dx, dw, db = aten_fast.linear_backward(g, xl, wl, nx, nw, nb)
+        xd, wd, bd = ctx.dtypes
+        return (
+            aten_fast.cast_to(dx, xd) if dx is not None else None,
+            aten_fast.cast_to(dw, wd) if dw is not None else None,
+            aten_fast.cast_to(db, bd) if db is not None else None,
+            None,
+        )
+
+
+def fused_linear(x, w, b, dt):
+    return _FusedLinear.apply(x, w, b, dt)
+
+
+def fused_linear_inputs(x, w, b, dt) -> bool:
+    """Whether the autocast linear can take the fused path."""
+    def ok(t):
+        return (
+            isinstance(t, TorchMojoTensor)
+            and t.dtype in (torch.float32, torch.bfloat16, torch.float16)
+            and hasattr(t, "_holder")
+        )
+    return (
+        dt in (torch.bfloat16, torch.float16)
+        and ok(x) and ok(w) and (b is None or (ok(b) and b.dim() == 1))
+        and w.dim() == 2 and x.dim() >= 1 and x.shape[-1] == w.shape[1]
+        and (b is None or b.shape[0] == w.shape[0])
+    )
 
 
 class _FusedCrossEntropy(torch.autograd.Function):
