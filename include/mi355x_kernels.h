@@ -377,6 +377,25 @@ int mi355x_gemm(void* c, int c_dtype, int64_t c_rs, int64_t c_bs,
                 int ab_dtype, const void* bias, int bias_dtype, int beta,
                 int64_t batch, int64_t m, int64_t n, int64_t k,
                 void* workspace, int64_t ws_bytes, mi355x_stream_t stream);
+/* mi355x_gemm with options (the linear backward of the autocast path,
+ * fast_aten_linear_backward aten_fast.py:8815-8907: dW = dY^T X and
+ * db = sum(dY, 0) from one pass over dY):
+ *   flags MI355X_GEMM_BETA   add the existing C (as beta == 1 above);
+ *         MI355X_GEMM_ROUND  round C (and the row sums) to ab_dtype before
+ *                            storing them in a wider c_dtype, the value a
+ *                            16-bit result widened afterwards would have;
+ *   a_rowsum (optional, [batch][m] of a_rowsum_dtype): sum over k of each
+ *                            row of A, accumulated in f32.
+ * Same workspace query as mi355x_gemm. */
+#define MI355X_GEMM_BETA 1
+#define MI355X_GEMM_ROUND 2
+int mi355x_gemm_ex(void* c, int c_dtype, int64_t c_rs, int64_t c_bs,
+                   const void* a, int64_t a_rs, int64_t a_cs, int64_t a_bs,
+                   const void* b, int64_t b_rs, int64_t b_cs, int64_t b_bs,
+                   int ab_dtype, const void* bias, int bias_dtype, int flags,
+                   void* a_rowsum, int a_rowsum_dtype,
+                   int64_t batch, int64_t m, int64_t n, int64_t k,
+                   void* workspace, int64_t ws_bytes, mi355x_stream_t stream);
 
 /* ---- causal flash attention (fast_fused_flash_attention_forward
  *      aten_fast.py:7533-7587 -> flash_attention_ops.mojo:48-112 ->

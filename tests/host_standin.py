@@ -464,6 +464,26 @@ class HostStandIn:
         C.copy_(r)
         return 0
 
+    def mi355x_gemm_ex(self, c, cdt, crs, cbs, a, ars, acs, abs_, b, brs, bcs, bbs, abdt, bias, bdt,
+                       flags, rowsum, rsdt, batch, m, n, k, ws, wsb, stream):
+        A = view(_val(a), DT[abdt], (batch, m, k), (abs_, ars, acs)).float()
+        B = view(_val(b), DT[abdt], (batch, k, n), (bbs, brs, bcs)).float()
+        C = view(_val(c), DT[cdt], (batch, m, n), (cbs, crs, 1))
+        r = torch.bmm(A, B)
+        if bias:
+            r = r + dense(_val(bias), DT[bdt], (n,)).float()
+        if flags & 1:
+            r = r + C.float()
+        if flags & 2:
+            r = r.to(DT[abdt]).float()
+        C.copy_(r)
+        if rowsum:
+            rs = A.sum(2)
+            if flags & 2:
+                rs = rs.to(DT[abdt]).float()
+            dense(_val(rowsum), DT[rsdt], (batch, m)).copy_(rs)
+        return 0
+
     def mi355x_attn_fwd(self, o, obhs, lse, q, qbhs, k, kbhs, v, vbhs, B, H, Sq, Skv, D, scale, causal, dt, stream):
         def t(p, st, s):
             return view(_val(p), DT[dt], (B, H, s, D), (st[0], st[1], st[2], 1))

@@ -243,3 +243,37 @@ def test_attention_cfg1_shape_properties(kernels):
     assert tot.abs().max().item() < 0.5
     # dV columns: sum over keys of dV = sum over queries of dO (P rows sum to 1)
     tol_close(host(dv).double().sum(2).numpy(), do.double().sum(2).numpy(), atol=0.5, rtol=2e-2, what="sum dV")
+
+
+@pytest.mark.parametrize("m,n,k,layout,batch", [(2304, 768, 16384, "TN", 1), (300, 200, 1001, "NT", 1),
+                                                (130, 96, 320, "NN", 2)])
+def test_gemm_ex_round_and_rowsum(kernels, m, n, k, layout, batch):
+    """mi355x_gemm_ex with MI355X_GEMM_ROUND (f32 C holding bf16-rounded
+    values) and the row sums of A (the linear bias gradient), with and
+    without split-K, ragged K and a batch."""
+    A = (randn(batch, m, k) * 0.5).bfloat16()
+    B = (randn(batch, k, n) * 0.1).bfloat16()
+    if layout[0] == "N":
+        ta, a_rs, a_cs = dev(A.contiguous()), k, 1
+    else:
+        ta, a_rs, a_cs = dev(A.transpose(1, 2).contiguous()), 1, m
+    if layout[1] == "N":
+        tb, b_rs, b_cs = dev(B.contiguous()), n, 1
+    else:
+        tb, b_rs, b_cs = dev(B.transpose(1, 2).contiguous()), 1, k
+    a_bs, b_bs = (m * k, k * n) if batch > 1 else (0, 0)
+    c = torch.empty(batch, m, n, device="cuda")
+    rs = torch.empty(batch, m, device="cuda")
+    ws_n = lib().mi355x_gemm_workspace_bytes(p(ta), a_rs, a_cs, a_bs, p(tb), b_rs, b_cs, b_bs, CODE[torch.bfloat16],
+                                             batch, m, n, k)
+    ws = workspace(ws_n) if ws_n else None
+    call("mi355x_gemm_ex", p(c), CODE[torch.float32], n, m * n, p(ta), a_rs, a_cs, a_bs, p(tb), b_rs, b_cs, b_bs,
+         CODE[torch.bfloat16], None, 0, 2, p(rs), CODE[torch.float32], batch, m, n, k, p(ws), ws_n, None)
+    got_c, got_rs = host(c), host(rs)
+    # ROUND: every stored value is a bf16 value
+    assert torch.equal(got_c, got_c.bfloat16().float())
+    assert torch.equal(got_rs, got_rs.bfloat16().float())
+    exp_c = np.einsum("bmk,bkn->bmn", A.double().numpy(), B.double().numpy())
+    exp_rs = A.double().numpy().sum(2)
+    tol_close(got_c.numpy(), exp_c, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what="C")
+    tol_close(got_rs.numpy(), exp_rs, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what="rowsum")

@@ -62,7 +62,17 @@ struct GemmArgs {
   int64_t kchunk;  // K per split
   int tiles_n;     // tiles along n
   int batch;       // batch count (grid.y = splits * batch)
+  int ab_dt;       // operand dtype (for rounding through it)
+  int round_c;     // round C (and the row sums) through ab_dt before storing
+  void* rowsum;    // optional sum over k of A's rows [batch][m], or null
+  int rowsum_dt;
+  float* rs_part;  // split-K row-sum partials [splits][batch][m]
 };
+
+// v rounded to the 16-bit operand dtype and widened back.
+__device__ __forceinline__ float round_through(float v, int dt) {
+  return dt == MI355X_BF16 ? (float)(bf16)v : (float)(f16)v;
+}
 
 __device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
   switch (dt) {
@@ -93,7 +103,19 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs g, int splits, int
     void* Cb = (char*)g.c + bi * g.c_bs * c_es;
     const int64_t off = row * g.c_rs + col;
     if (g.beta) v += ld_any(Cb, g.c_dt, off);
+    if (g.round_c) v = round_through(v, g.ab_dt);
     st_any(Cb, g.c_dt, off, v);
+  }
+}
+
+// Sum split-K row-sum partials into rowsum[batch][m].
+__global__ void __launch_bounds__(256) rowsum_reduce(GemmArgs g, int splits, int64_t nb) {
+  const int64_t total = nb * g.m;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+    float v = 0.f;
+    for (int s = 0; s < splits; ++s) v += g.rs_part[s * total + idx];
+    if (g.round_c) v = round_through(v, g.ab_dt);
+    st_any(g.rowsum, g.rowsum_dt, idx, v);
   }
 }
 
@@ -262,7 +284,7 @@ struct TileCfg<2> {  // C192: 128x192, waves of 64x96, 80 KB LDS, two blocks per
 // inside the tile are 32-bit (the host checks the row stride); EDGE adds the
 // bounds checks that only partial tiles need.  Each store instruction covers
 // four 16-column runs, and the j loop fills whole 128-byte lines.
-template <typename CT, bool BETA, bool EDGE, int TM, int TN>
+template <typename CT, typename T, bool BETA, bool EDGE, bool ROUND, int TM, int TN>
 __device__ __forceinline__ void store_tile(CT* __restrict__ C, int c_rs, const f32x4 (&acc)[TM][TN],
                                            const float (&bias)[TN], int rows_left, int cols_left, int lr,
                                            int lg) {
@@ -279,25 +301,33 @@ __device__ __forceinline__ void store_tile(CT* __restrict__ C, int c_rs, const f
         if (EDGE && c >= cols_left) continue;
         float v = acc[i][j][e] + bias[j];
         if (BETA) v += (float)row[c];
+        if (ROUND) v = (float)(T)v;
         row[c] = (CT)v;
       }
     }
 }
 
-template <typename CT, int TM, int TN>
+template <typename CT, typename T, int TM, int TN>
 __device__ __forceinline__ void store_any(CT* C, int c_rs, const f32x4 (&acc)[TM][TN], const float (&bias)[TN],
-                                          bool beta, int rows_left, int cols_left, int lr, int lg) {
+                                          bool beta, bool round, int rows_left, int cols_left, int lr, int lg) {
   const bool edge = rows_left < TM * 16 || cols_left < TN * 16;
-  if (beta) {
-    if (edge) store_tile<CT, true, true>(C, c_rs, acc, bias, rows_left, cols_left, lr, lg);
-    else store_tile<CT, true, false>(C, c_rs, acc, bias, rows_left, cols_left, lr, lg);
+#define ST(B, E, R) store_tile<CT, T, B, E, R>(C, c_rs, acc, bias, rows_left, cols_left, lr, lg)
+  if (round) {  // round-through stores are only used without beta
+    if (edge) ST(false, true, true);
+    else ST(false, false, true);
+  } else if (beta) {
+    if (edge) ST(true, true, false);
+    else ST(true, false, false);
   } else {
-    if (edge) store_tile<CT, false, true>(C, c_rs, acc, bias, rows_left, cols_left, lr, lg);
-    else store_tile<CT, false, false>(C, c_rs, acc, bias, rows_left, cols_left, lr, lg);
+    if (edge) ST(false, true, false);
+    else ST(false, false, false);
   }
+#undef ST
 }
 
-template <typename T, int CFG, bool A_K, bool B_K, bool KT>
+// RS: also sum A's rows over k (blocks of the first column tile, waves of
+// the first wave column), from the fragments the MFMAs consume.
+template <typename T, int CFG, bool A_K, bool B_K, bool KT, bool RS>
 __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, TileCfg<CFG>::MIN_BLOCKS)
     gemm_tile(GemmArgs g) {
   typedef typename Mfma<T>::frag frag;
@@ -346,6 +376,10 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   lb.template issue<KT>(kbeg, lds + A_BYTES, kend);
   // k-contiguous fragment rows (.. + lr) share the swizzle of lr
   const int sw = (lr >> 1) & 7;
+  const bool rs_on = RS && tn == 0 && wn == 0;
+  float rsum[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) rsum[i] = 0.f;
 
   int cur = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += 64) {
@@ -376,6 +410,10 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
         if constexpr (A_K) af = *(const frag*)(at + (wm * WM + i * 16 + lr) * 128 + coff);
         else af = mn_frag<T, BM>(at, wm * WM + i * 16, ks);
         if (tail) mask_k(af, kfrag, kend);
+        if (rs_on) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rsum[i] += (float)af[e];
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af, bfr[j], acc[i][j]);
       }
@@ -384,6 +422,23 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   }
 
   const int64_t row0 = m0 + wm * WM, col0 = n0 + wn * WN;
+  if (rs_on) {
+    // lane (lg, lr) holds row lr's sum over k = 8*lg .. of each 32-k step
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      rsum[i] += __shfl_xor(rsum[i], 16, 64);
+      rsum[i] += __shfl_xor(rsum[i], 32, 64);
+      const int64_t r = row0 + i * 16 + lr;
+      if (lg == 0 && r < g.m) {
+        if (g.part) {
+          g.rs_part[((int64_t)split * g.batch + bidx) * g.m + r] = rsum[i];
+        } else {
+          const float v = g.round_c ? round_through(rsum[i], g.ab_dt) : rsum[i];
+          st_any(g.rowsum, g.rowsum_dt, (int64_t)bidx * g.m + r, v);
+        }
+      }
+    }
+  }
   const int rows_left = (int)min(g.m - row0, (int64_t)WM), cols_left = (int)min(g.n - col0, (int64_t)WN);
   if (rows_left <= 0 || cols_left <= 0) return;
   float bias[TN];
@@ -391,7 +446,7 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
 #pragma unroll
     for (int j = 0; j < TN; ++j) bias[j] = 0.f;
     float* P = g.part + ((int64_t)split * g.batch + bidx) * g.m * g.n + row0 * g.n + col0;
-    store_any<float>(P, (int)g.n, acc, bias, false, rows_left, cols_left, lr, lg);
+    store_any<float, T>(P, (int)g.n, acc, bias, false, false, rows_left, cols_left, lr, lg);
     return;
   }
 #pragma unroll
@@ -402,9 +457,10 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   const int64_t c_es = g.c_dt == MI355X_F32 ? 4 : 2;
   char* Cb = (char*)g.c + ((int64_t)bidx * g.c_bs + row0 * g.c_rs + col0) * c_es;
   const int c_rs = (int)g.c_rs;
-  if (g.c_dt == MI355X_BF16) store_any<bf16>((bf16*)Cb, c_rs, acc, bias, g.beta, rows_left, cols_left, lr, lg);
-  else if (g.c_dt == MI355X_F32) store_any<float>((float*)Cb, c_rs, acc, bias, g.beta, rows_left, cols_left, lr, lg);
-  else store_any<f16>((f16*)Cb, c_rs, acc, bias, g.beta, rows_left, cols_left, lr, lg);
+  const bool rnd = g.round_c && g.c_dt == MI355X_F32;  // 16-bit outputs are already rounded
+  if (g.c_dt == MI355X_BF16) store_any<bf16, T>((bf16*)Cb, c_rs, acc, bias, g.beta, false, rows_left, cols_left, lr, lg);
+  else if (g.c_dt == MI355X_F32) store_any<float, T>((float*)Cb, c_rs, acc, bias, g.beta, rnd, rows_left, cols_left, lr, lg);
+  else store_any<f16, T>((f16*)Cb, c_rs, acc, bias, g.beta, false, rows_left, cols_left, lr, lg);
 }
 
 // Pack an operand into a k-contiguous [rows][ld] buffer of 16-bit elements,
@@ -543,20 +599,35 @@ Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool b_kcontig) {
 
 // Launch one kernel instantiation; the first launch of each opts it into
 // more than 64 KB of dynamic LDS when it needs that.
-template <typename T, int CFG, bool A_K, bool B_K, bool KT>
+template <typename T, int CFG, bool A_K, bool B_K, bool KT, bool RS>
 int launch_kernel(const GemmArgs& g, dim3 grid, hipStream_t s) {
   typedef TileCfg<CFG> C;
   constexpr int NT = 64 * C::WGM * C::WGN;
   constexpr size_t lds = 2 * (size_t)(C::BM + C::BN) * 128;
   static bool attr = false;
   if (lds > 65536 && !attr) {
-    if (hipFuncSetAttribute((const void*)gemm_tile<T, CFG, A_K, B_K, KT>,
+    if (hipFuncSetAttribute((const void*)gemm_tile<T, CFG, A_K, B_K, KT, RS>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return fail(MI355X_ELAUNCH, "mi355x_gemm: cannot reserve %zu bytes of LDS", lds);
     attr = true;
   }
-  gemm_tile<T, CFG, A_K, B_K, KT><<<grid, NT, lds, s>>>(g);
+  gemm_tile<T, CFG, A_K, B_K, KT, RS><<<grid, NT, lds, s>>>(g);
   return check_launch("mi355x_gemm");
+}
+
+template <typename T, int CFG, bool KT, bool RS>
+int launch_layout(const GemmArgs& g, dim3 grid, hipStream_t s) {
+  const bool ak = g.a_cs == 1, bk = g.b_rs == 1;
+  if constexpr (CFG == 2) {  // 192-wide B tiles are only loaded k-contiguous
+    if (!bk) return fail(MI355X_EINVAL, "mi355x_gemm: 128x192 tiles need a k-contiguous B");
+    if (ak) return launch_kernel<T, CFG, true, true, KT, RS>(g, grid, s);
+    return launch_kernel<T, CFG, false, true, KT, RS>(g, grid, s);
+  } else {
+    if (ak && bk) return launch_kernel<T, CFG, true, true, KT, RS>(g, grid, s);
+    if (ak) return launch_kernel<T, CFG, true, false, KT, RS>(g, grid, s);
+    if (bk) return launch_kernel<T, CFG, false, true, KT, RS>(g, grid, s);
+    return launch_kernel<T, CFG, false, false, KT, RS>(g, grid, s);
+  }
 }
 
 template <typename T, int CFG, bool KT>
@@ -566,17 +637,8 @@ int launch_tile(GemmArgs g, int64_t batch, int splits, hipStream_t s) {
   g.tiles_n = tn;
   g.batch = (int)batch;
   dim3 grid((unsigned)(tm * tn), (unsigned)(batch * splits));
-  const bool ak = g.a_cs == 1, bk = g.b_rs == 1;
-  if constexpr (CFG == 2) {  // 192-wide B tiles are only loaded k-contiguous
-    if (!bk) return fail(MI355X_EINVAL, "mi355x_gemm: 128x192 tiles need a k-contiguous B");
-    if (ak) return launch_kernel<T, CFG, true, true, KT>(g, grid, s);
-    return launch_kernel<T, CFG, false, true, KT>(g, grid, s);
-  } else {
-    if (ak && bk) return launch_kernel<T, CFG, true, true, KT>(g, grid, s);
-    if (ak) return launch_kernel<T, CFG, true, false, KT>(g, grid, s);
-    if (bk) return launch_kernel<T, CFG, false, true, KT>(g, grid, s);
-    return launch_kernel<T, CFG, false, false, KT>(g, grid, s);
-  }
+  if (g.rowsum) return launch_layout<T, CFG, KT, true>(g, grid, s);
+  return launch_layout<T, CFG, KT, false>(g, grid, s);
 }
 
 int splitk_finish(const GemmArgs& g, int64_t batch, int splits, hipStream_t s) {
@@ -595,7 +657,12 @@ int launch_mfma(GemmArgs g, int64_t batch, const Plan& p, hipStream_t s) {
   else if (p.cfg == 2) rc = kt ? launch_tile<T, 2, true>(g, batch, p.splits, s) : launch_tile<T, 2, false>(g, batch, p.splits, s);
   else rc = kt ? launch_tile<T, 0, true>(g, batch, p.splits, s) : launch_tile<T, 0, false>(g, batch, p.splits, s);
   if (rc || !g.part) return rc;
-  return splitk_finish(g, batch, p.splits, s);
+  rc = splitk_finish(g, batch, p.splits, s);
+  if (rc || !g.rowsum) return rc;
+  int64_t blocks = (batch * g.m + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  rowsum_reduce<<<(unsigned)blocks, 256, 0, s>>>(g, p.splits, batch);
+  return check_launch("mi355x_gemm rowsum_reduce");
 }
 
 bool fdt(int d) { return d == MI355X_F32 || d == MI355X_BF16 || d == MI355X_F16; }
@@ -634,7 +701,10 @@ WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int64_t k, const void* a
   w.pack_b = !in_place(b, b_cs, b_rs, b_bs, n) || (b_rs != 1 && (double)n < small_rows);
   w.plan = plan_gemm(batch, m, n, k, w.pack_b || b_rs == 1);
   auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
-  w.part_bytes = w.plan.splits > 1 ? up((int64_t)w.plan.splits * batch * m * n * 4) : 0;
+  // split-K partials of C, then of the optional row sums of A
+  w.part_bytes = w.plan.splits > 1 ? up((int64_t)w.plan.splits * batch * m * n * 4) +
+                                         up((int64_t)w.plan.splits * batch * m * 4)
+                                   : 0;
   const int64_t ab = a_bs == 0 ? 1 : batch, bb = b_bs == 0 ? 1 : batch;
   w.a_bytes = w.pack_a ? up(ab * m * w.kp * 2) : 0;
   w.b_bytes = w.pack_b ? up(bb * n * w.kp * 2) : 0;
@@ -666,13 +736,19 @@ extern "C" int64_t mi355x_gemm_workspace_bytes(const void* a, int64_t a_rs, int6
   return ws_layout(batch, m, n, k, a, a_rs, a_cs, a_bs, b, b_rs, b_cs, b_bs).total;
 }
 
-extern "C" int mi355x_gemm(void* c, int c_dtype, int64_t c_rs, int64_t c_bs, const void* a,
-                           int64_t a_rs, int64_t a_cs, int64_t a_bs, const void* b, int64_t b_rs,
-                           int64_t b_cs, int64_t b_bs, int ab_dtype, const void* bias,
-                           int bias_dtype, int beta, int64_t batch, int64_t m, int64_t n,
-                           int64_t k, void* workspace, int64_t ws_bytes, mi355x_stream_t stream) {
+extern "C" int mi355x_gemm_ex(void* c, int c_dtype, int64_t c_rs, int64_t c_bs, const void* a,
+                              int64_t a_rs, int64_t a_cs, int64_t a_bs, const void* b, int64_t b_rs,
+                              int64_t b_cs, int64_t b_bs, int ab_dtype, const void* bias,
+                              int bias_dtype, int flags, void* a_rowsum, int a_rowsum_dtype,
+                              int64_t batch, int64_t m, int64_t n, int64_t k, void* workspace,
+                              int64_t ws_bytes, mi355x_stream_t stream) {
   MI_REQUIRE(fdt(ab_dtype) && fdt(c_dtype), "mi355x_gemm: unsupported dtype");
   MI_REQUIRE(!bias || fdt(bias_dtype), "mi355x_gemm: unsupported bias dtype");
+  MI_REQUIRE(!a_rowsum || fdt(a_rowsum_dtype), "mi355x_gemm: unsupported row-sum dtype");
+  MI_REQUIRE((flags & ~(MI355X_GEMM_BETA | MI355X_GEMM_ROUND)) == 0, "mi355x_gemm: unknown flags %d", flags);
+  const int beta = (flags & MI355X_GEMM_BETA) ? 1 : 0;
+  const int round_c = (flags & MI355X_GEMM_ROUND) ? 1 : 0;
+  MI_REQUIRE(!(beta && round_c), "mi355x_gemm: ROUND cannot be combined with BETA");
   MI_REQUIRE(batch >= 1 && m >= 0 && n >= 0 && k >= 0, "mi355x_gemm: bad shape");
   MI_REQUIRE(batch < 65536 && m < (1ll << 31) && n < (1ll << 31), "mi355x_gemm: shape too large");
   if (m == 0 || n == 0) return MI355X_OK;
@@ -682,8 +758,9 @@ extern "C" int mi355x_gemm(void* c, int c_dtype, int64_t c_rs, int64_t c_bs, con
   MI_REQUIRE(c && a && b, "mi355x_gemm: null pointer");
   hipStream_t s = (hipStream_t)stream;
   GemmArgs g{c, c_dtype, c_rs, c_bs, a, a_rs, a_cs, a_bs, b, b_rs, b_cs, b_bs, bias, bias_dtype,
-             beta, m, n, k, nullptr, k, 1, 1};
+             beta, m, n, k, nullptr, k, 1, 1, ab_dtype, round_c, a_rowsum, a_rowsum_dtype, nullptr};
   if (ab_dtype == MI355X_F32) {
+    MI_REQUIRE(!a_rowsum && !round_c, "mi355x_gemm: row sums and ROUND need 16-bit operands");
     dim3 grid(ceil_div(n, 64), ceil_div(m, 64), (unsigned)batch);
     gemm_f32<<<grid, 256, 0, s>>>(g);
     return check_launch("mi355x_gemm");
@@ -717,7 +794,18 @@ extern "C" int mi355x_gemm(void* c, int c_dtype, int64_t c_rs, int64_t c_bs, con
   if (w.plan.splits > 1) {
     g.part = (float*)ws;
     g.kchunk = w.plan.kchunk;
+    g.rs_part = (float*)(ws + (((int64_t)w.plan.splits * batch * m * n * 4 + 255) / 256 * 256));
   }
   if (ab_dtype == MI355X_BF16) return launch_mfma<bf16>(g, batch, w.plan, s);
   return launch_mfma<f16>(g, batch, w.plan, s);
+}
+
+extern "C" int mi355x_gemm(void* c, int c_dtype, int64_t c_rs, int64_t c_bs, const void* a,
+                           int64_t a_rs, int64_t a_cs, int64_t a_bs, const void* b, int64_t b_rs,
+                           int64_t b_cs, int64_t b_bs, int ab_dtype, const void* bias,
+                           int bias_dtype, int beta, int64_t batch, int64_t m, int64_t n,
+                           int64_t k, void* workspace, int64_t ws_bytes, mi355x_stream_t stream) {
+  return mi355x_gemm_ex(c, c_dtype, c_rs, c_bs, a, a_rs, a_cs, a_bs, b, b_rs, b_cs, b_bs, ab_dtype, bias,
+                        bias_dtype, beta ? MI355X_GEMM_BETA : 0, nullptr, 0, batch, m, n, k, workspace,
+                        ws_bytes, stream);
 }

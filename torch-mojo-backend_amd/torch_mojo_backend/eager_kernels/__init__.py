@@ -20,7 +20,7 @@ from pathlib import Path
 
 LIB_NAME = "libmi355x_kernels.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 c_int = ctypes.c_int
 c_i64 = ctypes.c_int64
@@ -141,6 +141,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_vp, c_i64, c_i64, c_i64,
             c_vp, c_i64, c_i64, c_i64,
             c_int, c_vp, c_int, c_int,
+            c_i64, c_i64, c_i64, c_i64,
+            c_vp, c_i64, c_vp,
+        ],
+    ),
+    "mi355x_gemm_ex": (
+        c_int,
+        [
+            c_vp, c_int, c_i64, c_i64,
+            c_vp, c_i64, c_i64, c_i64,
+            c_vp, c_i64, c_i64, c_i64,
+            c_int, c_vp, c_int, c_int, c_vp, c_int,
             c_i64, c_i64, c_i64, c_i64,
             c_vp, c_i64, c_vp,
         ],

@@ -1203,12 +1203,17 @@ def _gemm_operand(x: MT, rank: int):
     return x, rs, cs, bs
 
 
-def _gemm(out: MT, a: MT, b: MT, bias=None, beta=0, batch=1):
+def _gemm(out: MT, a: MT, b: MT, bias=None, beta=0, batch=1, round_out=False, rowsum=None):
+    """out = a @ b (+ bias) (+ out if beta); round_out rounds the result to
+    the operands' 16-bit dtype before storing it in a wider out; rowsum
+    (optional [m] or [batch, m] tensor) receives the row sums of a."""
     m, k = a._shape[-2], a._shape[-1]
     n = b._shape[-1]
     if out._numel == 0:
         return out
     if k == 0:
+        if rowsum is not None:
+            fill_(rowsum, 0)
         if beta:
             return out
         fill_(out, 0)
@@ -1229,14 +1234,16 @@ def _gemm(out: MT, a: MT, b: MT, bias=None, beta=0, batch=1):
     ws = lib().mi355x_gemm_workspace_bytes(a._ptr, ars, acs, abs_, b._ptr, brs, bcs, bbs,
                                            _code(a._dtype), batch, m, n, k)
     hold, wptr = _workspace(ws, a._device)
+    flags = (1 if beta else 0) | (2 if round_out else 0)
     check(
         "mi355x_gemm",
-        lib().mi355x_gemm(
+        lib().mi355x_gemm_ex(
             out._ptr, _code(out._dtype), c_rs, c_bs,
             a._ptr, ars, acs, abs_,
             b._ptr, brs, bcs, bbs,
             _code(a._dtype), bias._ptr if bias is not None else None,
-            _code(bias._dtype) if bias is not None else 0, int(beta),
+            _code(bias._dtype) if bias is not None else 0, flags,
+            rowsum._ptr if rowsum is not None else None, _code(rowsum._dtype) if rowsum is not None else 0,
             batch, m, n, k, ws_ptr_or_none(wptr), ws, _STREAM,
         ),
     )
@@ -1300,23 +1307,32 @@ def linear_forward(x: MT, w: MT, b) -> MT:
     return out
 
 
-def linear_backward(dy: MT, x: MT, w: MT, need_x: bool, need_w: bool, need_b: bool):
-    """(dx, dw, db) of linear_forward, each in the forward's compute dtype:
-    dx = dy w, dw = dy^T x, db = sum(dy, 0) (aten_fast.py:8815-8907)."""
+def linear_backward(dy: MT, x: MT, w: MT, need_x: bool, need_w: bool, need_b: bool,
+                    x_dtype, w_dtype, b_dtype):
+    """(dx, dw, db) of linear_forward (aten_fast.py:8815-8907): dx = dy w,
+    dw = dy^T x, db = sum(dy, 0), computed in the forward's 16-bit dtype and
+    delivered in x_dtype / w_dtype / b_dtype: a wider dtype gets the 16-bit
+    result widened (the GEMM rounds before storing), as the autocast casts'
+    own backward would produce.  db comes out of the dW GEMM as the row sums
+    of dy^T, so dy is read once for both."""
     n, k = w._shape
     d2 = _rows_view(dy)
     m = d2._shape[0]
+    cdt = dy._dtype
     dx = dw = db = None
     if need_x:
-        dx = _alloc(tuple(dy._shape[:-1]) + (k,), dy._dtype, dy._device)
-        _gemm(MT._view_of(dx, (m, k), (k, 1), 0, True), d2, w)
+        dx = _alloc(tuple(dy._shape[:-1]) + (k,), x_dtype, dy._device)
+        _gemm(MT._view_of(dx, (m, k), (k, 1), 0, True), d2, w, round_out=x_dtype != cdt)
+    if need_b:
+        db = _alloc((n,), b_dtype, dy._device)
     if need_w:
         x2 = _rows_view(x)
-        dw = _alloc((n, k), dy._dtype, dy._device)
+        dw = _alloc((n, k), w_dtype, dy._device)
         dyt = MT._view_of(d2, (n, m), (d2._strides[1], d2._strides[0]), d2._offset)
-        _gemm(dw, dyt, x2)
-    if need_b:
-        db = _reduce(RED["sum"], d2, [0], False, dy._dtype)
+        _gemm(dw, dyt, x2, round_out=w_dtype != cdt or (need_b and b_dtype != cdt), rowsum=db)
+    elif need_b:
+        r = _reduce(RED["sum"], d2, [0], False, cdt)
+        db = cast_to(r, b_dtype)
     return dx, dw, db
 
 

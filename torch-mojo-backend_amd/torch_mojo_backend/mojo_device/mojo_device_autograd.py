@@ -94,14 +94,9 @@ class _FusedLinear(torch.autograd.Function):
         nx, nw, nb = ctx.needs_input_grad[:3]
         nb = nb and ctx.dtypes[2] is not None
         g = grad if grad.dtype == xl.dtype else aten_fast.cast_to(grad, xl.dtype)
-        dx, dw, db = aten_fast.linear_backward(g, xl, wl, nx, nw, nb)
         xd, wd, bd = ctx.dtypes
-        return (
-            aten_fast.cast_to(dx, xd) if dx is not None else None,
-            aten_fast.cast_to(dw, wd) if dw is not None else None,
-            aten_fast.cast_to(db, bd) if db is not None else None,
-            None,
-        )
+        dx, dw, db = aten_fast.linear_backward(g, xl, wl, nx, nw, nb, xd, wd, bd)
+        return dx, dw, db, None
 
 
 def fused_linear(x, w, b, dt):
