@@ -129,8 +129,15 @@ def test_gpt_step_matches_cpu(mojo):
 
 def test_embedding_out_of_range_raises(mojo):
     w = torch.randn(10, 4).to("mojo")
-    with pytest.raises(IndexError):
-        F.embedding(torch.tensor([1, 10]).to("mojo"), w)
+    out = F.embedding(torch.tensor([1, 10]).to("mojo"), w)  # no host sync here
+    with pytest.raises(IndexError, match="index out of range"):
+        out.cpu()  # the flagged error surfaces at the next host read
+    assert torch.equal(F.embedding(torch.tensor([1, 9]).to("mojo"), w).cpu(), w.cpu()[[1, 9]])
+    lp = torch.randn(3, 5).log_softmax(1).to("mojo")
+    loss = F.nll_loss(lp, torch.tensor([0, 5, 1]).to("mojo"))
+    with pytest.raises(IndexError, match="Target is out of bounds"):
+        loss.item()
+    assert torch.isfinite(F.nll_loss(lp, torch.tensor([0, 4, 1]).to("mojo")).cpu())
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -48,7 +48,9 @@ def test_loader_signatures_cover_the_header():
 def test_abi_version_and_target(raw):
     raw.mi355x_abi_version.restype = ctypes.c_int
     raw.mi355x_target.restype = ctypes.c_char_p
-    assert raw.mi355x_abi_version() == 1
+    from torch_mojo_backend.eager_kernels import ABI_VERSION
+
+    assert raw.mi355x_abi_version() == ABI_VERSION
     assert raw.mi355x_target() == b"gfx950"
 
 

@@ -1135,31 +1135,56 @@ def fast_aten_index_select(self, dim, index):
         shape[d] = n_idx
     out = _alloc(shape, t._dtype, t._device)
     if out._numel:
-        err, eptr = _error_flag(t._device)
+        eptr = _error_slot(t._device, _INDEX_ERROR)
         check(
             "mi355x_index_select",
             lib().mi355x_index_select(out._ptr, src._ptr, _code(src._dtype), idx._ptr, outer,
                                       n_idx, rows, inner, rows * inner, inner, eptr, _STREAM),
         )
-        _raise_if_flagged(err, "index out of range in self")
     return out
 
 
-def _error_flag(device):
-    flag = _alloc((1,), torch.int32, device)
-    fill_(flag, 0)
-    return flag, flag._ptr
+# Device-side bounds errors.  Kernels that validate indices store 1 into an
+# int32 slot of a persistent per-device flag buffer instead of faulting;
+# nothing synchronises at launch.  The flags are read (and cleared) at the
+# next device->host read, which waits for the queue anyway, and the error is
+# raised there, like the reference's queued errors that surface at the next
+# drain (eager_kernels/call_queue.py).
+_ERROR_KINDS = (
+    (IndexError, "index out of range in self"),
+    (IndexError, "Target is out of bounds"),
+)
+_INDEX_ERROR, _TARGET_ERROR = 0, 1
+_error_flags: dict = {}      # device index -> int32 [len(_ERROR_KINDS)] flag tensor
+_errors_pending: set = set()  # devices with a flag launch since the last read
 
 
-_CHECK_INDEX_ERRORS = True
+def _error_slot(device, kind):
+    """Pointer to `kind`'s flag on `device`; the next host read checks it."""
+    flags = _error_flags.get(device)
+    if flags is None:
+        flags = _alloc((len(_ERROR_KINDS),), torch.int32, device)
+        fill_(flags, 0)
+        _error_flags[device] = flags
+    _errors_pending.add(device)
+    return flags._ptr + 4 * kind
 
 
-def _raise_if_flagged(flag, message):
-    """Surface a device-side bounds error.  Reading the flag is a host sync;
-    it is skipped when _CHECK_INDEX_ERRORS is off (the kernels still never
-    access out of bounds)."""
-    if _CHECK_INDEX_ERRORS and flag._to_cpu_tensor().item():
-        raise IndexError(message)
+def raise_pending_device_errors():
+    """Read the flags of every device with flagged launches since the last
+    call, clear them, and raise the first recorded error.  Called before
+    each device->host copy."""
+    if not _errors_pending:
+        return
+    devices = list(_errors_pending)
+    _errors_pending.clear()
+    for dev in devices:
+        flags = _error_flags[dev]
+        host = flags._holder[: 4 * len(_ERROR_KINDS)].to("cpu", copy=True).view(torch.int32)
+        if host.any():
+            fill_(flags, 0)
+            exc, message = _ERROR_KINDS[int(host.nonzero()[0, 0])]
+            raise exc(message)
 
 
 def fast_aten_index_tensor(self, indices):
@@ -1601,14 +1626,13 @@ def fast_aten_nll_loss_forward(self, target, weight, reduction, ignore_index):
     total = _alloc((), lp._dtype, lp._device)
     ws = lib().mi355x_nll_workspace_bytes(n)
     hold, wptr = _workspace(ws, lp._device)
-    err, eptr = _error_flag(lp._device)
+    eptr = _error_slot(lp._device, _TARGET_ERROR)
     check(
         "mi355x_nll_fwd",
         lib().mi355x_nll_fwd(out._ptr, total._ptr, x._ptr, _code(lp._dtype), tgt._ptr,
                              w._ptr if w is not None else None, n, c, int(reduction),
                              int(ignore_index), eptr, wptr, ws, _STREAM),
     )
-    _raise_if_flagged(err, "Target is out of bounds")
     return out, total
 
 
@@ -1658,13 +1682,12 @@ def fast_aten_embedding(weight, indices, padding_idx=-1, scale_grad_by_freq=Fals
     wsrc = w if w._strides[1] == 1 else materialize_contiguous(w)
     out = _alloc(tuple(idx._shape) + (dim,), w._dtype, w._device)
     if out._numel:
-        err, eptr = _error_flag(w._device)
+        eptr = _error_slot(w._device, _INDEX_ERROR)
         check(
             "mi355x_embedding_fwd",
             lib().mi355x_embedding_fwd(out._ptr, wsrc._ptr, _code(w._dtype), ids._ptr, ids._numel,
                                        num, dim, wsrc._strides[0], eptr, _STREAM),
         )
-        _raise_if_flagged(err, "index out of range in self")
     return out
 
 
@@ -2018,14 +2041,13 @@ def fused_cross_entropy_forward(x: MT, t: MT, reduction, ignore_index):
     total = _alloc((), torch.float32, x._device)
     ws = lib().mi355x_cross_entropy_workspace_bytes(n)
     hold, wptr = _workspace(ws, x._device)
-    err, eptr = _error_flag(x._device)
+    eptr = _error_slot(x._device, _TARGET_ERROR)
     check(
         "mi355x_cross_entropy_fwd",
         lib().mi355x_cross_entropy_fwd(out._ptr, total._ptr, lse._ptr, x._ptr, _code(x._dtype), ld,
                                        tgt._ptr, n, c, int(reduction), int(ignore_index), eptr, wptr,
                                        ws, _STREAM),
     )
-    _raise_if_flagged(err, "Target is out of bounds")
     return out, lse, total
 
 

@@ -217,7 +217,12 @@ class TorchMojoTensor(torch.Tensor):
         return out
 
     def _to_cpu_tensor(self) -> torch.Tensor:
-        """D2H copy into a new CPU tensor (waits for pending device work)."""
+        """D2H copy into a new CPU tensor (waits for pending device work).
+        A bounds error that a kernel flagged since the last host read is
+        raised here."""
+        from ..eager_kernels import aten_fast
+
+        aten_fast.raise_pending_device_errors()
         src = self._contig()
         out = torch.empty(src._shape, dtype=src._dtype)
         nbytes = src._numel * src._itemsize
