@@ -246,7 +246,9 @@ def test_attention_cfg1_shape_properties(kernels):
 
 
 @pytest.mark.parametrize("m,n,k,layout,batch", [(2304, 768, 16384, "TN", 1), (300, 200, 1001, "NT", 1),
-                                                (130, 96, 320, "NN", 2)])
+                                                (130, 96, 320, "NN", 2), (1000, 520, 4160, "TN", 1),
+                                                (768, 3072, 16384, "TT", 1), (2048, 3072, 1024, "NT", 1),
+                                                (4096, 4096, 512, "NT", 1)])
 def test_gemm_ex_round_and_rowsum(kernels, m, n, k, layout, batch):
     """mi355x_gemm_ex with MI355X_GEMM_ROUND (f32 C holding bf16-rounded
     values) and the row sums of A (the linear bias gradient), with and
@@ -273,7 +275,7 @@ def test_gemm_ex_round_and_rowsum(kernels, m, n, k, layout, batch):
     # ROUND: every stored value is a bf16 value
     assert torch.equal(got_c, got_c.bfloat16().float())
     assert torch.equal(got_rs, got_rs.bfloat16().float())
-    exp_c = np.einsum("bmk,bkn->bmn", A.double().numpy(), B.double().numpy())
-    exp_rs = A.double().numpy().sum(2)
+    exp_c = torch.bmm(A.double(), B.double()).numpy()
+    exp_rs = A.double().sum(2).numpy()
     tol_close(got_c.numpy(), exp_c, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what="C")
     tol_close(got_rs.numpy(), exp_rs, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what="rowsum")

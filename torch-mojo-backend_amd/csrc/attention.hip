@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(kThreads) attn_fwd_kernel(AttnArgs p) {
   __shared__ __attribute__((aligned(16))) T Ks[64 * (D + 8)];
   __shared__ __attribute__((aligned(16))) T Vt[D * 72];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
   const BlockCoord bc = block_coord();
   const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
@@ -342,7 +342,7 @@ template <int D>
 __device__ __forceinline__ void kv_tile_issue(const char* g, int64_t rs_bytes, int64_t row0,
                                               int64_t nrows, char* dst) {
   typedef KvLayout<D> L;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   constexpr int INSTR = L::TILE / 1024;
 #pragma unroll
   for (int it = 0; it < INSTR / 4; ++it) {
@@ -382,7 +382,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_fwd_v2(AttnArg
   constexpr int STAGE = 2 * L::TILE;  // K tile + V tile
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
   const BlockCoord bc = block_coord();
   const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
@@ -571,7 +571,7 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dkv(AttnBwdArgs p) {
   __shared__ float lse_s[64], delta_s[64];
 
   const AttnArgs& f = p.f;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
   const BlockCoord bc = block_coord();
   const int64_t k0 = bc.x * 64;
@@ -673,7 +673,7 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dq(AttnBwdArgs p) {
   __shared__ __attribute__((aligned(16))) T Vs[64 * (D + 8)];
 
   const AttnArgs& f = p.f;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
   const BlockCoord bc = block_coord();
   const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
@@ -772,7 +772,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
   const AttnArgs& f = p.f;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
   const BlockCoord bc = block_coord();
   const int64_t k0 = bc.x * 128;
@@ -922,7 +922,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
   const AttnArgs& f = p.f;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
   const BlockCoord bc = block_coord();
   const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;

@@ -66,7 +66,7 @@ struct GemmArgs {
   int round_c;     // round C (and the row sums) through ab_dt before storing
   void* rowsum;    // optional sum over k of A's rows [batch][m], or null
   int rowsum_dt;
-  float* rs_part;  // split-K row-sum partials [splits][batch][m]
+  float* rs_part;  // split-K row-sum partials [splits * rs_slots][batch][m]
 };
 
 // v rounded to the 16-bit operand dtype and widened back.
@@ -108,14 +108,35 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs g, int splits, int
   }
 }
 
-// Sum split-K row-sum partials into rowsum[batch][m].
-__global__ void __launch_bounds__(256) rowsum_reduce(GemmArgs g, int splits, int64_t nb) {
+// Sum the row-sum partials ([slots][nb * m]) into rowsum[batch][m].  A block
+// takes 32 rows at a time with 8 threads per row, each summing every 8th
+// slot, then combines the 8 in LDS.
+__global__ void __launch_bounds__(256) rowsum_reduce(GemmArgs g, int slots, int64_t nb) {
+  __shared__ float red[8][33];
   const int64_t total = nb * g.m;
-  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int64_t base = (int64_t)blockIdx.x * 32; base < total; base += (int64_t)gridDim.x * 32) {
+    const int64_t idx = base + tx;
     float v = 0.f;
-    for (int s = 0; s < splits; ++s) v += g.rs_part[s * total + idx];
-    if (g.round_c) v = round_through(v, g.ab_dt);
-    st_any(g.rowsum, g.rowsum_dt, idx, v);
+    if (idx < total) {
+      int s = ty;
+      for (; s + 24 < slots; s += 32) {
+        const float a0 = g.rs_part[s * total + idx], a1 = g.rs_part[(s + 8) * total + idx];
+        const float a2 = g.rs_part[(s + 16) * total + idx], a3 = g.rs_part[(s + 24) * total + idx];
+        v += (a0 + a1) + (a2 + a3);
+      }
+      for (; s < slots; s += 8) v += g.rs_part[s * total + idx];
+    }
+    red[ty][tx] = v;
+    __syncthreads();
+    if (ty == 0 && idx < total) {
+      float r = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r += red[j][tx];
+      if (g.round_c) r = round_through(r, g.ab_dt);
+      st_any(g.rowsum, g.rowsum_dt, idx, r);
+    }
+    __syncthreads();
   }
 }
 
@@ -136,7 +157,7 @@ struct TileLoad {
   int chunk;
 
   __device__ __forceinline__ void init(const char* base, int64_t ld_bytes, int64_t row0, int64_t rows) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int r = wave * 8 + (lane >> 3);
     chunk = (lane & 7) ^ ((r >> 1) & 7);
 #pragma unroll
@@ -150,7 +171,7 @@ struct TileLoad {
   // kend_bytes reloads chunk 0 (masked out of the MFMAs, address valid).
   template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0_bytes, char* dst, int64_t kend_bytes) const {
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_id();
     const int64_t koff = (KT && k0_bytes + chunk * 16 >= kend_bytes) ? k0_bytes - chunk * 16 : k0_bytes;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it)
@@ -182,7 +203,7 @@ struct TileLoadT {
   // A last partial chunk of rows reads into the row padding (the k stride
   // is at least the row count rounded up to 8, checked by the caller).
   __device__ __forceinline__ void init(const char* b, int64_t ld_bytes, int64_t r0, int64_t rows) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = wave_id();
     base = b;
     ld = ld_bytes;
     const int64_t last_chunk = ((rows - 1) >> 3) << 3;
@@ -197,7 +218,7 @@ struct TileLoadT {
   // KT: k-rows at or past kend reload row kend-1 (masked out of the MFMAs).
   template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0, char* dst, int64_t kend) const {
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_id();
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
       int64_t k = k0 + kr[it];
@@ -325,8 +346,12 @@ __device__ __forceinline__ void store_any(CT* C, int c_rs, const f32x4 (&acc)[TM
 #undef ST
 }
 
-// RS: also sum A's rows over k (blocks of the first column tile, waves of
-// the first wave column), from the fragments the MFMAs consume.
+// RS: also sum A's rows over k, from the fragments the MFMAs consume, with
+// one extra MFMA against a fragment of ones (every column of its 16x16
+// result is the row sum).  With split K the 32-k substeps are dealt round
+// robin over the tiles_n * WGN waves that hold the same rows (one substep in
+// that many per wave), each writing its own partial slot; without split K
+// the waves of the first wave column of the first column tile do it all.
 template <typename T, int CFG, bool A_K, bool B_K, bool KT, bool RS>
 __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, TileCfg<CFG>::MIN_BLOCKS)
     gemm_tile(GemmArgs g) {
@@ -358,7 +383,7 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   const int64_t a_ldb = (A_K ? g.a_rs : g.a_cs) * (int64_t)sizeof(T);
   const int64_t b_ldb = (B_K ? g.b_cs : g.b_rs) * (int64_t)sizeof(T);
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();  // scalar: the row-sum test branches on it
   const int wm = wave / C::WGN, wn = wave % C::WGN;
   const int lr = lane & 15, lg = lane >> 4;
 
@@ -376,10 +401,16 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   lb.template issue<KT>(kbeg, lds + A_BYTES, kend);
   // k-contiguous fragment rows (.. + lr) share the swizzle of lr
   const int sw = (lr >> 1) & 7;
-  const bool rs_on = RS && tn == 0 && wn == 0;
-  float rsum[TM];
+  const int rs_slots = g.part ? g.tiles_n * C::WGN : 1;
+  const int rs_slot = g.part ? (int)tn * C::WGN + wn : 0;
+  const bool rs_on = RS && (g.part || (tn == 0 && wn == 0));
+  int rs_q = 0;  // this wave's substep counter modulo rs_slots
+  f32x4 rsum[TM];
+  frag ones;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) rsum[i] = 0.f;
+  for (int i = 0; i < TM; ++i) rsum[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
 
   int cur = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += 64) {
@@ -395,6 +426,8 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
     const bool tail = KT && k0 + 64 > kend;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
+      const bool rs_now = rs_on && rs_q == rs_slot;
+      if (RS && ++rs_q == rs_slots) rs_q = 0;
       const int coff = ((ks * 4 + lg) ^ sw) * 16;
       const int64_t kfrag = k0 + ks * 32 + lg * 8;
       frag bfr[TN];
@@ -410,10 +443,7 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
         if constexpr (A_K) af = *(const frag*)(at + (wm * WM + i * 16 + lr) * 128 + coff);
         else af = mn_frag<T, BM>(at, wm * WM + i * 16, ks);
         if (tail) mask_k(af, kfrag, kend);
-        if (rs_on) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) rsum[i] += (float)af[e];
-        }
+        if (RS && rs_now) rsum[i] = Mfma<T>::mma(af, ones, rsum[i]);
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af, bfr[j], acc[i][j]);
       }
@@ -422,22 +452,22 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   }
 
   const int64_t row0 = m0 + wm * WM, col0 = n0 + wn * WN;
-  if (rs_on) {
-    // lane (lg, lr) holds row lr's sum over k = 8*lg .. of each 32-k step
+  if (RS && rs_on && lr == 0) {
+    // lane (lg, 0) holds rows 4*lg .. 4*lg+3 of each 16-row fragment
+    const int64_t slot = (int64_t)split * rs_slots + rs_slot;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      rsum[i] += __shfl_xor(rsum[i], 16, 64);
-      rsum[i] += __shfl_xor(rsum[i], 32, 64);
-      const int64_t r = row0 + i * 16 + lr;
-      if (lg == 0 && r < g.m) {
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t r = row0 + i * 16 + lg * 4 + e;
+        if (r >= g.m) continue;
         if (g.part) {
-          g.rs_part[((int64_t)split * g.batch + bidx) * g.m + r] = rsum[i];
+          g.rs_part[(slot * g.batch + bidx) * g.m + r] = rsum[i][e];
         } else {
-          const float v = g.round_c ? round_through(rsum[i], g.ab_dt) : rsum[i];
+          const float v = g.round_c ? round_through(rsum[i][e], g.ab_dt) : rsum[i][e];
           st_any(g.rowsum, g.rowsum_dt, (int64_t)bidx * g.m + r, v);
         }
       }
-    }
   }
   const int rows_left = (int)min(g.m - row0, (int64_t)WM), cols_left = (int)min(g.n - col0, (int64_t)WN);
   if (rows_left <= 0 || cols_left <= 0) return;
@@ -559,6 +589,12 @@ int64_t tiles_of(int cfg, int64_t batch, int64_t m, int64_t n) {
   return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch;
 }
 
+// Row-sum partial slots per split: one per wave column of every column tile.
+int64_t rs_slots_of(int cfg, int64_t n) {
+  const int64_t bn = cfg == 1 ? 256 : (cfg == 2 ? 192 : 128), wgn = cfg == 1 ? 4 : 2;
+  return (n + bn - 1) / bn * wgn;
+}
+
 // Pick the configuration that finishes in the least time: whole rounds of
 // the CUs' block slots (two C128 blocks or one C256 block per CU) times the
 // per-round time measured on gfx950 at K = 768..3072 (a C256 round does
@@ -659,9 +695,8 @@ int launch_mfma(GemmArgs g, int64_t batch, const Plan& p, hipStream_t s) {
   if (rc || !g.part) return rc;
   rc = splitk_finish(g, batch, p.splits, s);
   if (rc || !g.rowsum) return rc;
-  int64_t blocks = (batch * g.m + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  rowsum_reduce<<<(unsigned)blocks, 256, 0, s>>>(g, p.splits, batch);
+  const int64_t blocks = min((batch * g.m + 31) / 32, (int64_t)65536);
+  rowsum_reduce<<<(unsigned)blocks, 256, 0, s>>>(g, (int)(p.splits * rs_slots_of(p.cfg, g.n)), batch);
   return check_launch("mi355x_gemm rowsum_reduce");
 }
 
@@ -703,7 +738,7 @@ WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int64_t k, const void* a
   auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
   // split-K partials of C, then of the optional row sums of A
   w.part_bytes = w.plan.splits > 1 ? up((int64_t)w.plan.splits * batch * m * n * 4) +
-                                         up((int64_t)w.plan.splits * batch * m * 4)
+                                         up((int64_t)w.plan.splits * rs_slots_of(w.plan.cfg, n) * batch * m * 4)
                                    : 0;
   const int64_t ab = a_bs == 0 ? 1 : batch, bb = b_bs == 0 ? 1 : batch;
   w.a_bytes = w.pack_a ? up(ab * m * w.kp * 2) : 0;

@@ -16,6 +16,13 @@ namespace mi {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
+// This thread's wave within the block, in a scalar register.  Conditions
+// built from it are then scalar branches.  As a per-lane value the compiler
+// would treat them as divergent and guard their code with the exec mask,
+// and an MFMA under an exec mask still executes, reading operands whose
+// (masked-off) VALU set-up never ran.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 template <typename T>
 struct Mfma;
 
