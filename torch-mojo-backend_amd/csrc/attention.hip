@@ -31,6 +31,19 @@
 #include "common.h"
 #include "mfma.h"
 
+// D = 64 forward: waves per 128-query block (4: 32 queries per wave) and
+// blocks per CU it is compiled for (the second __launch_bounds__ argument is
+// the minimum number of waves per SIMD, which sets the register budget).
+#ifndef ATTN_FWD_WAVES
+#define ATTN_FWD_WAVES 4
+#endif
+#ifndef ATTN_FWD_BLOCKS
+#define ATTN_FWD_BLOCKS 2
+#endif
+#ifndef ATTN_ASM_DMA
+#define ATTN_ASM_DMA 1
+#endif
+
 namespace mi {
 namespace {
 
@@ -338,15 +351,15 @@ struct KvLayout {
 };
 
 // Issue the direct loads of a 64-row tile (rows row0.., clamped to nrows-1).
-template <int D>
+template <int D, int NW = 4>
 __device__ __forceinline__ void kv_tile_issue(const char* g, int64_t rs_bytes, int64_t row0,
                                               int64_t nrows, char* dst) {
   typedef KvLayout<D> L;
   const int lane = threadIdx.x & 63, wave = wave_id();
   constexpr int INSTR = L::TILE / 1024;
 #pragma unroll
-  for (int it = 0; it < INSTR / 4; ++it) {
-    const int blk = it * 4 + wave;
+  for (int it = 0; it < INSTR / NW; ++it) {
+    const int blk = it * NW + wave;
     const int r = blk * L::RPI + lane / L::CH;
     const int chunk = (lane % L::CH) ^ L::swz(r);
     int64_t gr = row0 + r;
@@ -355,6 +368,11 @@ __device__ __forceinline__ void kv_tile_issue(const char* g, int64_t rs_bytes, i
                                      (lptr_t)(dst + blk * 1024), 16, 0, 0);
   }
 }
+
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
 
 // Fragment of 8 permuted keys for head-dim row `d`: slots 0-3 = keys
 // t0*16+4g+0..3, slots 4-7 = keys t1*16+4g+0..3 (g = lane/16).
@@ -374,8 +392,64 @@ __device__ __forceinline__ typename Mfma<T>::frag tr_frag(const char* tile, int 
   return f;
 }
 
-template <typename T, int D, bool POS>
-__global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_fwd_v2(AttnArgs p) {
+// K/V tile loader for the forward: each thread's chunk offsets within a
+// tile are fixed, so a tile costs one scalar row-offset product plus one
+// 64-bit add per load.  Rows past the end (only in the last tile) reload the
+// last row; their scores are masked.
+template <int D, int NW>
+struct KvTileLoad {
+  typedef KvLayout<D> L;
+  static constexpr int IT = L::TILE / 1024 / NW;  // 1 KB load instructions per thread
+  const char* g;
+  int64_t rs;
+  int64_t off[IT];   // r * rs + chunk * 16
+  int row[IT];       // r, the tile row this thread loads
+  int coff[IT];      // chunk * 16
+  __device__ __forceinline__ void init(const char* base, int64_t rs_bytes) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    g = base;
+    rs = rs_bytes;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int blk = it * NW + wave;
+      row[it] = blk * L::RPI + lane / L::CH;
+      coff[it] = ((lane % L::CH) ^ L::swz(row[it])) * 16;
+      off[it] = row[it] * rs + coff[it];
+    }
+  }
+  __device__ __forceinline__ void issue(int64_t row0, int64_t nrows, char* dst) const {
+    const int wave = wave_id();
+    if (row0 + 64 <= nrows) {
+      const char* tb = g + row0 * rs;
+#pragma unroll
+      for (int it = 0; it < IT; ++it) load(tb + off[it], dst + (it * NW + wave) * 1024);
+    } else {
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int64_t gr = min(row0 + row[it], nrows - 1);
+        load(g + gr * rs + coff[it], dst + (it * NW + wave) * 1024);
+      }
+    }
+  }
+  static __device__ __forceinline__ void load(const char* src, char* dst) {
+#if ATTN_ASM_DMA
+    dma_b128(src, lds_base_of(dst));
+#else
+    __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)dst, 16, 0, 0);
+#endif
+  }
+};
+
+// Forward step softmax (per 16-query tile, exp2 domain).  The running max m
+// is only a reference: it moves (and O, l are rescaled) when a row's max
+// exceeds it by more than kSlack, so most steps skip the rescale and p stays
+// below 2^kSlack.  Row sums l come from an extra MFMA of a ones fragment
+// against P (the same bf16 P that multiplies V).
+constexpr float kSlack = 8.f;
+
+template <typename T, int D, bool POS, int NW>
+__global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 1) attn_fwd_v2(AttnArgs p) {
+  constexpr int QPW = 128 / NW, QT = QPW / 16;  // queries per wave, 16-query tiles per wave
   typedef typename Mfma<T>::frag frag;
   typedef KvLayout<D> L;
   constexpr int KS = D / 32, DT = D / 16;
@@ -389,127 +463,138 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_fwd_v2(AttnArg
   const int64_t q0 = qblock * 128;
   const int64_t b = bc.b, h = bc.h;
   const T* Q = (const T*)p.q + b * p.q_b + h * p.q_h;
-  const char* K = (const char*)((const T*)p.k + b * p.k_b + h * p.k_h);
-  const char* V = (const char*)((const T*)p.v + b * p.v_b + h * p.v_h);
-  const int64_t ks_b = p.k_s * (int64_t)sizeof(T), vs_b = p.v_s * (int64_t)sizeof(T);
+  KvTileLoad<D, NW> kl, vl;
+  kl.init((const char*)((const T*)p.k + b * p.k_b + h * p.k_h), p.k_s * (int64_t)sizeof(T));
+  vl.init((const char*)((const T*)p.v + b * p.v_b + h * p.v_h), p.v_s * (int64_t)sizeof(T));
 
-  frag qf[2][KS];
+  frag qf[QT][KS];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+  for (int qt = 0; qt < QT; ++qt) {
+    const int64_t qi = q0 + wave * QPW + qt * 16 + lr;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
       qf[qt][ks] = qi < p.Sq ? *(const frag*)(Q + qi * p.q_s + ks * 32 + lg * 8) : zero_frag<T>();
   }
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  f32x4 oacc[DT][2];
+  frag ones;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) oacc[dt][0] = oacc[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
+  float m[QT];
+  f32x4 oacc[DT][QT], lacc[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m[qt] = -INFINITY;
+    lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   int64_t kv_end = p.Skv;
   if (p.causal) kv_end = min(p.Skv, q0 + 128);
-  kv_tile_issue<D>(K, ks_b, 0, p.Skv, lds);
-  kv_tile_issue<D>(V, vs_b, 0, p.Skv, lds + L::TILE);
+  kl.issue(0, p.Skv, lds);
+  vl.issue(0, p.Skv, lds + L::TILE);
   const int sw = L::swz(lr);  // fragment rows kt*16 + lr share the swizzle of lr
+  const float c = p.scale_log2;
   int buf = 0;
   for (int64_t kb0 = 0; kb0 < kv_end; kb0 += 64) {
     __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
     __syncthreads();
     if (kb0 + 64 < kv_end) {
       char* nx = lds + (buf ^ 1) * STAGE;
-      kv_tile_issue<D>(K, ks_b, kb0 + 64, p.Skv, nx);
-      kv_tile_issue<D>(V, vs_b, kb0 + 64, p.Skv, nx + L::TILE);
+      kl.issue(kb0 + 64, p.Skv, nx);
+      vl.issue(kb0 + 64, p.Skv, nx + L::TILE);
     }
     const char* Kt = lds + buf * STAGE;
     const char* Vt = Kt + L::TILE;
-
-    f32x4 s[4][2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      frag kf[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        kf[ks] = *(const frag*)(Kt + (kt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4));
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        f32x4 a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) a = Mfma<T>::mma(kf[ks], qf[qt][ks], a);
-        s[kt][qt] = a;
-      }
-    }
-    // Online softmax in the exp2 domain.  With a positive scale the row max
-    // is taken on the raw scores and p = 2^(s*c - m) is one FMA + one exp;
-    // each lane keeps a partial row sum (its 16 keys per tile) under the
-    // shared max, summed across the four lane groups once at the end.  O is
-    // rescaled only when some row's max grew.
-    const bool need_mask = (kb0 + 64 > p.Skv) || (p.causal && kb0 + 64 > q0 + wave * 32);
-    const float c = p.scale_log2;
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      int lim = 63;  // keys kb0 + 0..lim are visible to this lane's query
-      if (need_mask) {
-        const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
-        int64_t lm = p.Skv - 1 - kb0;
-        if (p.causal && qi - kb0 < lm) lm = qi - kb0;
-        lim = (int)max((int64_t)-1, min((int64_t)63, lm));
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float v = POS ? s[kt][qt][e] : s[kt][qt][e] * c;
-          if (need_mask && kt * 16 + lg * 4 + e > lim) v = -INFINITY;
-          s[kt][qt][e] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = group_max(mx);
-      const float m_new = fmaxf(m[qt], POS ? mx * c : mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      float rs = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pv = fast_exp2(POS ? fmaf(s[kt][qt][e], c, -m_use) : s[kt][qt][e] - m_use);
-          s[kt][qt][e] = pv;
-          rs += pv;
-        }
-      const float alpha = fast_exp2(m[qt] - m_use);
-      l[qt] = l[qt] * alpha + rs;
-      m[qt] = m_new;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
-      }
-    }
-#pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
-      frag pf[2];
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pf[qt][e] = (T)s[2 * ks2][qt][e];
-          pf[qt][4 + e] = (T)s[2 * ks2 + 1][qt][e];
-        }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const frag vf = tr_frag<T, D>(Vt, dt, 2 * ks2, 2 * ks2 + 1);
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = Mfma<T>::mma(vf, pf[qt], oacc[dt][qt]);
-      }
-    }
     buf ^= 1;
+
+    // The step is instantiated with and without masking (uniform branch), so
+    // tiles inside the sequence and off the causal diagonal run no mask code.
+    auto step = [&](auto mask_tag) {
+      constexpr bool MASK = decltype(mask_tag)::value;
+      f32x4 s[4][QT];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        frag kf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          kf[ks] = *(const frag*)(Kt + (kt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4));
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) a = Mfma<T>::mma(kf[ks], qf[qt][ks], a);
+          s[kt][qt] = a;
+        }
+      }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        int lim = 63;  // keys kb0 + 0..lim are visible to this lane's query
+        if constexpr (MASK) {
+          const int64_t qi = q0 + wave * QPW + qt * 16 + lr;
+          int64_t lm = p.Skv - 1 - kb0;
+          if (p.causal && qi - kb0 < lm) lm = qi - kb0;
+          lim = (int)max((int64_t)-1, min((int64_t)63, lm));
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = POS ? s[kt][qt][e] : s[kt][qt][e] * c;
+            if (MASK && kt * 16 + lg * 4 + e > lim) v = -INFINITY;
+            s[kt][qt][e] = v;
+            mx = fmaxf(mx, v);
+          }
+        mx = group_max(mx);
+        const float mxc = POS ? mx * c : mx;
+        if (__builtin_amdgcn_ballot_w64(mxc > m[qt] + kSlack)) {
+          const float m_new = fmaxf(m[qt], mxc);
+          const float alpha = fast_exp2(m[qt] - m_new);
+          lacc[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
+          m[qt] = m_new;
+        }
+        const float m_use = m[qt] == -INFINITY ? 0.f : m[qt];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            s[kt][qt][e] = fast_exp2(POS ? fmaf(s[kt][qt][e], c, -m_use) : s[kt][qt][e] - m_use);
+      }
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        frag pf[QT];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pf[qt][e] = (T)s[2 * ks2][qt][e];
+            pf[qt][4 + e] = (T)s[2 * ks2 + 1][qt][e];
+          }
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) lacc[qt] = Mfma<T>::mma(ones, pf[qt], lacc[qt]);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const frag vf = tr_frag<T, D>(Vt, dt, 2 * ks2, 2 * ks2 + 1);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) oacc[dt][qt] = Mfma<T>::mma(vf, pf[qt], oacc[dt][qt]);
+        }
+      }
+    };
+    const bool need_mask = (kb0 + 64 > p.Skv) || (p.causal && kb0 + 64 > q0 + wave * QPW);
+    if (need_mask) step(BoolTag<true>{});
+    else step(BoolTag<false>{});
   }
 
+  // every element of lacc[qt] holds query lr's full row sum
+  float l[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) l[qt] = lacc[qt][0];
   T* O = (T*)p.o + b * p.o_b + h * p.o_h;
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) l[qt] = group_sum(l[qt]);
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int64_t qi = q0 + wave * 32 + qt * 16 + lr;
+  for (int qt = 0; qt < QT; ++qt) {
+    const int64_t qi = q0 + wave * QPW + qt * 16 + lr;
     if (qi >= p.Sq) continue;
     const float inv = l[qt] > 0.f ? 1.f / l[qt] : 0.f;
 #pragma unroll
@@ -1061,8 +1146,9 @@ template <typename T, int D>
 int fwd_launch(const AttnArgs& a, hipStream_t s) {
   dim3 grid(ceil_div(a.Sq, 128), (unsigned)a.H, (unsigned)a.B);
   if constexpr (D == 64 || D == 128) {
-    if (a.scale_log2 > 0.f) attn_fwd_v2<T, D, true><<<grid, kThreads, 0, s>>>(a);
-    else attn_fwd_v2<T, D, false><<<grid, kThreads, 0, s>>>(a);
+    constexpr int NW = D == 64 ? ATTN_FWD_WAVES : 4;
+    if (a.scale_log2 > 0.f) attn_fwd_v2<T, D, true, NW><<<grid, 64 * NW, 0, s>>>(a);
+    else attn_fwd_v2<T, D, false, NW><<<grid, 64 * NW, 0, s>>>(a);
   }
   else if (a.scale_log2 > 0.f) attn_fwd_kernel<T, D, true><<<grid, kThreads, 0, s>>>(a);
   else attn_fwd_kernel<T, D, false><<<grid, kThreads, 0, s>>>(a);

@@ -140,8 +140,6 @@ __global__ void __launch_bounds__(256) rowsum_reduce(GemmArgs g, int slots, int6
   }
 }
 
-typedef const void __attribute__((address_space(1)))* gptr_t;
-typedef void __attribute__((address_space(3)))* lptr_t;
 
 // k-contiguous operand tile: ROWS rows x 64 k, loaded by NT threads.  Thread
 // (wave w, lane l) handles rows r = 8*(it*WAVES + w) + l/8; with WAVES even
@@ -175,8 +173,7 @@ struct TileLoad {
     const int64_t koff = (KT && k0_bytes + chunk * 16 >= kend_bytes) ? k0_bytes - chunk * 16 : k0_bytes;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it)
-      __builtin_amdgcn_global_load_lds((gptr_t)(src[it] + koff), (lptr_t)(dst + (it * WAVES + wave) * 1024), 16,
-                                       0, 0);
+      dma_b128(src[it] + koff, lds_base_of(dst + (it * WAVES + wave) * 1024));
   }
 };
 
@@ -223,8 +220,7 @@ struct TileLoadT {
     for (int it = 0; it < ITERS; ++it) {
       int64_t k = k0 + kr[it];
       if (KT && k >= kend) k = kend - 1;
-      __builtin_amdgcn_global_load_lds((gptr_t)(base + k * ld + col_off[it]),
-                                       (lptr_t)(dst + (it * WAVES + wave) * 1024), 16, 0, 0);
+      dma_b128(base + k * ld + col_off[it], lds_base_of(dst + (it * WAVES + wave) * 1024));
     }
   }
 };
@@ -250,29 +246,25 @@ struct OperandLoad<ROWS, NT, false> {
   }
 };
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-// MFMA fragment (rows r0..r0+15, k = ks*32 + 8g + 0..7) from an m/n-
-// contiguous tile with two transposing reads: within a 16-lane group, lane i
-// receives element i%4 of the 4-element pieces of lanes i/4, 4+i/4, 8+i/4,
-// 12+i/4, so source lane 4e+q supplies k-row (.. + e), columns r0+4q..+3.
-template <typename T, int ROWS>
-__device__ __forceinline__ typename Mfma<T>::frag mn_frag(const char* tile, int r0, int ks) {
+// CNT MFMA fragments (rows r0 + 16i .. +15, k = ks*32 + 8g + 0..7) from an
+// m/n-contiguous tile, two transposing reads each: within a 16-lane group,
+// lane i receives element i%4 of the 4-element pieces of lanes i/4, 4+i/4,
+// 8+i/4, 12+i/4, so source lane 4e+q supplies k-row (.. + e), columns
+// r0+4q..+3.
+template <typename T, int ROWS, int CNT>
+__device__ __forceinline__ void mn_frags(const char* tile, int r0, int ks, typename Mfma<T>::frag (&f)[CNT]) {
   constexpr int ROWB = ROWS * 2;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, src = lane & 15;
-  const int m = r0 + 4 * (src & 3);
   const int k1 = ks * 32 + 8 * g + (src >> 2), k2 = k1 + 4;
-  const int o1 = k1 * ROWB + (((m >> 3) ^ kswz(k1)) << 4) + ((m & 7) << 1);
-  const int o2 = k2 * ROWB + (((m >> 3) ^ kswz(k2)) << 4) + ((m & 7) << 1);
-  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + o1));
-  s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + o2));
-  typename Mfma<T>::frag f;
-  short* fs = (short*)&f;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) fs[e] = a[e], fs[4 + e] = b[e];
-  return f;
+  for (int i = 0; i < CNT; ++i) {
+    const int m = r0 + i * 16 + 4 * (src & 3);
+    const s16x4 a = ds_read_tr(tile + k1 * ROWB + (((m >> 3) ^ kswz(k1)) << 4) + ((m & 7) << 1));
+    const s16x4 b = ds_read_tr(tile + k2 * ROWB + (((m >> 3) ^ kswz(k2)) << 4) + ((m & 7) << 1));
+    f[i] = join_frag<typename Mfma<T>::frag>(a, b);
+  }
 }
 
 // Zero the fragment slots whose k index (kbase + slot) is >= kend.
@@ -430,18 +422,19 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
       if (RS && ++rs_q == rs_slots) rs_q = 0;
       const int coff = ((ks * 4 + lg) ^ sw) * 16;
       const int64_t kfrag = k0 + ks * 32 + lg * 8;
-      frag bfr[TN];
+      frag bfr[TN], afr[A_K ? 1 : TM];
+      if constexpr (!B_K) mn_frags<T, BN, TN>(bt, wn * WN, ks, bfr);
+      if constexpr (!A_K) mn_frags<T, BM, TM>(at, wm * WM, ks, afr);
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         if constexpr (B_K) bfr[j] = *(const frag*)(bt + (wn * WN + j * 16 + lr) * 128 + coff);
-        else bfr[j] = mn_frag<T, BN>(bt, wn * WN + j * 16, ks);
         if (tail) mask_k(bfr[j], kfrag, kend);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         frag af;
         if constexpr (A_K) af = *(const frag*)(at + (wm * WM + i * 16 + lr) * 128 + coff);
-        else af = mn_frag<T, BM>(at, wm * WM + i * 16, ks);
+        else af = afr[i];
         if (tail) mask_k(af, kfrag, kend);
         if (RS && rs_now) rsum[i] = Mfma<T>::mma(af, ones, rsum[i]);
 #pragma unroll

@@ -23,6 +23,47 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 // (masked-off) VALU set-up never ran.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Byte offset of a shared-memory pointer within the block's LDS.
+__device__ __forceinline__ unsigned lds_off(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Direct global -> LDS loads (global_load_lds_dword{,x4}: each lane's 4 or 16
+// bytes land at lds_base + 4/16 * lane), issued from inline assembly.  The
+// builtin form is not used because the compiler then treats every later
+// transposing LDS read as a possible reader of the in-flight load and puts a
+// vmcnt(0) in front of it, so a pipeline that issues the next tiles before
+// reading the current one would wait for its newest loads on every step.
+// Callers wait for these loads themselves (explicit vmcnt waits + barriers).
+// lds_base must be wave-uniform; it is written to M0 here.
+__device__ __forceinline__ void dma_b128(const void* gptr, unsigned lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b32(const void* gptr, unsigned lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(gptr), "s"(lds_base) : "memory", "m0");
+}
+// Wave-uniform LDS byte offset of a shared-memory pointer.
+__device__ __forceinline__ unsigned lds_base_of(const void* p) { return __builtin_amdgcn_readfirstlane(lds_off(p)); }
+
+// Transposing 8-byte LDS read (ds_read_b64_tr_b16).
+__device__ __forceinline__ s16x4 ds_read_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+}
+
+// Fragment from two transposed 4-element pieces: slots 0-3 = a, 4-7 = b.
+template <typename F>
+__device__ __forceinline__ F join_frag(s16x4 a, s16x4 b) {
+  F f;
+  short* fs = (short*)&f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) fs[e] = a[e], fs[4 + e] = b[e];
+  return f;
+}
+
 template <typename T>
 struct Mfma;
 
