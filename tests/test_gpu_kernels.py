@@ -62,6 +62,22 @@ def test_map_binary_broadcast_exact(kernels, op, fn):
     assert torch.equal(host(out), fn(a, b).to(out_dt))
 
 
+@pytest.mark.parametrize("op,fn", [(0, lambda a, b: a + 0.5 * b), (1, lambda a, b: a - 0.5 * b),
+                                   (2, lambda a, b: a * b), (3, lambda a, b: a / b)])
+@pytest.mark.parametrize("ydt", [torch.float32, torch.bfloat16])
+def test_map_row_broadcast_fast_path(kernels, op, fn, ydt):
+    """x [5, 6, 64] (op) y [6, 64] broadcast over the leading dim: the dense
+    row-broadcast kernel (a position embedding added to every sequence)."""
+    a, b = randn(5, 6, 64), randn(6, 64).to(ydt)
+    ta, tb = dev(a), dev(b)
+    out = torch.empty(5, 6, 64, device="cuda")
+    ins = (ctypes.c_void_p * 3)(p(ta), p(tb), None)
+    dts = (ctypes.c_int * 3)(0, CODE[ydt], 0)
+    call("mi355x_map", op, p(out), 0, 2, ins, dts, i64(384, 64, 1, 384, 64, 1, 0, 64, 1), i64(5, 6, 64), 3,
+         0.5, 0.0, None)
+    assert torch.equal(host(out), fn(a, b.float()))
+
+
 def test_map_scalar_operand_and_integer_math(kernels):
     x = torch.arange(-20, 20, dtype=torch.int64)
     tx = dev(x)

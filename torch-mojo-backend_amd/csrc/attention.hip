@@ -369,6 +369,8 @@ __device__ __forceinline__ void kv_tile_issue(const char* g, int64_t rs_bytes, i
   }
 }
 
+__host__ __device__ inline int64_t ceil_div64(int64_t a, int64_t b) { return a <= 0 ? 0 : (a + b - 1) / b; }
+
 template <bool B>
 struct BoolTag {
   static constexpr bool value = B;
@@ -495,7 +497,13 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
   const int sw = L::swz(lr);  // fragment rows kt*16 + lr share the swizzle of lr
   const float c = p.scale_log2;
   int buf = 0;
-  for (int64_t kb0 = 0; kb0 < kv_end; kb0 += 64) {
+  // One step per 64 keys: the unmasked steps first, then the ones that
+  // cross this wave's causal diagonal or the key end.  Two loops, so the
+  // unmasked steps carry no mask code; every wave runs the same number of
+  // steps (and barriers).
+  auto step = [&](int64_t j, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int64_t kb0 = j * 64;
     __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
     __syncthreads();
     if (kb0 + 64 < kv_end) {
@@ -506,11 +514,6 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
     const char* Kt = lds + buf * STAGE;
     const char* Vt = Kt + L::TILE;
     buf ^= 1;
-
-    // The step is instantiated with and without masking (uniform branch), so
-    // tiles inside the sequence and off the causal diagonal run no mask code.
-    auto step = [&](auto mask_tag) {
-      constexpr bool MASK = decltype(mask_tag)::value;
       f32x4 s[4][QT];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
@@ -581,11 +584,13 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
           for (int qt = 0; qt < QT; ++qt) oacc[dt][qt] = Mfma<T>::mma(vf, pf[qt], oacc[dt][qt]);
         }
       }
-    };
-    const bool need_mask = (kb0 + 64 > p.Skv) || (p.causal && kb0 + 64 > q0 + wave * QPW);
-    if (need_mask) step(BoolTag<true>{});
-    else step(BoolTag<false>{});
-  }
+  };
+  const int64_t nkb = (kv_end + 63) / 64;
+  int64_t ju = min(nkb, p.Skv / 64);  // unmasked [0, ju), masked [ju, nkb)
+  if (p.causal) ju = min(ju, (q0 + wave * QPW) / 64);
+  int64_t j = 0;
+  for (; j < ju; ++j) step(j, BoolTag<false>{});
+  for (; j < nkb; ++j) step(j, BoolTag<true>{});
 
   // every element of lacc[qt] holds query lr's full row sum
   float l[QT];
@@ -901,7 +906,14 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
   const int sw = L::swz(lr);
   int buf = 0;
   if (qstart < f.Sq) issue(qstart, lds);
-  for (int64_t qb0 = qstart; qb0 < f.Sq; qb0 += 64) {
+  // One step per 64 queries.  Masks are needed only where the tile crosses
+  // this wave's causal diagonal (the first steps), the query end (the last
+  // step) or the key end (every step); the steps are split into three loops
+  // (masked, unmasked, masked) so the unmasked ones carry no mask code.  All
+  // waves run the same number of steps, hence of barriers.
+  auto step = [&](int64_t j, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int64_t qb0 = qstart + j * 64;
     __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
     __syncthreads();
     if (qb0 + 64 < f.Sq) issue(qb0 + 64, lds + (buf ^ 1) * STAGE);
@@ -910,74 +922,83 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
     const float* lse_s = (const float*)(Qt + 2 * L::TILE);
     const float* del_s = lse_s + 64;
     buf ^= 1;
-    if (f.causal && kw > qb0 + 63) continue;  // every key of this wave is after every query
-    // Masks only where the tile crosses the causal diagonal or an edge; then
-    // in 32-bit indices relative to the tile.
-    const bool need_mask = (qb0 + 64 > f.Sq) || (kw + 32 > f.Skv) || (f.causal && kw + 31 > qb0);
-    const int q_lim = (int)min((int64_t)64, f.Sq - qb0);   // query rows < q_lim exist
-    const int k_lim = (int)min((int64_t)32, f.Skv - kw);   // key rows < k_lim exist
-    const int kq = (int)max((int64_t)-128, min((int64_t)128, kw - qb0));  // key row 0 minus query row 0
-    const float c = f.scale_log2;
+    if (f.causal && kw > qb0 + 63) return;  // every key of this wave is after every query
+      const int q_lim = (int)min((int64_t)64, f.Sq - qb0);   // query rows < q_lim exist
+      const int k_lim = (int)min((int64_t)32, f.Skv - kw);   // key rows < k_lim exist
+      const int kq = (int)max((int64_t)-128, min((int64_t)128, kw - qb0));  // key row 0 minus query row 0
+      const float c = f.scale_log2;
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      f32x4 pt[2][2], ds[2][2];  // [query tile in pair][key tile]
+      for (int qs = 0; qs < 2; ++qs) {
+        f32x4 pt[2][2], ds[2][2];  // [query tile in pair][key tile]
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int qt = 2 * qs + u;
-        frag qa[KS], da[KS];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int off = (qt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4);
-          qa[ks] = *(const frag*)(Qt + off);
-          da[ks] = *(const frag*)(dOt + off);
-        }
-        const float4 l4 = *(const float4*)(lse_s + qt * 16 + 4 * lg);
-        const float4 d4 = *(const float4*)(del_s + qt * 16 + 4 * lg);
-        const float lv[4] = {l4.x * kLog2e, l4.y * kLog2e, l4.z * kLog2e, l4.w * kLog2e};
-        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < 2; ++u) {
+          const int qt = 2 * qs + u;
+          frag qa[KS], da[KS];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
-            sa = Mfma<T>::mma(qa[ks], kf[t][ks], sa);
-            pa = Mfma<T>::mma(da[ks], vf[t][ks], pa);
+            const int off = (qt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4);
+            qa[ks] = *(const frag*)(Qt + off);
+            da[ks] = *(const frag*)(dOt + off);
           }
-          const int kr = t * 16 + lr;
+          const float4 l4 = *(const float4*)(lse_s + qt * 16 + 4 * lg);
+          const float4 d4 = *(const float4*)(del_s + qt * 16 + 4 * lg);
+          const float lv[4] = {l4.x * kLog2e, l4.y * kLog2e, l4.z * kLog2e, l4.w * kLog2e};
+          const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              sa = Mfma<T>::mma(qa[ks], kf[t][ks], sa);
+              pa = Mfma<T>::mma(da[ks], vf[t][ks], pa);
+            }
+            const int kr = t * 16 + lr;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float pv = fast_exp2(fmaf(sa[e], c, -lv[e]));
+              if constexpr (MASK) {
+                const int qr = qt * 16 + 4 * lg + e;
+                if (qr >= q_lim || kr >= k_lim || (f.causal && kq + kr > qr)) pv = 0.f;
+              }
+              pt[u][t][e] = pv;
+              ds[u][t][e] = pv * (pa[e] - dv[e]);
+            }
+          }
+        }
+        frag pb[2], sb[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            float pv = fast_exp2(fmaf(sa[e], c, -lv[e]));
-            if (need_mask) {
-              const int qr = qt * 16 + 4 * lg + e;
-              if (qr >= q_lim || kr >= k_lim || (f.causal && kq + kr > qr)) pv = 0.f;
-            }
-            pt[u][t][e] = pv;
-            ds[u][t][e] = pv * (pa[e] - dv[e]);
+            pb[t][e] = (T)pt[0][t][e];
+            pb[t][4 + e] = (T)pt[1][t][e];
+            sb[t][e] = (T)ds[0][t][e];
+            sb[t][4 + e] = (T)ds[1][t][e];
+          }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const frag dof = tr_frag<T, D>(dOt, dt, 2 * qs, 2 * qs + 1);
+          const frag qtf = tr_frag<T, D>(Qt, dt, 2 * qs, 2 * qs + 1);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            dva[dt][t] = Mfma<T>::mma(dof, pb[t], dva[dt][t]);
+            dka[dt][t] = Mfma<T>::mma(qtf, sb[t], dka[dt][t]);
           }
         }
       }
-      frag pb[2], sb[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pb[t][e] = (T)pt[0][t][e];
-          pb[t][4 + e] = (T)pt[1][t][e];
-          sb[t][e] = (T)ds[0][t][e];
-          sb[t][4 + e] = (T)ds[1][t][e];
-        }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const frag dof = tr_frag<T, D>(dOt, dt, 2 * qs, 2 * qs + 1);
-        const frag qtf = tr_frag<T, D>(Qt, dt, 2 * qs, 2 * qs + 1);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          dva[dt][t] = Mfma<T>::mma(dof, pb[t], dva[dt][t]);
-          dka[dt][t] = Mfma<T>::mma(qtf, sb[t], dka[dt][t]);
-        }
-      }
-    }
+  };
+  const int64_t nqb = qstart < f.Sq ? (f.Sq - qstart + 63) / 64 : 0;
+  int64_t j1 = 0, j2 = nqb;  // masked [0, j1), unmasked [j1, j2), masked [j2, nqb)
+  if (kw + 32 > f.Skv) {
+    j1 = nqb;
+  } else {
+    if (f.causal) j1 = min(nqb, max((int64_t)0, ceil_div64(kw + 31 - qstart, 64)));
+    j2 = max(j1, min(nqb, (f.Sq - qstart) / 64));
   }
+  int64_t j = 0;
+  for (; j < j1; ++j) step(j, BoolTag<true>{});
+  for (; j < j2; ++j) step(j, BoolTag<false>{});
+  for (; j < nqb; ++j) step(j, BoolTag<true>{});
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int64_t kj = kw + t * 16 + lr;
@@ -1044,7 +1065,12 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
   int buf = 0;
   kv_tile_issue<D>(K, ks_b, 0, f.Skv, lds);
   kv_tile_issue<D>(V, vs_b, 0, f.Skv, lds + L::TILE);
-  for (int64_t kb0 = 0; kb0 < kv_end; kb0 += 64) {
+  // One step per 64 keys: unmasked steps first, then the ones that cross
+  // this wave's causal diagonal or the key end (or all of them when the
+  // wave's queries cross the query end); same step count on every wave.
+  auto step = [&](int64_t j, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int64_t kb0 = j * 64;
     __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
     __syncthreads();
     if (kb0 + 64 < kv_end) {
@@ -1055,61 +1081,69 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
     const char* Kt = lds + buf * STAGE;
     const char* Vt = Kt + L::TILE;
     buf ^= 1;
-    if (f.causal && kb0 > qw + 31) continue;  // every key after every query of this wave
-    const bool need_mask = (kb0 + 64 > f.Skv) || (qw + 32 > f.Sq) || (f.causal && kb0 + 63 > qw);
-    const int q_lim = (int)min((int64_t)32, f.Sq - qw);    // query rows < q_lim exist
-    const int k_lim = (int)min((int64_t)64, f.Skv - kb0);  // key rows < k_lim exist
-    const int qk = (int)max((int64_t)-128, min((int64_t)128, qw - kb0));  // query row 0 minus key row 0
-    const float c = f.scale_log2;
+    if (f.causal && kb0 > qw + 31) return;  // every key after every query of this wave
+      const int q_lim = (int)min((int64_t)32, f.Sq - qw);    // query rows < q_lim exist
+      const int k_lim = (int)min((int64_t)64, f.Skv - kb0);  // key rows < k_lim exist
+      const int qk = (int)max((int64_t)-128, min((int64_t)128, qw - kb0));  // query row 0 minus key row 0
+      const float c = f.scale_log2;
 #pragma unroll
-    for (int ks2 = 0; ks2 < 2; ++ks2) {
-      f32x4 ds[2][2];  // [key tile in pair][query tile]
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        f32x4 ds[2][2];  // [key tile in pair][query tile]
 #pragma unroll
-      for (int v2 = 0; v2 < 2; ++v2) {
-        const int kt = 2 * ks2 + v2;
-        frag ka[KS], va[KS];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int off = (kt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4);
-          ka[ks] = *(const frag*)(Kt + off);
-          va[ks] = *(const frag*)(Vt + off);
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+        for (int v2 = 0; v2 < 2; ++v2) {
+          const int kt = 2 * ks2 + v2;
+          frag ka[KS], va[KS];
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) {
-            sa = Mfma<T>::mma(ka[ks], qf[u][ks], sa);
-            pa = Mfma<T>::mma(va[ks], df[u][ks], pa);
+            const int off = (kt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4);
+            ka[ks] = *(const frag*)(Kt + off);
+            va[ks] = *(const frag*)(Vt + off);
           }
-          const int qr = u * 16 + lr;
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+              sa = Mfma<T>::mma(ka[ks], qf[u][ks], sa);
+              pa = Mfma<T>::mma(va[ks], df[u][ks], pa);
+            }
+            const int qr = u * 16 + lr;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float pv = fast_exp2(fmaf(sa[e], c, -lse2[u]));
+              if constexpr (MASK) {
+                const int kr = kt * 16 + 4 * lg + e;
+                if (qr >= q_lim || kr >= k_lim || (f.causal && kr > qk + qr)) pv = 0.f;
+              }
+              ds[v2][u][e] = pv * (pa[e] - dlt[u]);
+            }
+          }
+        }
+        frag sb[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            float pv = fast_exp2(fmaf(sa[e], c, -lse2[u]));
-            if (need_mask) {
-              const int kr = kt * 16 + 4 * lg + e;
-              if (qr >= q_lim || kr >= k_lim || (f.causal && kr > qk + qr)) pv = 0.f;
-            }
-            ds[v2][u][e] = pv * (pa[e] - dlt[u]);
+            sb[u][e] = (T)ds[0][u][e];
+            sb[u][4 + e] = (T)ds[1][u][e];
           }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const frag ktf = tr_frag<T, D>(Kt, dt, 2 * ks2, 2 * ks2 + 1);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) dqa[dt][u] = Mfma<T>::mma(ktf, sb[u], dqa[dt][u]);
         }
       }
-      frag sb[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sb[u][e] = (T)ds[0][u][e];
-          sb[u][4 + e] = (T)ds[1][u][e];
-        }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const frag ktf = tr_frag<T, D>(Kt, dt, 2 * ks2, 2 * ks2 + 1);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) dqa[dt][u] = Mfma<T>::mma(ktf, sb[u], dqa[dt][u]);
-      }
-    }
+  };
+  const int64_t nkb = (kv_end + 63) / 64;
+  int64_t ju = 0;  // unmasked [0, ju), masked [ju, nkb)
+  if (qw + 32 <= f.Sq) {
+    ju = min(nkb, f.Skv / 64);
+    if (f.causal) ju = min(ju, qw < 63 ? (int64_t)0 : (qw - 63) / 64 + 1);
   }
+  int64_t j = 0;
+  for (; j < ju; ++j) step(j, BoolTag<false>{});
+  for (; j < nkb; ++j) step(j, BoolTag<true>{});
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const int64_t qi = qw + u * 16 + lr;

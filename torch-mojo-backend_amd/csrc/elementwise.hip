@@ -381,6 +381,32 @@ __global__ void __launch_bounds__(kThreads) binary_x4(int op, float* __restrict_
   }
 }
 
+// out = x (op) y with y one dense row of inner4 float4s broadcast over the
+// `outer` rows of x and out (a position embedding added to every sequence).
+template <typename TX, typename TY>
+__global__ void __launch_bounds__(kThreads) binary_x4_rows(int op, float* __restrict__ out, const TX* __restrict__ x,
+                                                           const TY* __restrict__ y, float alpha, int64_t inner4,
+                                                           int64_t outer) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < inner4; i += (int64_t)gridDim.x * kThreads) {
+    const float4 b = ld4<TY, float>(y, i);
+    for (int64_t o = blockIdx.y; o < outer; o += gridDim.y) {
+      const int64_t k = o * inner4 + i;
+      const float4 a = ld4<TX, float>(x, k);
+      float4 r;
+      if (op == MI355X_OP_ADD) {
+        r.x = a.x + alpha * b.x; r.y = a.y + alpha * b.y; r.z = a.z + alpha * b.z; r.w = a.w + alpha * b.w;
+      } else if (op == MI355X_OP_SUB) {
+        r.x = a.x - alpha * b.x; r.y = a.y - alpha * b.y; r.z = a.z - alpha * b.z; r.w = a.w - alpha * b.w;
+      } else if (op == MI355X_OP_MUL) {
+        r.x = a.x * b.x; r.y = a.y * b.y; r.z = a.z * b.z; r.w = a.w * b.w;
+      } else {
+        r.x = a.x / b.x; r.y = a.y / b.y; r.z = a.z / b.z; r.w = a.w / b.w;
+      }
+      ((float4*)out)[k] = r;
+    }
+  }
+}
+
 // Dense casts f32 <-> bf16, 8 elements per thread-iteration.
 __global__ void __launch_bounds__(kThreads) cast_f32_bf16(bf16* __restrict__ out,
                                                           const float* __restrict__ in,
@@ -621,6 +647,26 @@ extern "C" int mi355x_map(int op, void* out, int out_dtype, int nin, const void*
     else if (!xb) binary_x4<float, bf16><<<grid, kThreads, 0, s>>>(op, o, (const float*)ins[0], (const bf16*)ins[1], al, n / 4);
     else if (!yb) binary_x4<bf16, float><<<grid, kThreads, 0, s>>>(op, o, (const bf16*)ins[0], (const float*)ins[1], al, n / 4);
     else binary_x4<bf16, bf16><<<grid, kThreads, 0, s>>>(op, o, (const bf16*)ins[0], (const bf16*)ins[1], al, n / 4);
+    return check_launch("mi355x_map");
+  }
+  // y one dense row broadcast over the rows of a dense x and out
+  if (g.ndim == 2 && nin == 2 && ins[0] && ins[1] && out_dtype == MI355X_F32 && f32_or_bf16(in_dtypes[0]) &&
+      f32_or_bf16(in_dtypes[1]) && g.st[0][1] == 1 && g.st[1][1] == 1 && g.st[2][1] == 1 &&
+      g.st[0][0] == g.shape[1] && g.st[1][0] == g.shape[1] && g.st[2][0] == 0 && g.shape[1] % 4 == 0 &&
+      aligned(out, 16) && aligned(ins[0], 16) && aligned(ins[1], 16) &&
+      (op == MI355X_OP_ADD || op == MI355X_OP_SUB || op == MI355X_OP_MUL || op == MI355X_OP_DIV)) {
+    const int64_t inner4 = g.shape[1] / 4, outer = g.shape[0];
+    const unsigned gx = grid_for(inner4);
+    int64_t gy = 4096 / gx;
+    gy = gy < 1 ? 1 : (gy > outer ? outer : (gy > 65535 ? 65535 : gy));
+    const dim3 grid(gx, (unsigned)gy);
+    const float al = (float)s0;
+    float* o = (float*)out;
+    const bool xb = in_dtypes[0] == MI355X_BF16, yb = in_dtypes[1] == MI355X_BF16;
+    if (!xb && !yb) binary_x4_rows<float, float><<<grid, kThreads, 0, s>>>(op, o, (const float*)ins[0], (const float*)ins[1], al, inner4, outer);
+    else if (!xb) binary_x4_rows<float, bf16><<<grid, kThreads, 0, s>>>(op, o, (const float*)ins[0], (const bf16*)ins[1], al, inner4, outer);
+    else if (!yb) binary_x4_rows<bf16, float><<<grid, kThreads, 0, s>>>(op, o, (const bf16*)ins[0], (const float*)ins[1], al, inner4, outer);
+    else binary_x4_rows<bf16, bf16><<<grid, kThreads, 0, s>>>(op, o, (const bf16*)ins[0], (const bf16*)ins[1], al, inner4, outer);
     return check_launch("mi355x_map");
   }
   MapArgs a{};
