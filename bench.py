@@ -1,6 +1,6 @@
 """Benchmark: nanoGPT-124M eager training on the mojo device (one MI355X).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only all|model|sdpa|gemm|hbm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only all|model|sdpa|gemm|hbm|gemma]
 
 Prints ONE JSON line.  `value` is the whole-job training throughput in
 tokens/s of BASELINE config 3 (GPT-2 small, batch 16 x 1024 tokens, bf16
@@ -13,6 +13,9 @@ after W warmup steps.  Alongside it:
                 stream they run on), against 2.5 PFLOP/s dense bf16;
   gemm          config 2 sweep (M = 16384, fwd / dX / dW) TFLOP/s;
   hbm           HBM-bound kernels at config 3 shapes, GB/s vs 8 TB/s;
+  cfg4_prefill  report only: one Gemma-3-1B-shaped prefill (grouped-query
+                sliding-window/global attention at head_dim 256, RMSNorm,
+                GeGLU, RoPE; 1 x 4096 tokens, bf16), tokens/s and TFLOP/s;
   cpu_baseline  the same training step in f32 on the host's cores with
                 stock PyTorch CPU (the reference's oracle), on a bounded
                 sample (four 1 x 1024-token steps, about 15 s on 8 cores).
@@ -184,6 +187,48 @@ def bench_hbm(iters):
     return out
 
 
+def bench_gemma(iters):
+    """Config 4 (report only): one Gemma-3-1B-shaped prefill, bf16, 1 x 4096
+    uniform token ids, random N(0, 0.02) weights."""
+    from torch_mojo_backend.gemma3 import Gemma3, Gemma3Config
+
+    cfg = Gemma3Config()
+    t = 4096
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        torch.manual_seed(0)
+        model = Gemma3(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    nparams = sum(p.numel() for p in model.parameters())
+    model.to("mojo")
+    idx = torch.randint(0, cfg.vocab_size, (1, t), generator=torch.Generator().manual_seed(3)).to("mojo")
+
+    def run():
+        with torch.no_grad():
+            return model(idx)
+
+    ms = time_gpu(run, max(2, iters // 5), warmup=1)
+    # algorithmic work: GEMMs, attention (local: the window's keys; global: causal), tied lm_head
+    h, hk, d, c, ff = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.hidden, cfg.d_ff
+    per_layer = 2 * t * (c * h * d + 2 * c * hk * d + h * d * c + 3 * c * ff)
+    n_global = sum(1 for i in range(cfg.layers) if (i + 1) % cfg.global_every == 0)
+    local_keys = sum(min(i + 1, cfg.window) for i in range(t))
+    attn = 4 * h * d * (n_global * t * (t + 1) / 2 + (cfg.layers - n_global) * local_keys)
+    flop = cfg.layers * per_layer + attn + 2 * t * c * cfg.vocab_size
+    return {
+        "workload": "Gemma-3-1B-shaped prefill: 26 layers, d_model 1152, 4 q / 1 kv heads, head_dim 256, "
+                    "GeGLU 6912, RMSNorm, RoPE, window 512 local : global 5:1, vocab 262144; bf16, 1 x 4096 ids",
+        "params": nparams,
+        "ms_per_prefill": ms,
+        "tokens_per_s": t / (ms * 1e-3),
+        "tflop_per_prefill": flop / 1e12,
+        "tflops": flop / (ms * 1e-3) / 1e12,
+        "mfu": flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+    }
+
+
 def bench_copy(iters):
     """Calibration for HBM-counter reads: a plain 1 GiB device copy (1 GiB
     read + 1 GiB written per launch) through the library's copy kernel."""
@@ -228,7 +273,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--block", type=int, default=1024)
-    ap.add_argument("--only", default="all", choices=["all", "model", "sdpa", "gemm", "hbm", "copy"])
+    ap.add_argument("--only", default="all", choices=["all", "model", "sdpa", "gemm", "hbm", "copy", "gemma"])
     ap.add_argument("--iters", type=int, default=20, help="launches per kernel timing")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -251,6 +296,8 @@ def main():
         res["model"] = bench_model(args)
     if args.only == "copy":
         res["copy"] = bench_copy(args.iters)
+    if args.only in ("all", "gemma"):
+        res["cfg4_prefill"] = bench_gemma(args.iters)
     traffic = None
     tfile = ROOT / "profiles" / "attention_traffic.json"
     if tfile.exists():

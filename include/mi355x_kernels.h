@@ -230,6 +230,15 @@ int mi355x_embedding_bwd(void* grad_weight, const void* grad_out, int dtype,
 /* ---- layer norm (LayerNormForward normalization_forward_ops.mojo:118;
  *      LayerNormBackwardF32 normalization_backward_dx.mojo:190-388,
  *      normalization_backward_params.mojo:41-143) ---------------------- */
+/* RMSNorm forward over the last dim (rows x cols, contiguous):
+ * y = x / sqrt(mean(x^2) + eps) * weight, rstd[rows] f32.  weight (optional)
+ * is f32 or the input dtype.  The reference has no eager RMSNorm (its
+ * Gemma-3 path runs under torch.compile, demo_scripts/gemma3.py:11); this
+ * serves aten::rms_norm for the Gemma-3-shaped workload and follows
+ * fast_aten_native_layer_norm's contract (aten_fast.py:5248-5371) minus the
+ * mean and bias. */
+int mi355x_rms_norm_fwd(void* y, float* rstd, const void* x, const void* weight, int weight_dtype,
+                        int64_t rows, int64_t cols, double eps, int dtype, mi355x_stream_t stream);
 /* y = (x - mean)*rstd*gamma + beta over rows of `cols` contiguous elements.
  * gamma/beta may be NULL.  mean/rstd: f32 [rows]. */
 int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,
@@ -413,6 +422,20 @@ int mi355x_attn_fwd(void* o, const int64_t* o_bhs, float* lse, const void* q,
                     const int64_t* v_bhs, int64_t batch, int64_t heads,
                     int64_t sq, int64_t skv, int64_t d, double scale,
                     int causal, int dtype, mi355x_stream_t stream);
+/* The same forward with grouped-query K/V heads (heads % kv_heads == 0,
+ * query head h reads K/V head h / (heads / kv_heads); k_bhs/v_bhs index the
+ * kv_heads heads), a causal sliding window (window > 0: query i sees keys
+ * i-window+1 .. i) and head_dim 256 (forward only).  It serves the
+ * Gemma-3-shaped prefill, which the reference runs through its masked-math
+ * SDPA decomposition instead (aten_fast.py:9112-9123, :6869) and
+ * fast_fused_flash_attention_forward's contract otherwise
+ * (aten_fast.py:7533-7587).  mi355x_attn_fwd is this call with
+ * kv_heads = heads and window = 0. */
+int mi355x_attn_fwd_ex(void* o, const int64_t* o_bhs, float* lse, const void* q,
+                       const int64_t* q_bhs, const void* k, const int64_t* k_bhs,
+                       const void* v, const int64_t* v_bhs, int64_t batch, int64_t heads,
+                       int64_t kv_heads, int64_t sq, int64_t skv, int64_t d, double scale,
+                       int causal, int64_t window, int dtype, mi355x_stream_t stream);
 /* dQ, dK, dV (written, never accumulated).  workspace holds the f32 row
  * terms D_i = sum(dO*O) and f32 dQ partials. */
 int64_t mi355x_attn_bwd_workspace_bytes(int64_t batch, int64_t heads,

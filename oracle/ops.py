@@ -165,25 +165,43 @@ def embedding_backward_f32(grad_out, idx, num_weights, padding_idx=-1):
 # (flash_attention_fwd_kernels.mojo:885-963, flash_attention_bwd_kernels.mojo:
 # 13-26 math, 63-66 top-left causal, 1403-1404 natural-log LSE)
 # ---------------------------------------------------------------------------
-def _scores(q, k, scale, causal):
-    s = np.einsum("...id,...jd->...ij", _f64(q), _f64(k)) * scale
+def _kv_heads(q, x):
+    """Grouped-query attention: K/V with H_kv heads serve H_q = g*H_kv query
+    heads, query head h reading K/V head h // g (torch SDPA enable_gqa)."""
+    x = _f64(x)
+    hq, hk = np.asarray(q).shape[-3], x.shape[-3]
+    if hk == hq:
+        return x
+    assert hq % hk == 0, (hq, hk)
+    return np.repeat(x, hq // hk, axis=-3)
+
+
+def _scores(q, k, scale, causal, window=0):
+    s = np.einsum("...id,...jd->...ij", _f64(q), _kv_heads(q, k)) * scale
     if causal:
         sq, skv = s.shape[-2], s.shape[-1]
-        mask = np.arange(skv)[None, :] > np.arange(sq)[:, None]  # top-left
+        i, j = np.arange(sq)[:, None], np.arange(skv)[None, :]
+        mask = j > i  # top-left
+        if window:
+            mask = mask | (i - j >= window)  # sliding window: keys i-window+1 .. i
         s = np.where(mask, -np.inf, s)
     return s
 
 
-def sdpa_forward(q, k, v, scale=None, causal=False):
-    """(O, LSE) with LSE the natural-log row log-sum-exp."""
+def sdpa_forward(q, k, v, scale=None, causal=False, window=0):
+    """(O, LSE) with LSE the natural-log row log-sum-exp.  K/V may have fewer
+    heads than Q (grouped-query attention); `window` > 0 (causal only) keeps
+    keys i-window+1 .. i for query i, the sliding-window mask of the Gemma-3
+    shaped workload (which the reference runs through its masked-math
+    decomposition, aten_fast.py:9112-9123, :6869)."""
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d) if scale is None else scale
-    s = _scores(q, k, scale, causal)
+    s = _scores(q, k, scale, causal, window)
     m = s.max(-1, keepdims=True)
     e = np.exp(s - m)
     lse = (m + np.log(e.sum(-1, keepdims=True)))[..., 0]
     p = np.exp(s - lse[..., None])
-    return np.einsum("...ij,...jd->...id", p, _f64(v)), lse
+    return np.einsum("...ij,...jd->...id", p, _kv_heads(q, v)), lse
 
 
 def sdpa_backward(do, q, k, v, o, lse, scale=None, causal=False):
@@ -200,6 +218,21 @@ def sdpa_backward(do, q, k, v, o, lse, scale=None, causal=False):
     dq = scale * np.einsum("...ij,...jd->...id", ds, _f64(k))
     dk = scale * np.einsum("...ij,...id->...jd", ds, _f64(q))
     return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm — the Gemma-3-shaped workload's norm.  The reference has no eager
+# RMSNorm kernel; this follows torch.nn.functional.rms_norm:
+# y = x / sqrt(mean(x^2 over the last dim) + eps) * weight.
+# ---------------------------------------------------------------------------
+def rms_norm(x, weight=None, eps=1e-6):
+    """y over the last dim; returns (y, rstd)."""
+    x = _f64(x)
+    rstd = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+    y = x * rstd
+    if weight is not None:
+        y = y * _f64(weight)
+    return y, rstd[..., 0]
 
 
 # ---------------------------------------------------------------------------

@@ -499,6 +499,39 @@ class HostStandIn:
         dense(_val(lse), torch.float32, (B, H, Sq)).copy_(L)
         return 0
 
+    def mi355x_rms_norm_fwd(self, y, rstd, x, w, wdt, rows, cols, eps, dt, stream):
+        X = dense(_val(x), DT[dt], (rows, cols)).double()
+        r = torch.rsqrt((X * X).mean(-1) + eps)
+        Y = X * r[:, None]
+        if w:
+            Y = Y * dense(_val(w), DT[wdt], (cols,)).double()
+        dense(_val(y), DT[dt], (rows, cols)).copy_(Y.to(DT[dt]))
+        if rstd:
+            dense(_val(rstd), torch.float32, (rows,)).copy_(r.float())
+        return 0
+
+    def mi355x_attn_fwd_ex(self, o, obhs, lse, q, qbhs, k, kbhs, v, vbhs, B, H, Hk, Sq, Skv, D, scale, causal,
+                           window, dt, stream):
+        def t(p, st, h, s):
+            return view(_val(p), DT[dt], (B, h, s, D), (st[0], st[1], st[2], 1))
+
+        Q = t(q, qbhs, H, Sq).float()
+        K = t(k, kbhs, Hk, Skv).float().repeat_interleave(H // Hk, dim=1)
+        V = t(v, vbhs, Hk, Skv).float().repeat_interleave(H // Hk, dim=1)
+        S = Q @ K.transpose(-1, -2) * scale
+        if causal:
+            i = torch.arange(Sq)[:, None]
+            j = torch.arange(Skv)[None, :]
+            keep = j <= i
+            if window:
+                keep = keep & (i - j < window)
+            S = S.masked_fill(~keep, float("-inf"))
+        L = torch.logsumexp(S, -1)
+        P = torch.exp(S - L[..., None])
+        t(o, obhs, H, Sq).copy_(P @ V)
+        dense(_val(lse), torch.float32, (B, H, Sq)).copy_(L)
+        return 0
+
     def mi355x_attn_bwd_workspace_bytes(self, B, H, Sq, Skv, D):
         return 16
 

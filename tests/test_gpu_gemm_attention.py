@@ -279,3 +279,42 @@ def test_gemm_ex_round_and_rowsum(kernels, m, n, k, layout, batch):
     exp_rs = A.double().sum(2).numpy()
     tol_close(got_c.numpy(), exp_c, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what="C")
     tol_close(got_rs.numpy(), exp_rs, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what="rowsum")
+
+
+def _attn_fwd_ex(q, k, v, causal, window, scale=None):
+    B, H, Sq, D = q.shape
+    Hk, Skv = k.shape[1], k.shape[2]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    o = torch.empty(B, Sq, H, D, dtype=q.dtype, device="cuda").transpose(1, 2)
+    lse = torch.empty(B, H, Sq, device="cuda")
+    call("mi355x_attn_fwd_ex", p(o), bhs(o), p(lse), p(q), bhs(q), p(k), bhs(k), p(v), bhs(v),
+         B, H, Hk, Sq, Skv, D, scale, int(causal), window, CODE[q.dtype], None)
+    return o, lse
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("heads,kv_heads", [(4, 1), (4, 2), (2, 2)])
+@pytest.mark.parametrize("s,window", [(130, 0), (300, 7), (300, 64), (200, 200), (257, 100)])
+def test_attention_fwd_ex_gqa_window_matches_oracle(kernels, d, heads, kv_heads, s, window):
+    """Grouped K/V heads, causal sliding window and head_dim 256 (the
+    Gemma-3-shaped prefill): O and LSE against the oracle."""
+    q = randn(1, heads, s, d).bfloat16()
+    k = randn(1, kv_heads, s, d).bfloat16()
+    v = randn(1, kv_heads, s, d).bfloat16()
+    o, lse = _attn_fwd_ex(dev(q), dev(k), dev(v), True, window)
+    eo, el = O.sdpa_forward(q.double().numpy(), k.double().numpy(), v.double().numpy(), causal=True, window=window)
+    tol_close(np64(o), eo, atol=2e-2, rtol=2e-2, what=f"O d{d} h{heads}/{kv_heads} w{window}")
+    tol_close(np64(lse), el, atol=1e-2, rtol=1e-3, what="LSE")
+
+
+def test_attention_fwd_ex_rejects_bad_arguments(kernels):
+    q = dev(randn(1, 3, 64, 64).bfloat16())
+    k = dev(randn(1, 2, 64, 64).bfloat16())
+    o = torch.empty(1, 64, 3, 64, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    lse = torch.empty(1, 3, 64, device="cuda")
+    rc = lib().mi355x_attn_fwd_ex(p(o), bhs(o), p(lse), p(q), bhs(q), p(k), bhs(k), p(k), bhs(k),
+                                  1, 3, 2, 64, 64, 64, 0.125, 1, 0, CODE[torch.bfloat16], None)
+    assert rc != 0 and b"multiple of kv_heads" in lib().mi355x_last_error()
+    rc = lib().mi355x_attn_fwd_ex(p(o), bhs(o), p(lse), p(q), bhs(q), p(q), bhs(q), p(q), bhs(q),
+                                  1, 3, 3, 64, 64, 64, 0.125, 0, 16, CODE[torch.bfloat16], None)
+    assert rc != 0 and b"needs causal" in lib().mi355x_last_error()

@@ -397,3 +397,20 @@ def test_foreach_norm_and_apply(kernels):
     call("mi355x_foreach_apply", 2, ptrs_in, None, None, None, numels, len(sizes), 0, 0.0, p(coef), None)
     for t, x in zip(tx, xs):
         assert torch.equal(host(t), x * 0.25)
+
+
+@pytest.mark.parametrize("cols", [1152, 256, 100])
+@pytest.mark.parametrize("dtype,wdt", [(torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+                                        (torch.bfloat16, torch.bfloat16)])
+def test_rms_norm_fwd_matches_oracle(kernels, cols, dtype, wdt):
+    rows = 37
+    x = (randn(rows, cols) * 2.0).to(dtype)
+    w = (1.0 + 0.1 * randn(cols)).to(wdt)
+    y = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    tx, tw = dev(x), dev(w)  # held: a freed temporary's memory would be reused by the next allocation
+    call("mi355x_rms_norm_fwd", p(y), p(rstd), p(tx), p(tw), CODE[wdt], rows, cols, 1e-6, CODE[dtype], None)
+    ey, er = O.rms_norm(x.double().numpy(), w.double().numpy(), eps=1e-6)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    tol_close(np64(y), ey, atol=tol, rtol=tol, what="y")
+    tol_close(np64(rstd), er, atol=1e-6, rtol=1e-5, what="rstd")

@@ -164,3 +164,28 @@ def test_fused_linear_under_autocast_gpu(mojo, shape, bias, strided):
     assert torch.allclose(wm.grad.cpu(), edw, atol=5e-2, rtol=2e-2)
     if bias:
         assert torch.allclose(bm.grad.cpu(), edb, atol=5e-2, rtol=2e-2)
+
+
+def test_gemma_shaped_prefill_matches_cpu(mojo):
+    """Gemma-3-shaped prefill (grouped-query windowed and global attention at
+    head_dim 256, RMSNorm, GeGLU, RoPE) in bf16 on the device against the same
+    bf16-rounded weights in f32 on the CPU."""
+    from torch_mojo_backend.gemma3 import Gemma3, Gemma3Config
+
+    cfg = Gemma3Config(vocab_size=512, hidden=256, layers=4, heads=4, kv_heads=1, head_dim=256, d_ff=512,
+                       window=40, global_every=2)
+    torch.manual_seed(0)
+    ref = Gemma3(cfg)
+    for _, prm in ref.named_parameters():
+        if prm.dim() == 1:
+            torch.nn.init.normal_(prm, std=0.1)
+    ref = ref.to(torch.bfloat16).float()
+    model = Gemma3(cfg)
+    model.load_state_dict(ref.state_dict())
+    model = model.to(torch.bfloat16).to("mojo")
+    idx = torch.randint(0, cfg.vocab_size, (1, 200), generator=torch.Generator().manual_seed(2))
+    with torch.no_grad():
+        got = model(idx.to("mojo")).float().cpu()
+        want = ref(idx)
+    err = (got - want).abs().max().item()
+    assert err <= 5e-2 * want.abs().max().item() + 5e-2, err

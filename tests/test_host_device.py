@@ -194,3 +194,85 @@ def test_fused_linear_under_autocast(mojo, shape, bias, strided):
     assert torch.allclose(wm.grad.cpu(), edw, atol=2e-2, rtol=2e-2)
     if bias:
         assert torch.allclose(bm.grad.cpu(), edb, atol=2e-2, rtol=2e-2)
+
+
+def _counting_library():
+    """Wrap the active kernel library so calls are counted by entry point."""
+    import collections
+
+    from torch_mojo_backend import eager_kernels as ek
+
+    inner = ek.lib()
+    calls = collections.Counter()
+
+    class Counting:
+        def __getattr__(self, name):
+            fn = getattr(inner, name)
+
+            def wrapped(*a, **k):
+                calls[name] += 1
+                return fn(*a, **k)
+
+            return wrapped
+
+    return inner, Counting(), calls
+
+
+def test_window_mask_tag_and_gqa_route(mojo):
+    from torch_mojo_backend import eager_kernels as ek
+    from torch_mojo_backend.masks import sliding_window_causal_mask, window_of
+
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(1, 4, 10, 64, generator=g).bfloat16()
+    k, v = (torch.randn(1, 2, 10, 64, generator=g).bfloat16() for _ in range(2))
+    mask = sliding_window_causal_mask(10, 3)
+    assert window_of(mask) == 3
+    inner, counting, calls = _counting_library()
+    ek.set_library_for_tests(counting)
+    try:
+        with torch.no_grad():
+            out = F.scaled_dot_product_attention(q.to("mojo"), k.to("mojo"), v.to("mojo"), attn_mask=mask,
+                                                 enable_gqa=True)
+        assert calls["mi355x_attn_fwd_ex"] == 1
+        ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), attn_mask=mask.cpu(), enable_gqa=True)
+        assert torch.allclose(out.float().cpu(), ref, atol=2e-2, rtol=2e-2)
+        mask[0, 0] = False  # an in-place edit voids the tag: the math path takes it
+        assert window_of(mask) is None
+        with torch.no_grad():
+            F.scaled_dot_product_attention(q.to("mojo"), k.to("mojo"), v.to("mojo"), attn_mask=mask,
+                                           enable_gqa=True)
+        assert calls["mi355x_attn_fwd_ex"] == 1
+    finally:
+        ek.set_library_for_tests(inner)
+
+
+def test_gemma_shaped_prefill_on_device(mojo):
+    """A small Gemma-3-shaped model (GQA, sliding window, RMSNorm, GeGLU,
+    RoPE) in bf16 on the device against the same weights in f32 on the CPU;
+    the windowed/grouped attention and RMSNorm go through their kernels."""
+    from torch_mojo_backend import eager_kernels as ek
+    from torch_mojo_backend.gemma3 import Gemma3, Gemma3Config
+
+    cfg = Gemma3Config(vocab_size=97, hidden=64, layers=3, heads=4, kv_heads=1, head_dim=64, d_ff=96,
+                       window=5, global_every=3)
+    torch.manual_seed(0)
+    ref = Gemma3(cfg)
+    for _, prm in ref.named_parameters():
+        if prm.dim() == 1:
+            torch.nn.init.normal_(prm, std=0.1)
+    ref = ref.to(torch.bfloat16).float()  # the bf16-rounded weights, in f32
+    model = Gemma3(cfg)
+    model.load_state_dict(ref.state_dict())
+    model = model.to(torch.bfloat16).to("mojo")
+    idx = torch.randint(0, 97, (2, 12), generator=torch.Generator().manual_seed(1))
+    inner, counting, calls = _counting_library()
+    ek.set_library_for_tests(counting)
+    try:
+        with torch.no_grad():
+            got = model(idx.to("mojo")).float().cpu()
+    finally:
+        ek.set_library_for_tests(inner)
+    with torch.no_grad():
+        want = ref(idx)
+    assert calls["mi355x_attn_fwd_ex"] == 3 and calls["mi355x_rms_norm_fwd"] >= 3 * 6 + 1
+    assert torch.allclose(got, want, atol=5e-2, rtol=5e-2), (got - want).abs().max()

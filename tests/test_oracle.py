@@ -202,6 +202,51 @@ def test_sdpa_special_cases_and_brute_force():
     close(lsec, lse_bf, rtol=1e-12, atol=1e-14)
 
 
+def test_sdpa_window_and_gqa_brute_force():
+    """Sliding-window causal attention with grouped-query heads (the
+    Gemma-3-shaped workload) against explicit loops: query head h reads K/V
+    head h // g; query i sees keys max(0, i-w+1) .. i."""
+    rng = np.random.default_rng(9)
+    hq, hk, t, d, w = 4, 2, 9, 4, 3
+    q = rng.normal(size=(1, hq, t, d))
+    k, v = rng.normal(size=(1, hk, t, d)), rng.normal(size=(1, hk, t, d))
+    o, lse = ops.sdpa_forward(q, k, v, causal=True, window=w)
+    g = hq // hk
+    for h in range(hq):
+        for i in range(t):
+            js = range(max(0, i - w + 1), i + 1)
+            sc = [sum(q[0, h, i, x] * k[0, h // g, j, x] for x in range(d)) / 2.0 for j in js]
+            m = max(sc)
+            z = sum(math.exp(x - m) for x in sc)
+            assert abs(lse[0, h, i] - (m + math.log(z))) < 1e-12
+            want = sum(math.exp(sv - m) / z * v[0, h // g, j] for sv, j in zip(sc, js))
+            close(o[0, h, i], want, rtol=1e-12, atol=1e-14)
+    # window >= T is plain causal attention; window 1 leaves only the diagonal: O = V
+    oc, lc = ops.sdpa_forward(q, k, v, causal=True)
+    ow, lw = ops.sdpa_forward(q, k, v, causal=True, window=t)
+    close(ow, oc, rtol=0, atol=0)
+    o1, _ = ops.sdpa_forward(q, k, v, causal=True, window=1)
+    close(o1, np.repeat(v, g, axis=1), rtol=1e-15, atol=0)
+
+
+def test_rms_norm_matches_torch_and_invariants():
+    import torch
+
+    rng = np.random.default_rng(10)
+    x, w = rng.normal(size=(5, 48)) * 3.0, rng.normal(size=48)
+    y, rstd = ops.rms_norm(x, w, eps=1e-6)
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x), (48,), torch.from_numpy(w), eps=1e-6).numpy()
+    close(y, ref, rtol=1e-12, atol=1e-12)
+    # unit weight: every row has root-mean-square sqrt(ms/(ms+eps)); scale invariance up to eps
+    y1, _ = ops.rms_norm(x, None, eps=1e-6)
+    ms = (x * x).mean(-1)
+    close(np.sqrt((y1 * y1).mean(-1)), np.sqrt(ms / (ms + 1e-6)), rtol=1e-12, atol=0)
+    y2, _ = ops.rms_norm(x * 7.0, None, eps=0.0)
+    y3, _ = ops.rms_norm(x, None, eps=0.0)
+    close(y2, y3, rtol=1e-12, atol=1e-14)
+    close(rstd, 1.0 / np.sqrt(ms + 1e-6), rtol=1e-14, atol=0)
+
+
 def test_sdpa_backward_finite_differences():
     rng = np.random.default_rng(6)
     shp = (1, 1, 4, 3)

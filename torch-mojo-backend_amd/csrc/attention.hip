@@ -70,6 +70,8 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e)
   float scale;
   int causal;
+  int64_t group;   // query heads per K/V head (grouped-query attention), >= 1
+  int64_t window;  // > 0: query i sees keys i-window+1 .. i (causal only); 0: none
 };
 
 // Stage a 64-row x D tile (rows row0.., row stride rs) into LDS: row-major
@@ -341,6 +343,7 @@ struct KvLayout {
   //   D = 64 (128-byte rows):  r & 7
   //   D = 128 (256-byte rows): bit 0 = r3, bits 1-2 = r0-r1, bit 3 = r2 ^ r3
   static __device__ __forceinline__ int swz(int row) {
+    if constexpr (D == 256) return row & 15;  // 512-byte rows: 16 rows at one chunk hit 16 bank groups
     return D == 64 ? (row & 7)
                    : (((row >> 3) & 1) | ((row & 3) << 1) | ((((row >> 2) ^ (row >> 3)) & 1) << 3));
   }
@@ -370,6 +373,9 @@ __device__ __forceinline__ void kv_tile_issue(const char* g, int64_t rs_bytes, i
 }
 
 __host__ __device__ inline int64_t ceil_div64(int64_t a, int64_t b) { return a <= 0 ? 0 : (a + b - 1) / b; }
+
+
+extern __shared__ __attribute__((aligned(1024))) char attn_dyn_lds[];
 
 template <bool B>
 struct BoolTag {
@@ -449,25 +455,31 @@ struct KvTileLoad {
 // against P (the same bf16 P that multiplies V).
 constexpr float kSlack = 8.f;
 
-template <typename T, int D, bool POS, int NW>
+template <typename T, int D, bool POS, int NW, int QPW>
 __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 1) attn_fwd_v2(AttnArgs p) {
-  constexpr int QPW = 128 / NW, QT = QPW / 16;  // queries per wave, 16-query tiles per wave
+  constexpr int QT = QPW / 16, QPB = NW * QPW;  // 16-query tiles per wave, queries per block
   typedef typename Mfma<T>::frag frag;
   typedef KvLayout<D> L;
   constexpr int KS = D / 32, DT = D / 16;
   constexpr int STAGE = 2 * L::TILE;  // K tile + V tile
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  char* lds;
+  if constexpr (D == 256) {
+    lds = attn_dyn_lds;  // 2 x 64 KB, launched with dynamic LDS
+  } else {
+    __shared__ __attribute__((aligned(1024))) char lds_static[2 * STAGE];
+    lds = lds_static;
+  }
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
   const BlockCoord bc = block_coord();
   const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
-  const int64_t q0 = qblock * 128;
-  const int64_t b = bc.b, h = bc.h;
+  const int64_t q0 = qblock * QPB;
+  const int64_t b = bc.b, h = bc.h, hk = h / p.group;  // K/V head of this query head
   const T* Q = (const T*)p.q + b * p.q_b + h * p.q_h;
   KvTileLoad<D, NW> kl, vl;
-  kl.init((const char*)((const T*)p.k + b * p.k_b + h * p.k_h), p.k_s * (int64_t)sizeof(T));
-  vl.init((const char*)((const T*)p.v + b * p.v_b + h * p.v_h), p.v_s * (int64_t)sizeof(T));
+  kl.init((const char*)((const T*)p.k + b * p.k_b + hk * p.k_h), p.k_s * (int64_t)sizeof(T));
+  vl.init((const char*)((const T*)p.v + b * p.v_b + hk * p.v_h), p.v_s * (int64_t)sizeof(T));
 
   frag qf[QT][KS];
 #pragma unroll
@@ -491,9 +503,11 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
   }
 
   int64_t kv_end = p.Skv;
-  if (p.causal) kv_end = min(p.Skv, q0 + 128);
-  kl.issue(0, p.Skv, lds);
-  vl.issue(0, p.Skv, lds + L::TILE);
+  if (p.causal) kv_end = min(p.Skv, q0 + QPB);
+  // first 64-key tile any query of the block can see (sliding window)
+  const int64_t j0 = p.window > 0 ? max((int64_t)0, q0 - p.window + 1) / 64 : 0;
+  kl.issue(j0 * 64, p.Skv, lds);
+  vl.issue(j0 * 64, p.Skv, lds + L::TILE);
   const int sw = L::swz(lr);  // fragment rows kt*16 + lr share the swizzle of lr
   const float c = p.scale_log2;
   int buf = 0;
@@ -531,12 +545,13 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
       }
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
-        int lim = 63;  // keys kb0 + 0..lim are visible to this lane's query
+        int lo = 0, lim = 63;  // keys kb0 + lo..lim are visible to this lane's query
         if constexpr (MASK) {
           const int64_t qi = q0 + wave * QPW + qt * 16 + lr;
           int64_t lm = p.Skv - 1 - kb0;
           if (p.causal && qi - kb0 < lm) lm = qi - kb0;
           lim = (int)max((int64_t)-1, min((int64_t)63, lm));
+          if (p.window > 0) lo = (int)max((int64_t)0, min((int64_t)64, qi - p.window + 1 - kb0));
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -544,7 +559,7 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float v = POS ? s[kt][qt][e] : s[kt][qt][e] * c;
-            if (MASK && kt * 16 + lg * 4 + e > lim) v = -INFINITY;
+            if (MASK && (kt * 16 + lg * 4 + e > lim || kt * 16 + lg * 4 + e < lo)) v = -INFINITY;
             s[kt][qt][e] = v;
             mx = fmaxf(mx, v);
           }
@@ -552,7 +567,9 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
         const float mxc = POS ? mx * c : mx;
         if (__builtin_amdgcn_ballot_w64(mxc > m[qt] + kSlack)) {
           const float m_new = fmaxf(m[qt], mxc);
-          const float alpha = fast_exp2(m[qt] - m_new);
+          // a row with every key so far masked (m_new = -inf, nothing
+          // accumulated) keeps its state: exp2(-inf - -inf) would be NaN
+          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m[qt] - m_new);
           lacc[qt] *= alpha;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
@@ -586,9 +603,14 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
       }
   };
   const int64_t nkb = (kv_end + 63) / 64;
-  int64_t ju = min(nkb, p.Skv / 64);  // unmasked [0, ju), masked [ju, nkb)
+  // masked [j0, jl) (window's lower edge), unmasked [jl, ju), masked [ju, nkb)
+  int64_t ju = min(nkb, p.Skv / 64);
   if (p.causal) ju = min(ju, (q0 + wave * QPW) / 64);
-  int64_t j = 0;
+  int64_t jl = j0;
+  if (p.window > 0) jl = min(nkb, max(j0, ceil_div64(q0 + wave * QPW + QPW - p.window, 64)));
+  ju = max(ju, jl);
+  int64_t j = j0;
+  for (; j < jl; ++j) step(j, BoolTag<true>{});
   for (; j < ju; ++j) step(j, BoolTag<false>{});
   for (; j < nkb; ++j) step(j, BoolTag<true>{});
 
@@ -1166,11 +1188,12 @@ bool strides_ok(const void* ptr, const int64_t* bhs) {
   return ((uintptr_t)ptr % 16 == 0) && bhs[0] % 8 == 0 && bhs[1] % 8 == 0 && bhs[2] % 8 == 0;
 }
 
-int check_common(int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D, int dtype) {
+int check_common(int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D, int dtype, bool fwd = false) {
   if (dtype != MI355X_BF16 && dtype != MI355X_F16)
     return fail(MI355X_EUNSUPPORTED, "mi355x_attn: dtype %d not supported (bf16/f16 only)", dtype);
-  if (D != 32 && D != 64 && D != 128)
-    return fail(MI355X_EUNSUPPORTED, "mi355x_attn: head_dim %lld not supported (32/64/128)", (long long)D);
+  if (D != 32 && D != 64 && D != 128 && !(fwd && D == 256))
+    return fail(MI355X_EUNSUPPORTED, "mi355x_attn: head_dim %lld not supported (32/64/128%s)", (long long)D,
+                fwd ? "/256" : "; 256 is forward-only");
   if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 || B >= 65536 || H >= 65536)
     return fail(MI355X_EINVAL, "mi355x_attn: bad shape");
   return MI355X_OK;
@@ -1178,11 +1201,30 @@ int check_common(int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D, int d
 
 template <typename T, int D>
 int fwd_launch(const AttnArgs& a, hipStream_t s) {
+  if constexpr (D == 256) {
+    // 64-query blocks of 4 waves x 16 queries; K/V stages need 128 KB of LDS
+    constexpr int NW = 4, QPW = 16;
+    constexpr size_t kLds = 4 * KvLayout<256>::TILE;
+    dim3 grid(ceil_div(a.Sq, NW * QPW), (unsigned)a.H, (unsigned)a.B);
+    auto kp = attn_fwd_v2<T, D, true, NW, QPW>;
+    auto kn = attn_fwd_v2<T, D, false, NW, QPW>;
+    static bool attr = false;
+    if (!attr) {
+      if (hipFuncSetAttribute((const void*)kp, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds) != hipSuccess ||
+          hipFuncSetAttribute((const void*)kn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds) != hipSuccess)
+        return fail(MI355X_ELAUNCH, "mi355x_attn_fwd: cannot raise the LDS limit for head_dim 256");
+      attr = true;
+    }
+    if (a.scale_log2 > 0.f) kp<<<grid, 64 * NW, kLds, s>>>(a);
+    else kn<<<grid, 64 * NW, kLds, s>>>(a);
+    return check_launch("mi355x_attn_fwd");
+  }
   dim3 grid(ceil_div(a.Sq, 128), (unsigned)a.H, (unsigned)a.B);
   if constexpr (D == 64 || D == 128) {
     constexpr int NW = D == 64 ? ATTN_FWD_WAVES : 4;
-    if (a.scale_log2 > 0.f) attn_fwd_v2<T, D, true, NW><<<grid, 64 * NW, 0, s>>>(a);
-    else attn_fwd_v2<T, D, false, NW><<<grid, 64 * NW, 0, s>>>(a);
+    constexpr int QPW = 128 / NW;
+    if (a.scale_log2 > 0.f) attn_fwd_v2<T, D, true, NW, QPW><<<grid, 64 * NW, 0, s>>>(a);
+    else attn_fwd_v2<T, D, false, NW, QPW><<<grid, 64 * NW, 0, s>>>(a);
   }
   else if (a.scale_log2 > 0.f) attn_fwd_kernel<T, D, true><<<grid, kThreads, 0, s>>>(a);
   else attn_fwd_kernel<T, D, false><<<grid, kThreads, 0, s>>>(a);
@@ -1207,6 +1249,15 @@ int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
   return check_launch("mi355x_attn_bwd");
 }
 
+#define MI_ATTN_FWD_DISPATCH(dtype, D, FN, ...)                               \
+  do {                                                                        \
+    if (D == 256) {                                                           \
+      if (dtype == MI355X_BF16) return FN<bf16, 256>(__VA_ARGS__);            \
+      return FN<f16, 256>(__VA_ARGS__);                                       \
+    }                                                                         \
+    MI_ATTN_DISPATCH(dtype, D, FN, __VA_ARGS__);                              \
+  } while (0)
+
 #define MI_ATTN_DISPATCH(dtype, D, FN, ...)                                   \
   do {                                                                        \
     if (dtype == MI355X_BF16) {                                               \
@@ -1224,21 +1275,38 @@ int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
 
 using namespace mi;
 
-extern "C" int mi355x_attn_fwd(void* o, const int64_t* o_bhs, float* lse, const void* q,
-                               const int64_t* q_bhs, const void* k, const int64_t* k_bhs,
-                               const void* v, const int64_t* v_bhs, int64_t batch, int64_t heads,
-                               int64_t sq, int64_t skv, int64_t d, double scale, int causal,
-                               int dtype, mi355x_stream_t stream) {
-  int rc = check_common(batch, heads, sq, skv, d, dtype);
+extern "C" int mi355x_attn_fwd_ex(void* o, const int64_t* o_bhs, float* lse, const void* q,
+                                  const int64_t* q_bhs, const void* k, const int64_t* k_bhs,
+                                  const void* v, const int64_t* v_bhs, int64_t batch, int64_t heads,
+                                  int64_t kv_heads, int64_t sq, int64_t skv, int64_t d, double scale,
+                                  int causal, int64_t window, int dtype, mi355x_stream_t stream) {
+  int rc = check_common(batch, heads, sq, skv, d, dtype, true);
   if (rc) return rc;
+  MI_REQUIRE(kv_heads >= 1 && heads % kv_heads == 0,
+             "mi355x_attn_fwd_ex: heads (%lld) must be a multiple of kv_heads (%lld)", (long long)heads,
+             (long long)kv_heads);
+  MI_REQUIRE(window >= 0 && (window == 0 || causal), "mi355x_attn_fwd_ex: a sliding window needs causal attention");
+  MI_REQUIRE(d != 32 || (kv_heads == heads && window == 0),
+             "mi355x_attn_fwd_ex: head_dim 32 supports neither grouped K/V heads nor a window");
   MI_REQUIRE(strides_ok(q, q_bhs) && strides_ok(k, k_bhs) && strides_ok(v, v_bhs),
              "mi355x_attn_fwd: q/k/v need 16-byte aligned bases and strides that are multiples of 8");
   MI_REQUIRE(((uintptr_t)o % 8 == 0) && o_bhs[0] % 4 == 0 && o_bhs[1] % 4 == 0 && o_bhs[2] % 4 == 0,
              "mi355x_attn_fwd: o needs 8-byte aligned rows");
   AttnArgs a{o, o_bhs[0], o_bhs[1], o_bhs[2], lse, q, q_bhs[0], q_bhs[1], q_bhs[2],
              k, k_bhs[0], k_bhs[1], k_bhs[2], v, v_bhs[0], v_bhs[1], v_bhs[2],
-             batch, heads, sq, skv, (float)(scale * 1.4426950408889634), (float)scale, causal};
-  MI_ATTN_DISPATCH(dtype, d, fwd_launch, a, (hipStream_t)stream);
+             batch, heads, sq, skv, (float)(scale * 1.4426950408889634), (float)scale, causal,
+             heads / kv_heads, window};
+  MI_ATTN_FWD_DISPATCH(dtype, d, fwd_launch, a, (hipStream_t)stream);
+}
+
+extern "C" int mi355x_attn_fwd(void* o, const int64_t* o_bhs, float* lse, const void* q,
+                               const int64_t* q_bhs, const void* k, const int64_t* k_bhs,
+                               const void* v, const int64_t* v_bhs, int64_t batch, int64_t heads,
+                               int64_t sq, int64_t skv, int64_t d, double scale, int causal,
+                               int dtype, mi355x_stream_t stream) {
+  if (d == 256) return fail(MI355X_EUNSUPPORTED, "mi355x_attn_fwd: head_dim 256 goes through mi355x_attn_fwd_ex");
+  return mi355x_attn_fwd_ex(o, o_bhs, lse, q, q_bhs, k, k_bhs, v, v_bhs, batch, heads, heads, sq, skv, d, scale,
+                            causal, 0, dtype, stream);
 }
 
 extern "C" int64_t mi355x_attn_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t sq,
@@ -1268,7 +1336,7 @@ extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const 
   AttnBwdArgs a;
   a.f = AttnArgs{(void*)o, o_bhs[0], o_bhs[1], o_bhs[2], (float*)lse, q, q_bhs[0], q_bhs[1], q_bhs[2],
                  k, k_bhs[0], k_bhs[1], k_bhs[2], v, v_bhs[0], v_bhs[1], v_bhs[2],
-                 batch, heads, sq, skv, (float)(scale * 1.4426950408889634), (float)scale, causal};
+                 batch, heads, sq, skv, (float)(scale * 1.4426950408889634), (float)scale, causal, 1, 0};
   a.dout = dout; a.do_b = do_bhs[0]; a.do_h = do_bhs[1]; a.do_s = do_bhs[2];
   a.dq = dq; a.dq_b = dq_bhs[0]; a.dq_h = dq_bhs[1]; a.dq_s = dq_bhs[2];
   a.dk = dk; a.dk_b = dk_bhs[0]; a.dk_h = dk_bhs[1]; a.dk_s = dk_bhs[2];

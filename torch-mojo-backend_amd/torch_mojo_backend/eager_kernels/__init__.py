@@ -20,7 +20,7 @@ from pathlib import Path
 
 LIB_NAME = "libmi355x_kernels.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 c_int = ctypes.c_int
 c_i64 = ctypes.c_int64
@@ -161,6 +161,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [
             c_vp, P_i64, c_vp, c_vp, P_i64, c_vp, P_i64, c_vp, P_i64,
             c_i64, c_i64, c_i64, c_i64, c_i64, c_double, c_int, c_int, c_vp,
+        ],
+    ),
+    "mi355x_rms_norm_fwd": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_i64, c_double, c_int, c_vp]),
+    "mi355x_attn_fwd_ex": (
+        c_int,
+        [
+            c_vp, P_i64, c_vp, c_vp, P_i64, c_vp, P_i64, c_vp, P_i64,
+            c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_double, c_int, c_i64, c_int, c_vp,
         ],
     ),
     "mi355x_attn_bwd_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64]),

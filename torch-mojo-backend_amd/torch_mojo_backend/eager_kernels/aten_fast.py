@@ -1867,16 +1867,115 @@ def sdpa_math(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
     return torch.matmul(probs, value)
 
 
+def fused_fa_ex_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa):
+    """Forward-only fused attention beyond the flash-pair gate: grouped K/V
+    heads (enable_gqa), head_dim 256, and a sliding-window causal mask built
+    by torch_mojo_backend.masks.  Returns (q, k, v, causal, window) or None."""
+    from ..masks import window_of
+
+    q, k, v = _t(query), _t(key), _t(value)
+    if (
+        q is None or k is None or v is None
+        or float(dropout_p) != 0.0
+        or q._device != k._device or q._device != v._device
+        or q._dtype not in _MFMA_DTYPES
+        or q._dtype != k._dtype or q._dtype != v._dtype
+        or len(q._shape) != 4 or len(k._shape) != 4 or len(v._shape) != 4
+    ):
+        return None
+    b, h, sq, d = q._shape
+    hk, skv = k._shape[1], k._shape[2]
+    if k._shape[0] != b or tuple(k._shape) != tuple(v._shape) or k._shape[3] != d:
+        return None
+    if hk != h and not (enable_gqa and hk > 0 and h % hk == 0):
+        return None
+    if min(b, h, sq, skv) <= 0 or d not in (64, 128, 256):
+        return None
+    if scale is not None and not math.isfinite(float(scale)):
+        return None
+    causal, window = bool(is_causal), 0
+    if attn_mask is not None:
+        w = window_of(attn_mask)
+        if w is None or is_causal or sq != skv:
+            return None
+        causal, window = True, w
+    return q, k, v, causal, window
+
+
+def fused_flash_attention_forward_ex(q: MT, k: MT, v: MT, causal, window, scale):
+    q, k, v = _fa_head_contig(q), _fa_head_contig(k), _fa_head_contig(v)
+    b, h, sq, d = q._shape
+    hk, skv = k._shape[1], k._shape[2]
+    scale_value = float(scale) if scale is not None else 1.0 / math.sqrt(d)
+    out = alloc_bthd(b, h, sq, d, q._dtype, q._device)
+    lse = _alloc((b, h, sq), torch.float32, q._device)
+    check(
+        "mi355x_attn_fwd_ex",
+        lib().mi355x_attn_fwd_ex(out._ptr, _bhs(out), lse._ptr, q._ptr, _bhs(q), k._ptr, _bhs(k),
+                                 v._ptr, _bhs(v), b, h, hk, sq, skv, d, scale_value, int(causal),
+                                 int(window), _code(q._dtype), _STREAM),
+    )
+    return out, lse
+
+
 def fast_aten_scaled_dot_product_attention(
     query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, *, scale=None, enable_gqa=False
 ):
-    """No-grad SDPA (aten_fast.py:9102-9211): fused kernel when eligible,
-    otherwise the decomposition."""
+    """No-grad SDPA (aten_fast.py:9102-9211): fused kernel when eligible
+    (including grouped K/V heads, head_dim 256 and sliding-window masks from
+    torch_mojo_backend.masks), otherwise the decomposition."""
     inputs = fused_fa_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa)
     if inputs is not None:
         out, _ = fused_flash_attention_forward(*inputs, is_causal, scale)
         return out
+    ex = fused_fa_ex_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa)
+    if ex is not None:
+        q, k, v, causal, window = ex
+        out, _ = fused_flash_attention_forward_ex(q, k, v, causal, window, scale)
+        return out
     return sdpa_math(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa)
+
+
+def rms_norm_inputs(x, normalized_shape, weight) -> bool:
+    """Whether the fused RMSNorm kernel takes these inputs (metadata only)."""
+    t = _t(x)
+    if t is None or t._dtype not in (torch.float32, torch.bfloat16, torch.float16) or not normalized_shape:
+        return False
+    if tuple(t._shape[len(t._shape) - len(normalized_shape):]) != tuple(normalized_shape):
+        return False
+    n = math.prod(normalized_shape)
+    if weight is not None:
+        w = _t(weight)
+        if w is None or w._numel != n or w._dtype not in (torch.float32, t._dtype):
+            return False
+    return n > 0
+
+
+def rms_norm_forward(x: MT, normalized_shape, weight, eps):
+    """(y, rstd [rows] f32) of rms_norm over the trailing `normalized_shape`
+    dims, or NOT_HANDLED."""
+    n = math.prod(normalized_shape) if normalized_shape else 1
+    if tuple(x._shape[len(x._shape) - len(normalized_shape):]) != tuple(normalized_shape) or n <= 0:
+        return NOT_HANDLED
+    if x._dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        return NOT_HANDLED
+    w = None
+    if weight is not None:
+        w = _require(weight)
+        if w._numel != n or w._dtype not in (torch.float32, x._dtype):
+            return NOT_HANDLED
+        w = _contig(w)
+    xc = _contig(x)
+    rows = xc._numel // n
+    y = _alloc(x._shape, x._dtype, x._device)
+    rstd = _alloc((rows,), torch.float32, x._device)
+    check(
+        "mi355x_rms_norm_fwd",
+        lib().mi355x_rms_norm_fwd(y._ptr, rstd._ptr, xc._ptr, w._ptr if w is not None else None,
+                                  _code(w._dtype) if w is not None else 0, rows, n, float(eps),
+                                  _code(x._dtype), _STREAM),
+    )
+    return y, rstd
 
 
 # ---------------------------------------------------------------------------

@@ -75,6 +75,7 @@ def register_autograd_ops() -> None:
     _library = torch.library.Library("aten", "IMPL", "AutogradPrivateUse1")
     _library.impl("scaled_dot_product_attention", _scaled_dot_product_attention_autograd)
     _library.impl("cross_entropy_loss", _cross_entropy_loss_autograd)
+    _library.impl("rms_norm", _rms_norm_autograd)
     _registered = True
 
 
@@ -162,3 +163,54 @@ def _cross_entropy_loss_autograd(input, target, weight=None, reduction=1, ignore
         logp, target, weight, reduction={0: "none", 1: "mean", 2: "sum"}[reduction],
         ignore_index=ignore_index,
     )
+
+
+class _FusedRMSNorm(torch.autograd.Function):
+    """rms_norm (the Gemma-3-shaped workload's norm): the forward is one
+    gfx950 kernel that also keeps the row rstd; the backward uses it,
+    dx = r*(g*w) - x * r^3/n * sum(g*w*x) and dw = sum_rows(g*x*r), from
+    device ops in f32."""
+
+    @staticmethod
+    def forward(ctx, x, normalized_shape, weight, eps):
+        y, rstd = aten_fast.rms_norm_forward(x, normalized_shape, weight, eps)
+        ctx.save_for_backward(x, weight, rstd)
+        ctx.n = len(normalized_shape)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, weight, rstd = ctx.saved_tensors
+        nd = ctx.n
+        dims = tuple(range(x.dim() - nd, x.dim()))
+        n = 1
+        for d in dims:
+            n *= x.shape[d]
+        xf, gf = x.float(), grad.float()
+        r = rstd.view(tuple(x.shape[: x.dim() - nd]) + (1,) * nd)
+        gw = gf * weight.float() if weight is not None else gf
+        dot = (gw * xf).sum(dim=dims, keepdim=True)
+        dx = (r * gw - xf * (r * r * r) * (dot / n)).to(x.dtype) if ctx.needs_input_grad[0] else None
+        dw = None
+        if weight is not None and ctx.needs_input_grad[2]:
+            lead = tuple(range(x.dim() - nd))
+            dw = (gf * xf * r).sum(dim=lead).to(weight.dtype) if lead else (gf * xf * r).to(weight.dtype)
+        return dx, None, dw, None
+
+
+def _rms_norm_autograd(input, normalized_shape, weight=None, eps=None):
+    if eps is None:
+        eps = torch.finfo(input.dtype).eps
+    shape = tuple(int(v) for v in normalized_shape)
+    if isinstance(input, TorchMojoTensor) and (weight is None or isinstance(weight, TorchMojoTensor)):
+        with torch._C._AutoDispatchBelowAutograd():
+            ok = aten_fast.rms_norm_inputs(input, shape, weight)
+        if ok:
+            return _FusedRMSNorm.apply(input, shape, weight, float(eps))
+    # other inputs: the decomposition on the device
+    dims = tuple(range(input.dim() - len(shape), input.dim()))
+    xf = input.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(dim=dims, keepdim=True) + eps)
+    if weight is not None:
+        y = y * weight.float()
+    return y.to(input.dtype)
