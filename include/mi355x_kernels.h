@@ -231,14 +231,34 @@ int mi355x_embedding_bwd(void* grad_weight, const void* grad_out, int dtype,
  *      LayerNormBackwardF32 normalization_backward_dx.mojo:190-388,
  *      normalization_backward_params.mojo:41-143) ---------------------- */
 /* RMSNorm forward over the last dim (rows x cols, contiguous):
- * y = x / sqrt(mean(x^2) + eps) * weight, rstd[rows] f32.  weight (optional)
- * is f32 or the input dtype.  The reference has no eager RMSNorm (its
+ * y = x / sqrt(mean(x^2) + eps) * (weight + weight_offset), rstd[rows] f32.
+ * weight (optional; without it the scale is 1) is f32 or the input dtype;
+ * weight_offset = 1 gives Gemma's (1 + w) scale without a separate add.  The reference has no eager RMSNorm (its
  * Gemma-3 path runs under torch.compile, demo_scripts/gemma3.py:11); this
  * serves aten::rms_norm for the Gemma-3-shaped workload and follows
  * fast_aten_native_layer_norm's contract (aten_fast.py:5248-5371) minus the
  * mean and bias. */
 int mi355x_rms_norm_fwd(void* y, float* rstd, const void* x, const void* weight, int weight_dtype,
-                        int64_t rows, int64_t cols, double eps, int dtype, mi355x_stream_t stream);
+                        double weight_offset, int64_t rows, int64_t cols, double eps, int dtype,
+                        mi355x_stream_t stream);
+/* Rotary position embedding, half-split ("rotate_half") form, over
+ * [batch, heads, seq, d] views (unit d stride, *_bht = the batch/head/seq
+ * element strides, multiples of 4): y[i] = x[i] cos[t][i] - x[i+d/2] sin[t][i],
+ * y[i+d/2] = x[i+d/2] cos[t][i+d/2] + x[i] sin[t][i+d/2]; inverse = 1 applies
+ * the transposed map (the backward).  cos/sin: dense [seq][d] in dtype; d a
+ * multiple of 8.  The Gemma-3-shaped workload's RoPE; the reference has no
+ * eager kernel for it (its Gemma-3 demo runs under torch.compile,
+ * demo_scripts/gemma3.py:11) and would run the elementwise chain through
+ * its _to_copy / add / mul ops (aten_fast.py:1232, :2510). */
+int mi355x_rope(void* y, const int64_t* y_bht, const void* x, const int64_t* x_bht, const void* cos_table,
+                const void* sin_table, int64_t batch, int64_t heads, int64_t seq, int64_t d, int inverse,
+                int dtype, mi355x_stream_t stream);
+/* GeGLU: y = gelu(gate) * up over n contiguous elements, gelu exact or tanh
+ * (approximate), gelu(gate) rounded to dtype before the product as the
+ * aten gelu + mul pair does (fast_aten_gelu aten_fast.py:2940-2968, then
+ * the elementwise mul). */
+int mi355x_geglu_fwd(void* y, const void* gate, const void* up, int64_t n, int approximate, int dtype,
+                     mi355x_stream_t stream);
 /* y = (x - mean)*rstd*gamma + beta over rows of `cols` contiguous elements.
  * gamma/beta may be NULL.  mean/rstd: f32 [rows]. */
 int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,

@@ -499,15 +499,35 @@ class HostStandIn:
         dense(_val(lse), torch.float32, (B, H, Sq)).copy_(L)
         return 0
 
-    def mi355x_rms_norm_fwd(self, y, rstd, x, w, wdt, rows, cols, eps, dt, stream):
+    def mi355x_rms_norm_fwd(self, y, rstd, x, w, wdt, woff, rows, cols, eps, dt, stream):
         X = dense(_val(x), DT[dt], (rows, cols)).double()
         r = torch.rsqrt((X * X).mean(-1) + eps)
         Y = X * r[:, None]
         if w:
-            Y = Y * dense(_val(w), DT[wdt], (cols,)).double()
+            Y = Y * (dense(_val(w), DT[wdt], (cols,)).double() + woff)
         dense(_val(y), DT[dt], (rows, cols)).copy_(Y.to(DT[dt]))
         if rstd:
             dense(_val(rstd), torch.float32, (rows,)).copy_(r.float())
+        return 0
+
+    def mi355x_rope(self, y, ybht, x, xbht, cos, sin, B, H, T, D, inverse, dt, stream):
+        X = view(_val(x), DT[dt], (B, H, T, D), (xbht[0], xbht[1], xbht[2], 1)).float()
+        C = dense(_val(cos), DT[dt], (T, D)).float()
+        S = dense(_val(sin), DT[dt], (T, D)).float()
+        h = D // 2
+        x1, x2 = X[..., :h], X[..., h:]
+        if inverse:
+            out = torch.cat([x1 * C[:, :h] + x2 * S[:, h:], x2 * C[:, h:] - x1 * S[:, :h]], -1)
+        else:
+            out = torch.cat([x1 * C[:, :h] - x2 * S[:, :h], x2 * C[:, h:] + x1 * S[:, h:]], -1)
+        view(_val(y), DT[dt], (B, H, T, D), (ybht[0], ybht[1], ybht[2], 1)).copy_(out)
+        return 0
+
+    def mi355x_geglu_fwd(self, y, gate, up, n, approximate, dt, stream):
+        g = dense(_val(gate), DT[dt], (n,))
+        u = dense(_val(up), DT[dt], (n,))
+        a = torch.nn.functional.gelu(g.float(), approximate="tanh" if approximate else "none").to(DT[dt])
+        dense(_val(y), DT[dt], (n,)).copy_((a.float() * u.float()).to(DT[dt]))
         return 0
 
     def mi355x_attn_fwd_ex(self, o, obhs, lse, q, qbhs, k, kbhs, v, vbhs, B, H, Hk, Sq, Skv, D, scale, causal,

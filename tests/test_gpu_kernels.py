@@ -409,8 +409,45 @@ def test_rms_norm_fwd_matches_oracle(kernels, cols, dtype, wdt):
     y = torch.empty(rows, cols, dtype=dtype, device="cuda")
     rstd = torch.empty(rows, device="cuda")
     tx, tw = dev(x), dev(w)  # held: a freed temporary's memory would be reused by the next allocation
-    call("mi355x_rms_norm_fwd", p(y), p(rstd), p(tx), p(tw), CODE[wdt], rows, cols, 1e-6, CODE[dtype], None)
+    call("mi355x_rms_norm_fwd", p(y), p(rstd), p(tx), p(tw), CODE[wdt], 0.0, rows, cols, 1e-6, CODE[dtype], None)
     ey, er = O.rms_norm(x.double().numpy(), w.double().numpy(), eps=1e-6)
     tol = 1e-5 if dtype == torch.float32 else 1e-2
     tol_close(np64(y), ey, atol=tol, rtol=tol, what="y")
     tol_close(np64(rstd), er, atol=1e-6, rtol=1e-5, what="rstd")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rope_forward_and_inverse(kernels, dtype):
+    """Rotary embedding on a [B,H,T,D] view with BTHD storage: against the
+    rotate_half formula, and inverse(forward(x)) = x on a true rotation."""
+    B, H, T, D = 2, 3, 37, 64
+    xs = randn(B, T, H, D).to(dtype)
+    x = dev(xs).transpose(1, 2)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, dtype=torch.float64) / D))
+    ang = torch.arange(T, dtype=torch.float64)[:, None] * inv[None, :]
+    ang = torch.cat([ang, ang], -1)
+    cos, sin = dev(ang.cos().to(dtype)), dev(ang.sin().to(dtype))
+    y = torch.empty(B, T, H, D, dtype=dtype, device="cuda").transpose(1, 2)
+    z = torch.empty_like(y)
+    call("mi355x_rope", p(y), i64(*y.stride()[:3]), p(x), i64(*x.stride()[:3]), p(cos), p(sin), B, H, T, D, 0,
+         CODE[dtype], None)
+    call("mi355x_rope", p(z), i64(*z.stride()[:3]), p(y), i64(*y.stride()[:3]), p(cos), p(sin), B, H, T, D, 1,
+         CODE[dtype], None)
+    xf = xs.double().transpose(1, 2)
+    c, sn = host(cos).double(), host(sin).double()
+    want = xf * c + torch.cat([-xf[..., D // 2:], xf[..., :D // 2]], -1) * sn
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    tol_close(np64(y), want.numpy(), atol=tol, rtol=tol, what="rope")
+    tol_close(np64(z), xf.numpy(), atol=2 * tol, rtol=2 * tol, what="inverse")
+
+
+@pytest.mark.parametrize("approximate", [0, 1])
+def test_geglu_bit_exact_vs_gelu_then_mul(kernels, approximate):
+    n = 4096 + 5
+    gate, up = dev(randn(n).bfloat16()), dev(randn(n).bfloat16())
+    y = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    call("mi355x_geglu_fwd", p(y), p(gate), p(up), n, approximate, CODE[torch.bfloat16], None)
+    a = torch.empty_like(y)
+    call("mi355x_gelu_fwd", p(a), p(gate), n, approximate, CODE[torch.bfloat16], None)
+    want = (host(a).float() * host(up).float()).bfloat16()
+    assert torch.equal(host(y), want)

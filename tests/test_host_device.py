@@ -276,3 +276,29 @@ def test_gemma_shaped_prefill_on_device(mojo):
         want = ref(idx)
     assert calls["mi355x_attn_fwd_ex"] == 3 and calls["mi355x_rms_norm_fwd"] >= 3 * 6 + 1
     assert torch.allclose(got, want, atol=5e-2, rtol=5e-2), (got - want).abs().max()
+
+
+def test_fused_gemma_ops_gradients(mojo):
+    """rotary_embedding, geglu and rms_norm(weight_offset) on the device
+    against autograd of their formulas on the CPU."""
+    from torch_mojo_backend import ops
+
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(2, 3, 7, 16, generator=g)
+    ang = torch.randn(7, 8, generator=g)
+    cos, sin = torch.cat([ang.cos()] * 2, -1), torch.cat([ang.sin()] * 2, -1)
+    gate, up = torch.randn(5, 24, generator=g), torch.randn(5, 24, generator=g)
+    h, w = torch.randn(5, 24, generator=g), torch.randn(24, generator=g) * 0.1
+    dy1, dy2, dy3 = torch.randn(2, 3, 7, 16, generator=g), torch.randn(5, 24, generator=g), torch.randn(5, 24, generator=g)
+
+    def run(dev):
+        ts = [t.to(dev).requires_grad_() for t in (x, gate, up, h, w)]
+        xm, gm, um, hm, wm = ts
+        y1 = ops.rotary_embedding(xm, cos.to(dev), sin.to(dev))
+        y2 = ops.geglu(gm, um)
+        y3 = ops.rms_norm(hm, wm, 1e-6, weight_offset=1.0)
+        torch.autograd.backward([y1, y2, y3], [dy1.to(dev), dy2.to(dev), dy3.to(dev)])
+        return [y.detach().cpu() for y in (y1, y2, y3)] + [t.grad.cpu() for t in ts]
+
+    for a, b in zip(run("mojo"), run("cpu")):
+        assert torch.allclose(a, b, atol=1e-5, rtol=1e-5), (a - b).abs().max()

@@ -85,6 +85,26 @@ __global__ void __launch_bounds__(kThreads) gelu_bwd_kernel(T* __restrict__ dx, 
     dx[i] = from_f32<T>(gelu_grad_f(to_f32(dy[i]), to_f32(x[i]), approx));
 }
 
+// GeGLU: y = gelu(gate) * up (the Gemma-3-shaped MLP), with gelu(gate)
+// rounded to the storage type before the product, as the two ATen ops do.
+template <typename T>
+__global__ void __launch_bounds__(kThreads) geglu_fwd_kernel(T* __restrict__ y, const T* __restrict__ gate,
+                                                             const T* __restrict__ up, int64_t n, int approx) {
+  const int64_t n8 = (aligned16(y) && aligned16(gate) && aligned16(up)) ? n / 8 : 0;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n8; i += stride) {
+    Pack8<T> g = ((const Pack8<T>*)gate)[i];
+    Pack8<T> u = ((const Pack8<T>*)up)[i];
+    Pack8<T> r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      r.v[e] = from_f32<T>(to_f32(from_f32<T>(gelu_f(to_f32(g.v[e]), approx))) * to_f32(u.v[e]));
+    ((Pack8<T>*)y)[i] = r;
+  }
+  for (int64_t i = n8 * 8 + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride)
+    y[i] = from_f32<T>(to_f32(from_f32<T>(gelu_f(to_f32(gate[i]), approx))) * to_f32(up[i]));
+}
+
 unsigned grid_for(int64_t n) {
   int64_t b = (n / 8 + kThreads - 1) / kThreads;
   if (b < 1) b = 1;
@@ -124,4 +144,19 @@ extern "C" int mi355x_gelu_bwd(void* dx, const void* dy, const void* x, int64_t 
     default: return fail(MI355X_EUNSUPPORTED, "mi355x_gelu_bwd: unsupported dtype %d", dtype);
   }
   return check_launch("mi355x_gelu_bwd");
+}
+
+extern "C" int mi355x_geglu_fwd(void* y, const void* gate, const void* up, int64_t n, int approximate, int dtype,
+                                mi355x_stream_t stream) {
+  MI_REQUIRE(n >= 0, "mi355x_geglu_fwd: bad size");
+  if (n == 0) return MI355X_OK;
+  MI_REQUIRE(y && gate && up, "mi355x_geglu_fwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MI355X_F32: geglu_fwd_kernel<float><<<grid_for(n), kThreads, 0, s>>>((float*)y, (const float*)gate, (const float*)up, n, approximate); break;
+    case MI355X_BF16: geglu_fwd_kernel<bf16><<<grid_for(n), kThreads, 0, s>>>((bf16*)y, (const bf16*)gate, (const bf16*)up, n, approximate); break;
+    case MI355X_F16: geglu_fwd_kernel<f16><<<grid_for(n), kThreads, 0, s>>>((f16*)y, (const f16*)gate, (const f16*)up, n, approximate); break;
+    default: return fail(MI355X_EUNSUPPORTED, "mi355x_geglu_fwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("mi355x_geglu_fwd");
 }

@@ -118,7 +118,7 @@ __global__ void __launch_bounds__(kThreads)
 template <typename T, typename W, int NV>
 __global__ void __launch_bounds__(kThreads)
     rms_fwd_wave(T* __restrict__ y, float* __restrict__ rstd_out, const T* __restrict__ x,
-                 const W* __restrict__ w, int64_t rows, int cols, float eps) {
+                 const W* __restrict__ w, int64_t rows, int cols, float eps, float w_off) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -145,7 +145,7 @@ __global__ void __launch_bounds__(kThreads)
       if (w) Vec4<W>::load(w + c, g);
       float o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = v[j][e] * r * g[e];
+      for (int e = 0; e < 4; ++e) o[e] = v[j][e] * r * (w ? g[e] + w_off : 1.f);
       Vec4<T>::store(yr + c, o);
     }
   }
@@ -155,7 +155,7 @@ __global__ void __launch_bounds__(kThreads)
 template <typename T, typename W>
 __global__ void __launch_bounds__(kThreads)
     rms_fwd_block(T* __restrict__ y, float* __restrict__ rstd_out, const T* __restrict__ x,
-                  const W* __restrict__ w, int64_t rows, int64_t cols, float eps) {
+                  const W* __restrict__ w, int64_t rows, int64_t cols, float eps, float w_off) {
   __shared__ float red[kWaves];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * cols;
@@ -168,7 +168,7 @@ __global__ void __launch_bounds__(kThreads)
   T* yr = y + row * cols;
   for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
     float o = to_f32(xr[c]) * r;
-    if (w) o *= to_f32(w[c]);
+    if (w) o *= to_f32(w[c]) + w_off;
     yr[c] = from_f32<T>(o);
   }
   if (threadIdx.x == 0 && rstd_out) rstd_out[row] = r;
@@ -388,26 +388,27 @@ int fwd_impl(T* y, float* mean, float* rstd, const T* x, const T* g, const T* b,
 }
 
 template <typename T, typename W>
-int rms_impl(T* y, float* rstd, const T* x, const W* w, int64_t rows, int64_t cols, float eps, hipStream_t s) {
+int rms_impl(T* y, float* rstd, const T* x, const W* w, int64_t rows, int64_t cols, float eps, float w_off,
+             hipStream_t s) {
   const int nv = (aligned(x, 4 * sizeof(T)) && aligned(y, 4 * sizeof(T)) && aligned(w, 4 * sizeof(W))) ? wave_nv(cols) : 0;
   const unsigned grid = ceil_div(rows, kWaves);
   switch (nv) {
-    case 1: rms_fwd_wave<T, W, 1><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps); break;
-    case 2: rms_fwd_wave<T, W, 2><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps); break;
-    case 3: rms_fwd_wave<T, W, 3><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps); break;
-    case 4: rms_fwd_wave<T, W, 4><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps); break;
-    case 8: rms_fwd_wave<T, W, 8><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps); break;
-    default: rms_fwd_block<T, W><<<(unsigned)rows, kThreads, 0, s>>>(y, rstd, x, w, rows, cols, eps);
+    case 1: rms_fwd_wave<T, W, 1><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps, w_off); break;
+    case 2: rms_fwd_wave<T, W, 2><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps, w_off); break;
+    case 3: rms_fwd_wave<T, W, 3><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps, w_off); break;
+    case 4: rms_fwd_wave<T, W, 4><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps, w_off); break;
+    case 8: rms_fwd_wave<T, W, 8><<<grid, kThreads, 0, s>>>(y, rstd, x, w, rows, (int)cols, eps, w_off); break;
+    default: rms_fwd_block<T, W><<<(unsigned)rows, kThreads, 0, s>>>(y, rstd, x, w, rows, cols, eps, w_off);
   }
   return check_launch("mi355x_rms_norm_fwd");
 }
 
 template <typename T>
 int rms_dispatch_w(void* y, float* rstd, const void* x, const void* w, int w_dtype, int64_t rows, int64_t cols,
-                   float eps, hipStream_t s) {
+                   float eps, float w_off, hipStream_t s) {
   if (!w || w_dtype == MI355X_F32)
-    return rms_impl<T, float>((T*)y, rstd, (const T*)x, (const float*)w, rows, cols, eps, s);
-  return rms_impl<T, T>((T*)y, rstd, (const T*)x, (const T*)w, rows, cols, eps, s);
+    return rms_impl<T, float>((T*)y, rstd, (const T*)x, (const float*)w, rows, cols, eps, w_off, s);
+  return rms_impl<T, T>((T*)y, rstd, (const T*)x, (const T*)w, rows, cols, eps, w_off, s);
 }
 
 template <typename T>
@@ -519,7 +520,8 @@ extern "C" int mi355x_layer_norm_bwd(void* dx, void* dgamma, void* dbeta, const 
 }
 
 extern "C" int mi355x_rms_norm_fwd(void* y, float* rstd, const void* x, const void* weight, int weight_dtype,
-                                   int64_t rows, int64_t cols, double eps, int dtype, mi355x_stream_t stream) {
+                                   double weight_offset, int64_t rows, int64_t cols, double eps, int dtype,
+                                   mi355x_stream_t stream) {
   MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_rms_norm_fwd: bad shape [%lld, %lld]", (long long)rows, (long long)cols);
   if (rows == 0) return MI355X_OK;
   MI_REQUIRE(y && x, "mi355x_rms_norm_fwd: null pointer");
@@ -527,9 +529,9 @@ extern "C" int mi355x_rms_norm_fwd(void* y, float* rstd, const void* x, const vo
              "mi355x_rms_norm_fwd: weight dtype must be f32 or the input dtype");
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case MI355X_F32: return rms_dispatch_w<float>(y, rstd, x, weight, weight_dtype, rows, cols, (float)eps, s);
-    case MI355X_BF16: return rms_dispatch_w<bf16>(y, rstd, x, weight, weight_dtype, rows, cols, (float)eps, s);
-    case MI355X_F16: return rms_dispatch_w<f16>(y, rstd, x, weight, weight_dtype, rows, cols, (float)eps, s);
+    case MI355X_F32: return rms_dispatch_w<float>(y, rstd, x, weight, weight_dtype, rows, cols, (float)eps, (float)weight_offset, s);
+    case MI355X_BF16: return rms_dispatch_w<bf16>(y, rstd, x, weight, weight_dtype, rows, cols, (float)eps, (float)weight_offset, s);
+    case MI355X_F16: return rms_dispatch_w<f16>(y, rstd, x, weight, weight_dtype, rows, cols, (float)eps, (float)weight_offset, s);
   }
   return fail(MI355X_EUNSUPPORTED, "mi355x_rms_norm_fwd: unsupported dtype %d", dtype);
 }

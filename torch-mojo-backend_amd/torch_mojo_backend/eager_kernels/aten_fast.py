@@ -1951,9 +1951,9 @@ def rms_norm_inputs(x, normalized_shape, weight) -> bool:
     return n > 0
 
 
-def rms_norm_forward(x: MT, normalized_shape, weight, eps):
+def rms_norm_forward(x: MT, normalized_shape, weight, eps, weight_offset=0.0):
     """(y, rstd [rows] f32) of rms_norm over the trailing `normalized_shape`
-    dims, or NOT_HANDLED."""
+    dims (scale weight + weight_offset), or NOT_HANDLED."""
     n = math.prod(normalized_shape) if normalized_shape else 1
     if tuple(x._shape[len(x._shape) - len(normalized_shape):]) != tuple(normalized_shape) or n <= 0:
         return NOT_HANDLED
@@ -1972,10 +1972,40 @@ def rms_norm_forward(x: MT, normalized_shape, weight, eps):
     check(
         "mi355x_rms_norm_fwd",
         lib().mi355x_rms_norm_fwd(y._ptr, rstd._ptr, xc._ptr, w._ptr if w is not None else None,
-                                  _code(w._dtype) if w is not None else 0, rows, n, float(eps),
-                                  _code(x._dtype), _STREAM),
+                                  _code(w._dtype) if w is not None else 0, float(weight_offset), rows, n,
+                                  float(eps), _code(x._dtype), _STREAM),
     )
     return y, rstd
+
+
+def rope_forward(x: MT, cos: MT, sin: MT, inverse=False) -> MT:
+    """Rotary embedding of x [B, H, T, D] with dense [T, D] tables; the output
+    is allocated [B, T, H, D]-dense (as the attention kernels' inputs are) and
+    returned as a [B, H, T, D] view."""
+    b, h, t, d = x._shape
+    if x._strides[3] != 1 or any(st % 4 for st in x._strides[:3]) or x._ptr % (4 * x._itemsize):
+        x = materialize_contiguous(x)
+    c = _contig(cos) if cos._dtype == x._dtype else materialize_contiguous(cos, x._dtype)
+    sn = _contig(sin) if sin._dtype == x._dtype else materialize_contiguous(sin, x._dtype)
+    out = alloc_bthd(b, h, t, d, x._dtype, x._device)
+    strides = lambda v: _i64(v._strides[:3])  # noqa: E731
+    check(
+        "mi355x_rope",
+        lib().mi355x_rope(out._ptr, strides(out), x._ptr, strides(x), c._ptr, sn._ptr, b, h, t, d, int(inverse),
+                          _code(x._dtype), _STREAM),
+    )
+    return out
+
+
+def geglu_forward(gate: MT, up: MT, approximate: str) -> MT:
+    g, u = _contig(gate), _contig(up)
+    out = _alloc(g._shape, g._dtype, g._device)
+    check(
+        "mi355x_geglu_fwd",
+        lib().mi355x_geglu_fwd(out._ptr, g._ptr, u._ptr, g._numel, 1 if approximate == "tanh" else 0,
+                               _code(g._dtype), _STREAM),
+    )
+    return out
 
 
 # ---------------------------------------------------------------------------

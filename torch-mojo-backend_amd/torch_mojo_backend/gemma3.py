@@ -10,9 +10,11 @@ N(0, 0.02); there is no checkpoint loading (no network).
 
 The model is written with plain torch ops so that it runs unchanged on the
 CPU (the parity reference) and on the mojo device, where the ops land on the
-gfx950 kernels: linear -> GEMM, rms_norm -> the fused RMSNorm, SDPA with
-enable_gqa / a sliding-window mask from torch_mojo_backend.masks -> the
-grouped-query windowed flash forward, gelu(tanh) -> the GELU kernel.
+gfx950 kernels: linear -> GEMM, RMSNorm (1 + w) -> the fused RMSNorm, SDPA
+with enable_gqa / a sliding-window mask from torch_mojo_backend.masks -> the
+grouped-query windowed flash forward, RoPE and GeGLU -> their fused kernels
+(torch_mojo_backend.ops, which falls back to the plain formulas off the
+device).
 """
 
 from __future__ import annotations
@@ -24,6 +26,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import ops
 from .masks import sliding_window_causal_mask
 
 
@@ -53,7 +56,7 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.zeros(dim))
 
     def forward(self, x):
-        return F.rms_norm(x, (x.shape[-1],), 1.0 + self.weight.float(), self.eps)
+        return ops.rms_norm(x, self.weight, self.eps, weight_offset=1.0)
 
 
 def rope_tables(seq_len, dim, base, device, dtype):
@@ -65,9 +68,8 @@ def rope_tables(seq_len, dim, base, device, dtype):
 
 
 def apply_rope(x, cos, sin):
-    half = x.shape[-1] // 2
-    rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
-    return x * cos + rot * sin
+    """x * cos + rotate_half(x) * sin (one fused kernel on the mojo device)."""
+    return ops.rotary_embedding(x, cos, sin)
 
 
 class Attention(nn.Module):
@@ -107,7 +109,7 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(cfg.d_ff, cfg.hidden, bias=False)
 
     def forward(self, x):
-        return self.down_proj(F.gelu(self.gate_proj(x), approximate="tanh") * self.up_proj(x))
+        return self.down_proj(ops.geglu(self.gate_proj(x), self.up_proj(x), approximate="tanh"))
 
 
 class Block(nn.Module):

@@ -166,16 +166,17 @@ def _cross_entropy_loss_autograd(input, target, weight=None, reduction=1, ignore
 
 
 class _FusedRMSNorm(torch.autograd.Function):
-    """rms_norm (the Gemma-3-shaped workload's norm): the forward is one
-    gfx950 kernel that also keeps the row rstd; the backward uses it,
-    dx = r*(g*w) - x * r^3/n * sum(g*w*x) and dw = sum_rows(g*x*r), from
-    device ops in f32."""
+    """rms_norm (the Gemma-3-shaped workload's norm) with scale w (+ an
+    optional constant offset): the forward is one gfx950 kernel that also
+    keeps the row rstd; the backward uses it, dx = r*(g*w) - x * r^3/n *
+    sum(g*w*x) and dw = sum_rows(g*x*r), from device ops in f32."""
 
     @staticmethod
-    def forward(ctx, x, normalized_shape, weight, eps):
-        y, rstd = aten_fast.rms_norm_forward(x, normalized_shape, weight, eps)
+    def forward(ctx, x, normalized_shape, weight, eps, weight_offset=0.0):
+        y, rstd = aten_fast.rms_norm_forward(x, normalized_shape, weight, eps, weight_offset)
         ctx.save_for_backward(x, weight, rstd)
         ctx.n = len(normalized_shape)
+        ctx.offset = weight_offset
         return y
 
     @staticmethod
@@ -188,14 +189,14 @@ class _FusedRMSNorm(torch.autograd.Function):
             n *= x.shape[d]
         xf, gf = x.float(), grad.float()
         r = rstd.view(tuple(x.shape[: x.dim() - nd]) + (1,) * nd)
-        gw = gf * weight.float() if weight is not None else gf
+        gw = gf * (weight.float() + ctx.offset) if weight is not None else gf
         dot = (gw * xf).sum(dim=dims, keepdim=True)
         dx = (r * gw - xf * (r * r * r) * (dot / n)).to(x.dtype) if ctx.needs_input_grad[0] else None
         dw = None
         if weight is not None and ctx.needs_input_grad[2]:
             lead = tuple(range(x.dim() - nd))
             dw = (gf * xf * r).sum(dim=lead).to(weight.dtype) if lead else (gf * xf * r).to(weight.dtype)
-        return dx, None, dw, None
+        return dx, None, dw, None, None
 
 
 def _rms_norm_autograd(input, normalized_shape, weight=None, eps=None):
