@@ -302,3 +302,40 @@ def test_fused_gemma_ops_gradients(mojo):
 
     for a, b in zip(run("mojo"), run("cpu")):
         assert torch.allclose(a, b, atol=1e-5, rtol=1e-5), (a - b).abs().max()
+
+
+def test_allocation_retries_once_after_out_of_memory(mojo, monkeypatch):
+    """An allocation the allocator refuses is retried once after releasing
+    cached blocks (the reference's drain-and-retry,
+    torch_mojo_tensor.py:213-244); a second refusal propagates."""
+    from torch_mojo_backend.mojo_device import torch_mojo_tensor as tm
+
+    real = torch.empty
+    fails = {"n": 1}
+
+    def flaky(*a, **k):
+        if fails["n"] > 0:
+            fails["n"] -= 1
+            raise torch.OutOfMemoryError("out of memory (test)")
+        return real(*a, **k)
+
+    monkeypatch.setattr(tm.torch, "empty", flaky)
+    x = torch.ones(5).to("mojo")
+    assert torch.equal(x.cpu(), torch.ones(5))
+    fails["n"] = 2
+    with pytest.raises(torch.OutOfMemoryError):
+        torch.ones(7).to("mojo")
+
+
+def test_checkpoints_pickle_as_cpu_tensors(mojo, tmp_path):
+    """torch.save of device tensors and state_dicts writes plain CPU tensors
+    (torch_mojo_tensor.py:572-583), so the file loads without the backend."""
+    lin = torch.nn.Linear(4, 3)
+    ref = {k: v.clone() for k, v in lin.state_dict().items()}
+    lin.to("mojo")
+    path = tmp_path / "ckpt.pt"
+    torch.save({"model": lin.state_dict(), "t": torch.arange(6.0).to("mojo")}, path)
+    loaded = torch.load(path, weights_only=True)
+    assert loaded["t"].device.type == "cpu" and torch.equal(loaded["t"], torch.arange(6.0))
+    for k, v in ref.items():
+        assert loaded["model"][k].device.type == "cpu" and torch.equal(loaded["model"][k], v)
