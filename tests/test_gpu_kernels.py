@@ -191,7 +191,9 @@ def test_embedding_backward_bit_exact_vs_sequential_f32(kernels):
 # layer norm / gelu / softmax / nll
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype,rows,cols", [(torch.float32, 16384, 768), (torch.float32, 33, 1000),
-                                             (torch.bfloat16, 300, 768), (torch.float32, 7, 4099)])
+                                             (torch.bfloat16, 300, 768), (torch.float32, 7, 4099),
+                                             (torch.float32, 8197, 768), (torch.bfloat16, 3, 256),
+                                             (torch.float32, 100, 2048)])
 def test_layer_norm_fwd_bwd(kernels, dtype, rows, cols):
     x = randn(rows, cols) * 3 + 1
     g, b = randn(cols), randn(cols)

@@ -10,7 +10,8 @@
 //   xhat = (x-mean)*rstd, g = dy*gamma,
 //   dx   = rstd * (g - mean(g) - xhat*mean(g*xhat)),
 // while each lane accumulates dgamma += dy*xhat and dbeta += dy for its
-// columns over the rows its block owns.  Block partials go to a workspace
+// columns over the rows its block owns.  Each wave loads its next row before
+// it computes the current one.  Block partials go to a workspace
 // [blocks, cols] and a second kernel sums them in a fixed order, so the
 // result is deterministic.
 #include "common.h"
@@ -174,78 +175,103 @@ __global__ void __launch_bounds__(kThreads)
   if (threadIdx.x == 0 && rstd_out) rstd_out[row] = r;
 }
 
+// One row of x and dy for this lane's columns.  Columns past `cols` read
+// column 0 (always in bounds) and are zeroed, so the loads need no branch and
+// the row stays in registers.
 template <typename T, int NV>
-__global__ void __launch_bounds__(kThreads)
+__device__ __forceinline__ void ln_load_row(const T* __restrict__ x, const T* __restrict__ dy, int64_t base,
+                                            const int (&coff)[NV], const bool (&cv)[NV], float (&xv)[NV][4],
+                                            float (&dv)[NV][4]) {
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    Vec4<T>::load(x + base + coff[j], xv[j]);
+    Vec4<T>::load(dy + base + coff[j], dv[j]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xv[j][e] = cv[j] ? xv[j][e] : 0.f;
+      dv[j][e] = cv[j] ? dv[j][e] : 0.f;
+    }
+  }
+}
+
+template <typename T, int NV, int W>
+__global__ void __launch_bounds__(64 * W)
     ln_bwd_wave(T* __restrict__ dx, float* __restrict__ part_g, float* __restrict__ part_b,
                 const T* __restrict__ dy, const T* __restrict__ x, const float* __restrict__ mean,
                 const float* __restrict__ rstd, const T* __restrict__ gamma, int64_t rows, int cols,
                 int64_t rows_per_block) {
-  __shared__ float lds[2][kWaves][NV * 256];
+  __shared__ float lds[2][W][NV * 256];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const bool want_params = part_g != nullptr;
+  int coff[NV];
+  bool cv[NV];
   float pg[NV][4], pb[NV][4], gm[NV][4];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (j * 64 + lane) * 4;
+    cv[j] = c < cols;
+    coff[j] = cv[j] ? c : 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) pg[j][e] = pb[j][e] = 0.f, gm[j][e] = 1.f;
-    if (gamma && c < cols) Vec4<T>::load(gamma + c, gm[j]);
+    if (gamma) {
+      Vec4<T>::load(gamma + coff[j], gm[j]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gm[j][e] = cv[j] ? gm[j][e] : 0.f;
+    }
   }
   const float inv_n = 1.f / (float)cols;
   const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
   const int64_t r1 = min(rows, r0 + rows_per_block);
-  // One row's dx and its contribution to this lane's dgamma/dbeta columns.
-  auto process = [&](int64_t row, const float (&xv)[NV][4], const float (&dv)[NV][4]) {
-    const float mu = mean[row], rs = rstd[row];
+  // The host sizes the grid so every block owns at least one row.  Each wave
+  // takes rows r0+wid, r0+wid+W, ... and loads the next one before it
+  // computes the current one (the last prefetch re-reads row r1-1).
+  const int64_t last = r1 - 1;
+  int64_t row = r0 + wid;
+  float xa[NV][4], da[NV][4];
+  float mu = 0.f, rs = 0.f;
+  {
+    const int64_t first = min(row, last);
+    ln_load_row<T, NV>(x, dy, first * cols, coff, cv, xa, da);
+    mu = mean[first];
+    rs = rstd[first];
+  }
+  for (; row < r1; row += W) {
+    const int64_t nxt = min(row + W, last);
+    float xn[NV][4], dn[NV][4];
+    ln_load_row<T, NV>(x, dy, nxt * cols, coff, cv, xn, dn);
+    const float mu_n = mean[nxt], rs_n = rstd[nxt];
     float xh[NV][4], gy[NV][4];
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
     for (int j = 0; j < NV; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        xh[j][e] = (xv[j][e] - mu) * rs;
-        gy[j][e] = dv[j][e] * gm[j][e];
+        xh[j][e] = (xa[j][e] - mu) * rs;
+        gy[j][e] = da[j][e] * gm[j][e];
         s1 += gy[j][e];
         s2 += gy[j][e] * xh[j][e];
-        pg[j][e] += dv[j][e] * xh[j][e];
-        pb[j][e] += dv[j][e];
+        pg[j][e] += da[j][e] * xh[j][e];
+        pb[j][e] += da[j][e];
       }
     if (dx) {
       const float m1 = wave_sum(s1) * inv_n;
       const float m2 = wave_sum(s2) * inv_n;
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        const int c = (j * 64 + lane) * 4;
-        if (c < cols) {
+        if (cv[j]) {
           float o[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = rs * (gy[j][e] - m1 - xh[j][e] * m2);
-          Vec4<T>::store(dx + row * cols + c, o);
+          Vec4<T>::store(dx + row * cols + coff[j], o);
         }
       }
     }
-  };
-  auto load = [&](int64_t row, float (&xv)[NV][4], float (&dv)[NV][4]) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int c = (j * 64 + lane) * 4;
-      if (c < cols) {
-        Vec4<T>::load(x + row * cols + c, xv[j]);
-        Vec4<T>::load(dy + row * cols + c, dv[j]);
-      } else {
+    for (int j = 0; j < NV; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xv[j][e] = dv[j][e] = 0.f;
-      }
-    }
-  };
-  // Two rows per iteration, both rows' loads issued before either is used.
-  for (int64_t row = r0 + wid; row < r1; row += 2 * kWaves) {
-    const int64_t row2 = row + kWaves;
-    float xa[NV][4], da[NV][4], xb[NV][4], db[NV][4];
-    load(row, xa, da);
-    if (row2 < r1) load(row2, xb, db);
-    process(row, xa, da);
-    if (row2 < r1) process(row2, xb, db);
+      for (int e = 0; e < 4; ++e) xa[j][e] = xn[j][e], da[j][e] = dn[j][e];
+    mu = mu_n;
+    rs = rs_n;
   }
   if (!want_params) return;
 #pragma unroll
@@ -256,10 +282,10 @@ __global__ void __launch_bounds__(kThreads)
       lds[1][wid][(j * 64 + lane) * 4 + e] = pb[j][e];
     }
   __syncthreads();
-  for (int c = threadIdx.x; c < cols; c += kThreads) {
+  for (int c = threadIdx.x; c < cols; c += 64 * W) {
     float g = 0.f, b = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) g += lds[0][w][c], b += lds[1][w][c];
+    for (int w = 0; w < W; ++w) g += lds[0][w][c], b += lds[1][w][c];
     part_g[(int64_t)blockIdx.x * cols + c] = g;
     part_b[(int64_t)blockIdx.x * cols + c] = b;
   }
@@ -311,44 +337,46 @@ __global__ void __launch_bounds__(kThreads)
   part_b[(int64_t)blockIdx.y * cols + c] = b;
 }
 
-// dgamma/dbeta = sum of the block partials, in two fixed-order passes so
-// the result is deterministic and each pass has enough blocks in flight:
-//   mid:   group y of kGroups sums partials [y*per, (y+1)*per) for 64
-//          columns per block (4 lanes per column, combined through LDS);
-//   final: one thread per column sums the kGroups group sums in order.
-constexpr int kGroups = 16;
+// dgamma/dbeta = sum of the block partials [nparts, cols] in a fixed order,
+// so the result is deterministic.  A block owns 16 columns; its 16 row groups
+// (ty) each sum partials ty, ty+16, ... with every load issued before the
+// adds, then group sums are combined in LDS in group order.  With at most a
+// few hundred partials this is one latency-bound pass over an L2-resident
+// workspace.
+constexpr int kSumCols = 16, kSumGroups = 16;
 
-__global__ void __launch_bounds__(kThreads)
-    ln_bwd_params_mid(float* __restrict__ mid_g, float* __restrict__ mid_b, const float* __restrict__ part_g,
+template <typename T>
+__global__ void __launch_bounds__(kSumCols * kSumGroups)
+    ln_bwd_params_sum(T* __restrict__ dgamma, T* __restrict__ dbeta, const float* __restrict__ part_g,
                       const float* __restrict__ part_b, int nparts, int64_t cols) {
-  __shared__ float lg[4][65], lb[4][65];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int64_t c = (int64_t)blockIdx.x * 64 + tx;
-  const int per = (nparts + kGroups - 1) / kGroups;
-  const int p0 = blockIdx.y * per, p1 = min(nparts, p0 + per);
+  __shared__ float lg[kSumGroups][kSumCols + 1], lb[kSumGroups][kSumCols + 1];
+  const int tx = threadIdx.x % kSumCols, ty = threadIdx.x / kSumCols;
+  const int64_t c = (int64_t)blockIdx.x * kSumCols + tx;
   float g = 0.f, b = 0.f;
-  if (c < cols)
-    for (int q = p0 + ty; q < p1; q += 4) g += part_g[(int64_t)q * cols + c], b += part_b[(int64_t)q * cols + c];
+  if (c < cols) {
+    int q = ty;
+    for (; q + 3 * kSumGroups < nparts; q += 4 * kSumGroups) {
+      float vg[4], vb[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        vg[u] = part_g[(int64_t)(q + u * kSumGroups) * cols + c];
+        vb[u] = part_b[(int64_t)(q + u * kSumGroups) * cols + c];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) g += vg[u], b += vb[u];
+    }
+    for (; q < nparts; q += kSumGroups) g += part_g[(int64_t)q * cols + c], b += part_b[(int64_t)q * cols + c];
+  }
   lg[ty][tx] = g;
   lb[ty][tx] = b;
   __syncthreads();
   if (ty == 0 && c < cols) {
-    mid_g[(int64_t)blockIdx.y * cols + c] = (lg[0][tx] + lg[1][tx]) + (lg[2][tx] + lg[3][tx]);
-    mid_b[(int64_t)blockIdx.y * cols + c] = (lb[0][tx] + lb[1][tx]) + (lb[2][tx] + lb[3][tx]);
-  }
-}
-
-template <typename T>
-__global__ void __launch_bounds__(kThreads)
-    ln_bwd_params_final(T* __restrict__ dgamma, T* __restrict__ dbeta, const float* __restrict__ mid_g,
-                        const float* __restrict__ mid_b, int64_t cols) {
-  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (c >= cols) return;
-  float g = 0.f, b = 0.f;
+    float sg = 0.f, sb = 0.f;
 #pragma unroll
-  for (int y = 0; y < kGroups; ++y) g += mid_g[(int64_t)y * cols + c], b += mid_b[(int64_t)y * cols + c];
-  if (dgamma) dgamma[c] = from_f32<T>(g);
-  if (dbeta) dbeta[c] = from_f32<T>(b);
+    for (int y = 0; y < kSumGroups; ++y) sg += lg[y][tx], sb += lb[y][tx];
+    if (dgamma) dgamma[c] = from_f32<T>(sg);
+    if (dbeta) dbeta[c] = from_f32<T>(sb);
+  }
 }
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -363,11 +391,27 @@ int wave_nv(int64_t cols) {
   return 8;
 }
 
-int bwd_blocks(int64_t rows) {
-  int64_t b = (rows + 15) / 16;
+// Backward rows per block: about 16 (four per wave), with at most
+// kMaxBwdBlocks partials; the block count is then trimmed so that every block
+// owns at least one row.
+int64_t bwd_rows_per_block(int64_t rows) {
+  static const char* forced = getenv("MI355X_LN_BWD_BLOCKS");  // tuning override: maximum block count
+  const int64_t max_blocks = forced ? atoll(forced) : 256;
+  int64_t b = (rows + 31) / 32;
+  if (b > max_blocks) b = max_blocks;
   if (b > kMaxBwdBlocks) b = kMaxBwdBlocks;
   if (b < 1) b = 1;
-  return (int)b;
+  return rows > 0 ? (rows + b - 1) / b : 1;
+}
+
+int bwd_waves() {
+  static const char* forced = getenv("MI355X_LN_BWD_WAVES");  // tuning override: 4 or 8
+  return forced && atoi(forced) == 8 ? 8 : 4;
+}
+
+int bwd_blocks(int64_t rows) {
+  const int64_t rpb = bwd_rows_per_block(rows);
+  return rows > 0 ? (int)((rows + rpb - 1) / rpb) : 1;
 }
 
 template <typename T>
@@ -417,7 +461,7 @@ int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* m
              hipStream_t s) {
   const bool params = dgamma || dbeta;
   const int nb = bwd_blocks(rows);
-  const int64_t rpb = (rows + nb - 1) / nb;
+  const int64_t rpb = bwd_rows_per_block(rows);
   float* pg = params ? ws : nullptr;
   float* pb = params ? ws + (int64_t)nb * cols : nullptr;
   const size_t al = 4 * sizeof(T);
@@ -427,7 +471,11 @@ int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* m
     switch (nv) {
 #define LN_BWD_CASE(V)                                                                          \
   case V:                                                                                       \
-    ln_bwd_wave<T, V><<<nb, kThreads, 0, s>>>(dx, pg, pb, dy, x, mean, rstd, gamma, rows,       \
+    if (bwd_waves() == 8)                                                                       \
+      ln_bwd_wave<T, V, 8><<<nb, 512, 0, s>>>(dx, pg, pb, dy, x, mean, rstd, gamma, rows,       \
+                                              (int)cols, rpb);                                  \
+    else                                                                                        \
+      ln_bwd_wave<T, V, 4><<<nb, 256, 0, s>>>(dx, pg, pb, dy, x, mean, rstd, gamma, rows,       \
                                               (int)cols, rpb);                                  \
     break;
       LN_BWD_CASE(1)
@@ -445,10 +493,8 @@ int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* m
     }
   }
   if (params) {
-    float* mg = ws + 2 * (int64_t)nb * cols;
-    float* mb = mg + (int64_t)kGroups * cols;
-    ln_bwd_params_mid<<<dim3(ceil_div(cols, 64), kGroups), kThreads, 0, s>>>(mg, mb, pg, pb, nb, cols);
-    ln_bwd_params_final<T><<<ceil_div(cols, kThreads), kThreads, 0, s>>>(dgamma, dbeta, mg, mb, cols);
+    ln_bwd_params_sum<T><<<ceil_div(cols, kSumCols), kSumCols * kSumGroups, 0, s>>>(dgamma, dbeta, pg, pb,
+                                                                                   nb, cols);
   }
   return check_launch("mi355x_layer_norm_bwd");
 }
@@ -481,7 +527,7 @@ extern "C" int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const vo
 }
 
 extern "C" int64_t mi355x_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t cols) {
-  return 2 * ((int64_t)bwd_blocks(rows) + kGroups) * cols * (int64_t)sizeof(float);
+  return 2 * (int64_t)bwd_blocks(rows) * cols * (int64_t)sizeof(float);
 }
 
 extern "C" int mi355x_layer_norm_bwd(void* dx, void* dgamma, void* dbeta, const void* dy,
