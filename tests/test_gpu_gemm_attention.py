@@ -109,18 +109,21 @@ def test_gemm_accumulate_and_batched(kernels):
     tol_close(np64(tc), exp, atol=2e-2, rtol=1e-2, what="batched beta=1")
 
 
-def test_gemm_split_k_with_bias_and_beta(kernels):
-    """Small C, long K (the weight-gradient regime) takes the split-K path."""
-    m, n, k = 96, 80, 8192
+@pytest.mark.parametrize("n,c_dtype", [(80, torch.float32), (78, torch.float32), (80, torch.bfloat16)])
+def test_gemm_split_k_with_bias_and_beta(kernels, n, c_dtype):
+    """Small C, long K (the weight-gradient regime) takes the split-K path:
+    the 4-column reduction (n % 4 == 0) and the scalar one, f32 and bf16 C."""
+    m, k = 96, 8192
     assert lib().mi355x_gemm_workspace_bytes(None, 1, m, 0, None, n, 1, 0, 1, 1, m, n, k) > 0
     A = randn(k, m).bfloat16()  # stored m-contiguous: A(m, k) = A_store[k, m]
     B = randn(k, n).bfloat16()
     bias = randn(n)
-    C0 = randn(m, n)
+    C0 = randn(m, n).to(c_dtype)
     tc = dev(C0)
     _gemm(tc, dev(A), dev(B), m, n, k, 1, m, n, 1, torch.bfloat16, bias=dev(bias), beta=1)
     exp = C0.double().numpy() + A.double().numpy().T @ B.double().numpy() + bias.double().numpy()
-    tol_close(np64(tc), exp, atol=0.5, rtol=1e-2, what="split-K")
+    atol = 0.5 if c_dtype == torch.float32 else 1.0
+    tol_close(np64(tc), exp, atol=atol, rtol=1e-2, what="split-K")
 
 
 @pytest.mark.parametrize("K,N", [(768, 2304), (3072, 768)])

@@ -38,6 +38,7 @@
 
 #include "common.h"
 #include "mfma.h"
+#include "vec.h"
 
 extern __shared__ __attribute__((aligned(16))) char gemm_smem[];
 
@@ -105,6 +106,40 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs g, int splits, int
     if (g.beta) v += ld_any(Cb, g.c_dt, off);
     if (g.round_c) v = round_through(v, g.ab_dt);
     st_any(Cb, g.c_dt, off, v);
+  }
+}
+
+// splitk_reduce for n % 4 == 0 with 4-aligned C strides and fewer than 2^31
+// elements: each thread sums four adjacent columns with 16-byte partial
+// loads and 32-bit index math.
+template <typename CT>
+__global__ void __launch_bounds__(256) splitk_reduce4(GemmArgs g, int splits, int nb) {
+  const uint32_t n4 = (uint32_t)(g.n / 4), mn4 = (uint32_t)g.m * n4;
+  const uint32_t total = (uint32_t)nb * mn4;
+  const float4* P = (const float4*)g.part;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    const uint32_t bi = i / mn4, rem = i - bi * mn4;
+    const uint32_t row = rem / n4, col = (rem - row * n4) * 4;
+    float4 a = P[i];
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4 q = P[(uint32_t)sp * total + i];
+      a.x += q.x, a.y += q.y, a.z += q.z, a.w += q.w;
+    }
+    float v[4] = {a.x, a.y, a.z, a.w};
+    if (g.bias)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += ld_any(g.bias, g.bias_dt, col + e);
+    CT* C = (CT*)g.c + (int64_t)bi * g.c_bs + (int64_t)row * g.c_rs + col;
+    float old[4];
+    if (g.beta) {
+      Vec4<CT>::load(C, old);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += old[e];
+    }
+    if (g.round_c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = round_through(v[e], g.ab_dt);
+    Vec4<CT>::store(C, v);
   }
 }
 
@@ -277,20 +312,31 @@ __device__ __forceinline__ void mask_k(F& f, int64_t kbase, int64_t kend) {
 }
 
 // Block configurations.
+#ifndef GEMM_STAGES_128
+#define GEMM_STAGES_128 2
+#endif
+#ifndef GEMM_STAGES_192
+#define GEMM_STAGES_192 2
+#endif
 template <int CFG>
 struct TileCfg;
 template <>
 struct TileCfg<0> {  // C128
-  static constexpr int BM = 128, BN = 128, WGM = 2, WGN = 2, MIN_BLOCKS = 2;
+  static constexpr int BM = 128, BN = 128, WGM = 2, WGN = 2, STAGES = GEMM_STAGES_128;
+  static constexpr int MIN_BLOCKS = STAGES * (BM + BN) * 128 * 2 <= 160 * 1024 ? 2 : 1;
 };
 template <>
 struct TileCfg<1> {  // C256
-  static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 4, MIN_BLOCKS = 1;
+  static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 4, STAGES = 2, MIN_BLOCKS = 1;
 };
 template <>
-struct TileCfg<2> {  // C192: 128x192, waves of 64x96, 80 KB LDS, two blocks per CU (k-contiguous B only)
-  static constexpr int BM = 128, BN = 192, WGM = 2, WGN = 2, MIN_BLOCKS = 2;
+struct TileCfg<2> {  // C192: 128x192, waves of 64x96, 40 KB per stage (k-contiguous B only)
+  static constexpr int BM = 128, BN = 192, WGM = 2, WGN = 2, STAGES = GEMM_STAGES_192;
+  static constexpr int MIN_BLOCKS = STAGES * (BM + BN) * 128 * 2 <= 160 * 1024 ? 2 : 1;
 };
+
+// s_waitcnt immediate for vmcnt(n), other counters not waited on.
+constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 15) | ((n >> 4) << 14); }
 
 // Write one wave's accumulators to C (pointing at the wave tile's first
 // element), adding the preloaded bias and, with BETA, the old C.  Offsets
@@ -353,7 +399,7 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   constexpr int NT = 64 * C::WGM * C::WGN;
   constexpr int WM = BM / C::WGM, WN = BN / C::WGN;
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int A_BYTES = BM * 128, STAGE = A_BYTES + BN * 128;
+  constexpr int A_BYTES = BM * 128, STAGE = A_BYTES + BN * 128, S = C::STAGES;
   char* const lds = gemm_smem;
 
   // XCD-aware tile order within one (split, batch) plane.
@@ -387,10 +433,18 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
 
   OperandLoad<BM, NT, A_K> la;
   OperandLoad<BN, NT, B_K> lb;
+  constexpr int PER_STAGE = decltype(la.t)::ITERS + decltype(lb.t)::ITERS;  // DMA instructions per stage
+  static_assert(S == 2 || (S - 2) * PER_STAGE < 64, "vmcnt range");
   la.init(A, a_ldb, m0, g.m);
   lb.init(B, b_ldb, n0, g.n);
-  la.template issue<KT>(kbeg, lds, kend);
-  lb.template issue<KT>(kbeg, lds + A_BYTES, kend);
+  // Prologue: stages 0 .. S-2 in flight.
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st) {
+    if (kbeg + st * 64 < kend) {
+      la.template issue<KT>(kbeg + st * 64, lds + st * STAGE, kend);
+      lb.template issue<KT>(kbeg + st * 64, lds + st * STAGE + A_BYTES, kend);
+    }
+  }
   // k-contiguous fragment rows (.. + lr) share the swizzle of lr
   const int sw = (lr >> 1) & 7;
   const int rs_slots = g.part ? g.tiles_n * C::WGN : 1;
@@ -406,12 +460,16 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
 
   int cur = 0;
   for (int64_t k0 = kbeg; k0 < kend; k0 += 64) {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this step's tiles have landed
+    // This step's tiles have landed when at most the later stages' loads
+    // (S-2 stages, if issued) are still outstanding.
+    if (S > 2 && k0 + (S - 2) * 64 < kend) __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * PER_STAGE));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
-    if (k0 + 64 < kend) {
-      char* nxt = lds + (cur ^ 1) * STAGE;
-      la.template issue<KT>(k0 + 64, nxt, kend);
-      lb.template issue<KT>(k0 + 64, nxt + A_BYTES, kend);
+    if (k0 + (S - 1) * 64 < kend) {
+      // the slot read in the previous step; every wave is past it
+      char* nxt = lds + (cur == 0 ? S - 1 : cur - 1) * STAGE;
+      la.template issue<KT>(k0 + (S - 1) * 64, nxt, kend);
+      lb.template issue<KT>(k0 + (S - 1) * 64, nxt + A_BYTES, kend);
     }
     const char* at = lds + cur * STAGE;
     const char* bt = at + A_BYTES;
@@ -441,7 +499,7 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
         for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af, bfr[j], acc[i][j]);
       }
     }
-    cur ^= 1;
+    cur = cur == S - 1 ? 0 : cur + 1;
   }
 
   const int64_t row0 = m0 + wm * WM, col0 = n0 + wn * WN;
@@ -516,6 +574,63 @@ __global__ void __launch_bounds__(256) pack_k_contig(uint16_t* __restrict__ dst,
       const int64_t r = row0 + i, k = k0 + tx;
       if (r < rows && k < ld) D[r * ld + k] = k < kdim ? S[r * stride + k] : (uint16_t)0;
     }
+  }
+}
+
+// pack_k_contig with 16-byte global accesses, for sources whose base, row or
+// k stride and batch stride are 8-element aligned (and, transposed, whose row
+// count is a multiple of 8).  A 64x64 tile moves as 512 16-byte chunks, two
+// per thread each way.  The LDS tile is [k][row] with a 65-element pitch: the
+// 2-byte scatter of a loaded chunk and the 2-byte gather of a stored one then
+// hit distinct banks across the wave.
+__global__ void __launch_bounds__(256) pack_k_contig_v8(uint16_t* __restrict__ dst, int64_t ld,
+                                                        int64_t dst_bs, const uint16_t* __restrict__ src,
+                                                        int64_t stride, int64_t sbs, int64_t rows,
+                                                        int64_t kdim, int transposed) {
+  const int64_t b = blockIdx.z;
+  const int64_t row0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  const uint16_t* S = src + b * sbs;
+  uint16_t* D = dst + b * dst_bs;
+  const int t = threadIdx.x;
+  if (!transposed) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t r = row0 + (t >> 3) + 32 * j, k = k0 + (t & 7) * 8;
+      if (r >= rows || k >= ld) continue;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (k + 8 <= kdim) {
+        v = *(const uint4*)(S + r * stride + k);
+      } else if (k < kdim) {
+        uint16_t e8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) e8[e] = k + e < kdim ? S[r * stride + k + e] : (uint16_t)0;
+        v = *(const uint4*)e8;
+      }
+      *(uint4*)(D + r * ld + k) = v;
+    }
+    return;
+  }
+  __shared__ uint16_t tile[64][65];  // [k][row]
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int kl = (t >> 3) + 32 * j, rl = (t & 7) * 8;
+    const int64_t k = k0 + kl, r = row0 + rl;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (k < kdim && r < rows) v = *(const uint4*)(S + k * stride + r);
+    const uint16_t* e8 = (const uint16_t*)&v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[kl][rl + e] = e8[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int rl = (t >> 3) + 32 * j, kc = (t & 7) * 8;
+    const int64_t r = row0 + rl, k = k0 + kc;
+    if (r >= rows || k >= ld) continue;
+    uint16_t e8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) e8[e] = tile[kc + e][rl];
+    *(uint4*)(D + r * ld + k) = *(const uint4*)e8;
   }
 }
 
@@ -632,7 +747,7 @@ template <typename T, int CFG, bool A_K, bool B_K, bool KT, bool RS>
 int launch_kernel(const GemmArgs& g, dim3 grid, hipStream_t s) {
   typedef TileCfg<CFG> C;
   constexpr int NT = 64 * C::WGM * C::WGN;
-  constexpr size_t lds = 2 * (size_t)(C::BM + C::BN) * 128;
+  constexpr size_t lds = C::STAGES * (size_t)(C::BM + C::BN) * 128;
   static bool attr = false;
   if (lds > 65536 && !attr) {
     if (hipFuncSetAttribute((const void*)gemm_tile<T, CFG, A_K, B_K, KT, RS>,
@@ -672,6 +787,18 @@ int launch_tile(GemmArgs g, int64_t batch, int splits, hipStream_t s) {
 
 int splitk_finish(const GemmArgs& g, int64_t batch, int splits, hipStream_t s) {
   const int64_t total = batch * g.m * g.n;
+  const int64_t c_align = g.c_dt == MI355X_F32 ? 16 : 8;
+  if (g.n % 4 == 0 && g.c_rs % 4 == 0 && g.c_bs % 4 == 0 && (uintptr_t)g.c % c_align == 0 &&
+      (int64_t)splits * total < (1ll << 31)) {
+    int64_t blocks = (total / 4 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    switch (g.c_dt) {
+      case MI355X_F32: splitk_reduce4<float><<<(unsigned)blocks, 256, 0, s>>>(g, splits, (int)batch); break;
+      case MI355X_BF16: splitk_reduce4<bf16><<<(unsigned)blocks, 256, 0, s>>>(g, splits, (int)batch); break;
+      default: splitk_reduce4<f16><<<(unsigned)blocks, 256, 0, s>>>(g, splits, (int)batch); break;
+    }
+    return check_launch("mi355x_gemm splitk_reduce");
+  }
   int64_t blocks = (total + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(g, splits, batch);
@@ -746,6 +873,14 @@ int pack(uint16_t* dst, const void* src, int64_t batch, int64_t rows, int64_t kd
   // row_stride == 1: rows contiguous (transpose); else k_stride == 1 (straight)
   const bool transposed = row_stride == 1 && k_stride != 1;
   dim3 grid(ceil_div(ld, 64), ceil_div(rows, 64), (unsigned)batch);
+  const int64_t stride = transposed ? k_stride : row_stride;
+  const bool v8 = aligned16(src) && stride % 8 == 0 && sbs % 8 == 0 && ld % 64 == 0 &&
+                  (!transposed || rows % 8 == 0);
+  if (v8) {
+    pack_k_contig_v8<<<grid, 256, 0, s>>>(dst, ld, rows * ld, (const uint16_t*)src, stride, sbs, rows, kdim,
+                                          transposed ? 1 : 0);
+    return check_launch("mi355x_gemm pack");
+  }
   pack_k_contig<<<grid, 256, 0, s>>>(dst, ld, rows * ld, (const uint16_t*)src,
                                       transposed ? k_stride : row_stride, sbs, rows, kdim,
                                       transposed ? 1 : 0);
