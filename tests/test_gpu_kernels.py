@@ -401,6 +401,51 @@ def test_foreach_norm_and_apply(kernels):
         assert torch.equal(host(t), x * 0.25)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_foreach_norm_orders_and_apply_ops(kernels, dtype):
+    """Every norm order and the list/scalar forms of ADD, ADDCMUL, LERP and
+    SQRT, on sizes that exercise the 16-byte paths, their odd tails and a
+    tensor that starts off a 16-byte boundary."""
+    sizes = [3 * 32768 + 5, 16384 * 2, 1001, 9]
+    base = [randn(s + 1).to(dtype) for s in sizes]
+    xs = [b[1:] if i == 3 else b[:-1] for i, b in enumerate(base)]  # the last one is misaligned
+    tbase = [dev(b) for b in base]
+    tx = [tb[1:] if i == 3 else tb[:-1] for i, tb in enumerate(tbase)]
+    numels = i64(*sizes)
+    n = len(sizes)
+    ws_n = lib().mi355x_foreach_norm_workspace_bytes(numels, n)
+    ws = workspace(ws_n)
+    ptr = lambda ts: (ctypes.c_void_p * n)(*[p(t) for t in ts])
+    for ord_, ref in ((2.0, lambda v: v.double().norm()), (1.0, lambda v: v.double().abs().sum()),
+                      (float("inf"), lambda v: v.double().abs().max())):
+        outs = [torch.empty((), device="cuda") for _ in sizes]
+        call("mi355x_foreach_norm", ptr(outs), 0, ptr(tx), CODE[dtype], numels, n, ord_, p(ws), ws_n, None)
+        for o, x in zip(outs, xs):
+            r = ref(x).item()
+            assert abs(host(o).item() - r) <= 1e-5 * max(1.0, r), (ord_, host(o).item(), r)
+    ys = [randn(s).to(dtype) for s in sizes]
+    zs = [(randn(s).abs() + 0.5).to(dtype) for s in sizes]
+    ty, tz = [dev(y) for y in ys], [dev(z) for z in zs]
+    atol = 1e-6 if dtype == torch.float32 else 2e-2
+    cur = [x.float() for x in xs]
+    call("mi355x_foreach_apply", 0, ptr(tx), ptr(ty), None, None, numels, n, CODE[dtype], 0.5, None, None)
+    cur = [(c + 0.5 * y.float()).to(dtype).float() for c, y in zip(cur, ys)]
+    scal = (ctypes.c_double * n)(*[0.1 * (i + 1) for i in range(n)])
+    call("mi355x_foreach_apply", 41, ptr(tx), ptr(ty), ptr(tz), scal, numels, n, CODE[dtype], 0.0, None, None)
+    cur = [(c + 0.1 * (i + 1) * y.float() * z.float()).to(dtype).float() for i, (c, y, z) in enumerate(zip(cur, ys, zs))]
+    call("mi355x_foreach_apply", 43, ptr(tx), ptr(tz), None, None, numels, n, CODE[dtype], 0.25, None, None)
+    cur = [(c + 0.25 * (z.float() - c)).to(dtype).float() for c, z in zip(cur, zs)]
+    cur = [c.abs() for c in cur]
+    for t, c in zip(tx, cur):
+        t.copy_(c.to(dtype).to(t.device))
+    call("mi355x_foreach_apply", 65, ptr(tx), None, None, None, numels, n, CODE[dtype], 0.0, None, None)
+    cur = [c.sqrt().to(dtype).float() for c in cur]
+    for i, (t, c) in enumerate(zip(tx, cur)):
+        tol_close(host(t).float().numpy(), c.double().numpy(), atol=atol, rtol=atol, what=f"apply {i}")
+    # the misaligned tensor's neighbours in its base allocation are untouched
+    assert torch.equal(host(tbase[3])[:1], base[3][:1])
+
+
 @pytest.mark.parametrize("cols", [1152, 256, 100])
 @pytest.mark.parametrize("dtype,wdt", [(torch.float32, torch.float32), (torch.bfloat16, torch.float32),
                                         (torch.bfloat16, torch.bfloat16)])

@@ -84,12 +84,9 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
   int64_t i = begin;
   if (vec) {
     const int64_t nv = (end - begin) / 4;
-    for (int64_t q = threadIdx.x; q < nv; q += kThreads) {
-      const int64_t e = begin + q * 4;
-      float4 p = *(float4*)(t.param + e);
-      float4 g = *(const float4*)(t.grad + e);
-      float4 m = *(float4*)(t.exp_avg + e);
-      float4 v = *(float4*)(t.exp_avg_sq + e);
+    // Two float4 of each array per thread per iteration: all eight loads are
+    // in flight before the first update.
+    auto update = [&](float4& p, const float4& g, float4& m, float4& v) {
       float gg[4] = {g.x, g.y, g.z, g.w};
       float pp[4] = {p.x, p.y, p.z, p.w}, mm[4] = {m.x, m.y, m.z, m.w}, vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -97,9 +94,31 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
         float gj = (maximize ? -gg[j] : gg[j]) * inv_scale;
         adam_elem(pp[j], gj, mm[j], vv[j], nullptr, lr, s.b1, s.b2, s.wd, s.eps, step_size, bc2_sqrt, decay);
       }
-      *(float4*)(t.param + e) = make_float4(pp[0], pp[1], pp[2], pp[3]);
-      *(float4*)(t.exp_avg + e) = make_float4(mm[0], mm[1], mm[2], mm[3]);
-      *(float4*)(t.exp_avg_sq + e) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+      p = make_float4(pp[0], pp[1], pp[2], pp[3]);
+      m = make_float4(mm[0], mm[1], mm[2], mm[3]);
+      v = make_float4(vv[0], vv[1], vv[2], vv[3]);
+    };
+    float4* P = (float4*)(t.param + begin);
+    const float4* G = (const float4*)(t.grad + begin);
+    float4* M = (float4*)(t.exp_avg + begin);
+    float4* V = (float4*)(t.exp_avg_sq + begin);
+    int64_t q = threadIdx.x;
+    for (; q + kThreads < nv; q += 2 * kThreads) {
+      const int64_t q2 = q + kThreads;
+      float4 p0 = P[q], p1 = P[q2];
+      const float4 g0 = G[q], g1 = G[q2];
+      float4 m0 = M[q], m1 = M[q2], v0 = V[q], v1 = V[q2];
+      update(p0, g0, m0, v0);
+      update(p1, g1, m1, v1);
+      P[q] = p0, P[q2] = p1;
+      M[q] = m0, M[q2] = m1;
+      V[q] = v0, V[q2] = v1;
+    }
+    if (q < nv) {
+      float4 p0 = P[q], m0 = M[q], v0 = V[q];
+      const float4 g0 = G[q];
+      update(p0, g0, m0, v0);
+      P[q] = p0, M[q] = m0, V[q] = v0;
     }
     i = begin + nv * 4;
   }
@@ -139,12 +158,35 @@ __global__ void __launch_bounds__(kThreads) norm_partial(NormBatch b, int kind, 
   const int64_t begin = (chunk - b.chunk_start[k]) * kNormChunk;
   const int64_t end = min(b.numel[k], begin + kNormChunk);
   float acc = 0.f;
-  for (int64_t e = begin + threadIdx.x; e < end; e += kThreads) {
-    const float v = to_f32(x[e]);
+  auto take = [&](float v) {
     if (kind == 0) acc += v * v;
     else if (kind == 1) acc += fabsf(v);
     else acc = fmaxf(acc, fabsf(v));
+  };
+  int64_t e0 = begin;
+  if ((((uintptr_t)x) & 15) == 0) {
+    // 16-byte loads, two per thread per iteration (8 or 16 elements)
+    constexpr int V = 16 / sizeof(T);
+    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+    const int64_t nv = (end - begin) / V;
+    const u32x4* X = (const u32x4*)(x + begin);
+    int64_t q = threadIdx.x;
+    for (; q + kThreads < nv; q += 2 * kThreads) {
+      const u32x4 a = X[q], b2 = X[q + kThreads];
+      const T* ta = (const T*)&a;
+      const T* tb = (const T*)&b2;
+#pragma unroll
+      for (int j = 0; j < V; ++j) take(to_f32(ta[j])), take(to_f32(tb[j]));
+    }
+    if (q < nv) {
+      const u32x4 a = X[q];
+      const T* ta = (const T*)&a;
+#pragma unroll
+      for (int j = 0; j < V; ++j) take(to_f32(ta[j]));
+    }
+    e0 = begin + nv * V;
   }
+  for (int64_t e = e0 + threadIdx.x; e < end; e += kThreads) take(to_f32(x[e]));
   if (kind == 2) {
     acc = wave_max(acc);
     __syncthreads();
@@ -199,6 +241,20 @@ struct ApplyBatch {
   int has_scal;
 };
 
+__device__ __forceinline__ float apply_val(int op, float x, float y, float z, bool has_b, float s0, float sc,
+                                           bool has_ts, float tsv, bool has_scal) {
+  switch (op) {
+    case MI355X_OP_ADD: return x + s0 * (has_b ? y : 1.f);
+    case MI355X_OP_MUL: return x * (has_ts ? tsv : (has_scal ? sc : (has_b ? y : s0)));
+    case MI355X_OP_DIV: return x / (has_ts ? tsv : (has_scal ? sc : (has_b ? y : s0)));
+    case MI355X_OP_LERP: return (fabsf(s0) < 0.5f) ? x + s0 * (y - x) : y - (y - x) * (1.f - s0);
+    case MI355X_OP_ADDCMUL: return x + sc * y * z;
+    case MI355X_OP_ADDCDIV: return x + sc * (y / z);
+    case MI355X_OP_SQRT: return sqrtf(x);
+  }
+  return x;
+}
+
 template <typename T>
 __global__ void __launch_bounds__(kThreads) apply_kernel(ApplyBatch b, int op, float s0, const float* ts) {
   const int64_t chunk = blockIdx.x;
@@ -208,20 +264,31 @@ __global__ void __launch_bounds__(kThreads) apply_kernel(ApplyBatch b, int op, f
   const T* cc = (const T*)b.c[k];
   const float sc = b.has_scal ? (float)b.scal[k] : s0;
   const float tsv = ts ? *ts : 0.f;
+  const bool has_b = bb != nullptr, has_ts = ts != nullptr, has_scal = b.has_scal != 0;
   const int64_t begin = (chunk - b.chunk_start[k]) * kApplyChunk;
   const int64_t end = min(b.numel[k], begin + kApplyChunk);
-  for (int64_t e = begin + threadIdx.x; e < end; e += kThreads) {
-    float x = to_f32(a[e]);
-    switch (op) {
-      case MI355X_OP_ADD: x += s0 * (bb ? to_f32(bb[e]) : 1.f); break;
-      case MI355X_OP_MUL: x *= ts ? tsv : (b.has_scal ? sc : (bb ? to_f32(bb[e]) : s0)); break;
-      case MI355X_OP_DIV: x /= ts ? tsv : (b.has_scal ? sc : (bb ? to_f32(bb[e]) : s0)); break;
-      case MI355X_OP_LERP: { float y = to_f32(bb[e]); x = (fabsf(s0) < 0.5f) ? x + s0 * (y - x) : y - (y - x) * (1.f - s0); break; }
-      case MI355X_OP_ADDCMUL: x += sc * to_f32(bb[e]) * to_f32(cc[e]); break;
-      case MI355X_OP_ADDCDIV: x += sc * (to_f32(bb[e]) / to_f32(cc[e])); break;
-      case MI355X_OP_SQRT: x = sqrtf(x); break;
+  int64_t e0 = begin;
+  if constexpr (sizeof(T) == 4) {
+    if (((((uintptr_t)a) | ((uintptr_t)bb) | ((uintptr_t)cc)) & 15) == 0) {
+      const int64_t nv = (end - begin) / 4;
+      float4* A4 = (float4*)(a + begin);
+      const float4* B4 = (const float4*)(bb + begin);
+      const float4* C4 = (const float4*)(cc + begin);
+      for (int64_t q = threadIdx.x; q < nv; q += kThreads) {
+        const float4 x = A4[q];
+        const float4 y = bb ? B4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 z = cc ? C4[q] : make_float4(1.f, 1.f, 1.f, 1.f);
+        A4[q] = make_float4(apply_val(op, x.x, y.x, z.x, has_b, s0, sc, has_ts, tsv, has_scal),
+                            apply_val(op, x.y, y.y, z.y, has_b, s0, sc, has_ts, tsv, has_scal),
+                            apply_val(op, x.z, y.z, z.z, has_b, s0, sc, has_ts, tsv, has_scal),
+                            apply_val(op, x.w, y.w, z.w, has_b, s0, sc, has_ts, tsv, has_scal));
+      }
+      e0 = begin + nv * 4;
     }
-    a[e] = from_f32<T>(x);
+  }
+  for (int64_t e = e0 + threadIdx.x; e < end; e += kThreads) {
+    const float y = bb ? to_f32(bb[e]) : 0.f, z = cc ? to_f32(cc[e]) : 1.f;
+    a[e] = from_f32<T>(apply_val(op, to_f32(a[e]), y, z, has_b, s0, sc, has_ts, tsv, has_scal));
   }
 }
 
