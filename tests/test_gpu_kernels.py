@@ -294,7 +294,8 @@ def test_nll_fwd_bwd(kernels, reduction):
 
 
 @pytest.mark.parametrize("reduction", [0, 1, 2])
-@pytest.mark.parametrize("dtype,n,c", [(torch.bfloat16, 257, 50257), (torch.float32, 64, 1000)])
+@pytest.mark.parametrize("dtype,n,c", [(torch.bfloat16, 257, 50257), (torch.float32, 64, 1000),
+                                       (torch.float16, 33, 4001)])
 def test_fused_cross_entropy_matches_log_softmax_nll_chain(kernels, reduction, dtype, n, c):
     """The fused kernels against the oracle of the chain they replace:
     nll_loss(log_softmax(x)) forward, log_softmax_backward(nll_backward)
@@ -330,6 +331,33 @@ def test_fused_cross_entropy_matches_log_softmax_nll_chain(kernels, reduction, d
     tol = 1e-6 if dtype == torch.float32 else 2e-2
     tol_close(np64(dx)[:, :c], edx, atol=tol * 1e-2 + 1e-7, rtol=tol, what="ce dx")
     assert (host(dx)[:, c:] == 0).all()
+
+
+def test_fused_cross_entropy_nan_and_infinite_logits(kernels):
+    """A NaN logit makes its row's loss NaN and leaves the other rows alone;
+    -inf logits (masked classes) are legal and get zero gradient."""
+    n, c = 4, 3001
+    x = randn(n, c).bfloat16()
+    x[1, 17] = float("nan")
+    x[2, :1000] = float("-inf")
+    tgt = torch.tensor([5, 6, 2000, 7])
+    tx, tt = dev(x), dev(tgt)
+    out, lse, tw = torch.empty(n, device="cuda"), torch.empty(n, device="cuda"), torch.empty((), device="cuda")
+    ws_n = lib().mi355x_cross_entropy_workspace_bytes(n)
+    ws = workspace(ws_n)
+    call("mi355x_cross_entropy_fwd", p(out), p(tw), p(lse), p(tx), CODE[torch.bfloat16], c, p(tt), n, c,
+         0, -100, None, p(ws), ws_n, None)
+    got = host(out)
+    assert math.isnan(got[1].item())
+    exp = torch.nn.functional.cross_entropy(x.float(), tgt, reduction="none")
+    for i in (0, 2, 3):
+        assert abs(got[i].item() - exp[i].item()) < 1e-4
+    ld_dx = (c + 7) // 8 * 8
+    dx = torch.empty(n, ld_dx, dtype=torch.bfloat16, device="cuda")
+    call("mi355x_cross_entropy_bwd", p(dx), CODE[torch.bfloat16], ld_dx, p(tx), CODE[torch.bfloat16], c, p(lse),
+         p(tt), p(dev(torch.ones(n))), 0, None, n, c, -100, None)
+    d = host(dx).float()
+    assert (d[2, :1000] == 0).all() and torch.isfinite(d[2]).all() and torch.isfinite(d[0]).all()
 
 
 # ---------------------------------------------------------------------------

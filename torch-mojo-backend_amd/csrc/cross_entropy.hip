@@ -18,8 +18,10 @@
 // g_i = grad (per row for reduction none, else the scalar, / total_weight
 // for mean), zero for ignored rows and for the padding columns [c, ld_dx).
 // dx rows are 16-byte aligned (ld_dx a multiple of V), so each thread writes
-// whole 16-byte dx chunks; the V logits one needs come from two aligned
-// chunks shifted by the row's phase (v_alignbyte).
+// whole 16-byte dx chunks, two per iteration; the V logits one needs come
+// from two aligned chunks shifted by the row's phase (v_alignbyte).  Only
+// the first and last chunks of a row (and, backward, the target's chunk)
+// take the per-element masks; the rest go straight to exp2.
 // HBM traffic: forward reads the logits once; backward reads them once and
 // writes dx once.
 #include <math.h>
@@ -63,6 +65,10 @@ struct RowGeo {
   }
 };
 
+// exp2 on the hardware instruction: arguments here are <= 0 (or -inf), and
+// results below the f32 normal range only feed sums and bf16/f16 gradients.
+__device__ __forceinline__ float hw_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <typename T>
 __global__ void __launch_bounds__(kRowThreads)
     ce_fwd_rows(float* __restrict__ row_loss, float* __restrict__ row_valid, float* __restrict__ lse,
@@ -74,36 +80,42 @@ __global__ void __launch_bounds__(kRowThreads)
   const int64_t row = blockIdx.x;
   const T* r = x + row * ld;
   const RowGeo<T> geo(r, c);
+  const int nch = (int)geo.nch, ci = (int)c;
   float m = -INFINITY, sum = 0.f;  // max and sum of exp2((x - m) * log2e)
   bool nan = false;
-  for (int64_t j0 = threadIdx.x; j0 < geo.nch; j0 += (int64_t)kRowThreads * U) {
+  for (int j0 = threadIdx.x; j0 < nch; j0 += kRowThreads * U) {
     Chunk<T> ch[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = j0 + (int64_t)u * kRowThreads;
-      if (j < geo.nch) ch[u].w = geo.base[j];
+      const int j = j0 + u * kRowThreads;
+      if (j < nch) ch[u].w = geo.base[j];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t j = j0 + (int64_t)u * kRowThreads;
-      if (j >= geo.nch) break;
-      const int64_t k0 = j * V - geo.p;
+      const int j = j0 + u * kRowThreads;
+      if (j >= nch) break;
+      const int k0 = j * V - geo.p;
       float v[V];
-      float cm = -INFINITY;
+      if (k0 >= 0 && k0 + V <= ci) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[e] = ch[u].get(e);
+      } else {  // the row's first or last chunk
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[e] = (k0 + e >= 0 && k0 + e < ci) ? ch[u].get(e) : -INFINITY;
+      }
+      float cm = v[0];
 #pragma unroll
       for (int e = 0; e < V; ++e) {
-        const int64_t k = k0 + e;
-        v[e] = (k >= 0 && k < c) ? ch[u].get(e) : -INFINITY;
         nan |= v[e] != v[e];
         cm = fmaxf(cm, v[e]);
       }
       if (cm == -INFINITY) continue;
       if (cm > m) {
-        sum = (m == -INFINITY) ? 0.f : sum * exp2f((m - cm) * kLog2e);
+        sum = (m == -INFINITY) ? 0.f : sum * hw_exp2((m - cm) * kLog2e);
         m = cm;
       }
 #pragma unroll
-      for (int e = 0; e < V; ++e) sum += exp2f((v[e] - m) * kLog2e);
+      for (int e = 0; e < V; ++e) sum += hw_exp2((v[e] - m) * kLog2e);
     }
   }
   // wave then block merge of (m, sum)
@@ -195,7 +207,7 @@ __global__ void __launch_bounds__(kRowThreads)
                 const float* __restrict__ lse, const int64_t* __restrict__ target,
                 const float* __restrict__ grad, int grad_per_row, const float* __restrict__ total,
                 int64_t n, int64_t c, int64_t ignore_index) {
-  constexpr int V = Chunk<T>::V;
+  constexpr int V = Chunk<T>::V, U = 2;
   static_assert(sizeof(TD) == sizeof(T), "dx chunks follow the logits chunks");
   const int64_t row = blockIdx.x;
   const int64_t tg = target[row];
@@ -207,25 +219,43 @@ __global__ void __launch_bounds__(kRowThreads)
   const T* r = x + row * ld;
   const RowGeo<T> geo(r, c);
   const int bytes = geo.p * (int)sizeof(T);
+  const int nch = (int)geo.nch, ci = (int)c, tgi = valid ? (int)tg : -1;
   uint4* o = (uint4*)(dx + row * ld_dx);
-  const int64_t nout = ld_dx / V;
-  for (int64_t t = threadIdx.x; t < nout; t += kRowThreads) {
-    const int64_t k0 = t * V;
-    Chunk<T> ch;
-    if (k0 < c) {
-      const uint4 lo = geo.base[t];
-      const uint4 hi = (bytes && t + 1 < geo.nch) ? geo.base[t + 1] : make_uint4(0, 0, 0, 0);
-      ch.w = bytes ? shift_pair(lo, hi, bytes) : lo;
-    }
-    struct alignas(16) Out { TD v[V]; } out;
+  const int nout = (int)(ld_dx / V);
+  // U output chunks per thread per iteration, their loads issued first
+  for (int t0 = threadIdx.x; t0 < nout; t0 += kRowThreads * U) {
+    uint4 lo[U], hi[U];
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const int64_t k = k0 + e;
-      float d = 0.f;
-      if (k < c) d = g * (exp2f((ch.get(e) - l) * kLog2e) - (k == tg ? 1.f : 0.f));
-      out.v[e] = from_f32<TD>(d);
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u * kRowThreads;
+      lo[u] = hi[u] = make_uint4(0, 0, 0, 0);
+      if (t * V < ci) {
+        lo[u] = geo.base[t];
+        if (bytes && t + 1 < nch) hi[u] = geo.base[t + 1];
+      }
     }
-    o[t] = *(const uint4*)&out;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u * kRowThreads;
+      if (t >= nout) break;
+      const int k0 = t * V;
+      Chunk<T> ch;
+      ch.w = bytes ? shift_pair(lo[u], hi[u], bytes) : lo[u];
+      struct alignas(16) Out { TD v[V]; } out;
+      if (k0 + V <= ci && (tgi < k0 || tgi >= k0 + V)) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) out.v[e] = from_f32<TD>(g * hw_exp2((ch.get(e) - l) * kLog2e));
+      } else {  // the last chunk, padding past c, or the target's chunk
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const int k = k0 + e;
+          float d = 0.f;
+          if (k < ci) d = g * (hw_exp2((ch.get(e) - l) * kLog2e) - (k == tgi ? 1.f : 0.f));
+          out.v[e] = from_f32<TD>(d);
+        }
+      }
+      o[t] = *(const uint4*)&out;
+    }
   }
 }
 
@@ -242,6 +272,7 @@ extern "C" int mi355x_cross_entropy_fwd(void* out, float* total_weight, float* l
                                         int32_t* err_flag, void* workspace, int64_t ws_bytes,
                                         mi355x_stream_t stream) {
   MI_REQUIRE(n >= 0 && c > 0 && ld >= c, "mi355x_cross_entropy_fwd: bad shape");
+  MI_REQUIRE(c < (1ll << 30), "mi355x_cross_entropy_fwd: too many classes");
   MI_REQUIRE(reduction >= 0 && reduction <= 2, "mi355x_cross_entropy_fwd: bad reduction");
   MI_REQUIRE(dtype_size(dtype) == 0 || ((uintptr_t)logits % dtype_size(dtype)) == 0,
              "mi355x_cross_entropy_fwd: misaligned logits");
@@ -271,6 +302,7 @@ extern "C" int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx, c
                                         int reduction, const float* total_weight, int64_t n,
                                         int64_t c, int64_t ignore_index, mi355x_stream_t stream) {
   MI_REQUIRE(n >= 0 && c > 0 && ld >= c && ld_dx >= c, "mi355x_cross_entropy_bwd: bad shape");
+  MI_REQUIRE(c < (1ll << 30) && ld_dx < (1ll << 30), "mi355x_cross_entropy_bwd: too many classes");
   const int64_t v = 16 / (int64_t)dtype_size(dx_dtype);
   MI_REQUIRE(ld_dx % v == 0 && ((uintptr_t)dx % 16) == 0,
              "mi355x_cross_entropy_bwd: dx rows must be 16-byte aligned (ld_dx a multiple of %lld)", (long long)v);
