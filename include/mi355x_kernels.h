@@ -265,6 +265,16 @@ int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,
                           const void* gamma, const void* beta, int64_t rows,
                           int64_t cols, double eps, int dtype,
                           mi355x_stream_t stream);
+/* mi355x_layer_norm_fwd plus y_low: an optional second copy of y in a
+ * 16-bit type (low_dtype bf16/f16; f32 input only), written by the same
+ * kernel.  Under autocast the f32 layer_norm output is cast to the matmul
+ * dtype right away (fp32 policy for layer_norm, lower precision for linear:
+ * mojo_device_autocast.py:537-567); the copy saves that cast's read of y.
+ * No counterpart in the reference, whose cast is a separate _to_copy. */
+int mi355x_layer_norm_fwd_ex(void* y, void* y_low, int low_dtype, float* mean,
+                             float* rstd, const void* x, const void* gamma,
+                             const void* beta, int64_t rows, int64_t cols,
+                             double eps, int dtype, mi355x_stream_t stream);
 /* Any of dx/dgamma/dbeta may be NULL (output_mask, aten_fast.py:5475). */
 int64_t mi355x_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 int mi355x_layer_norm_bwd(void* dx, void* dgamma, void* dbeta,

@@ -240,6 +240,12 @@ class HostStandIn:
         return 0
 
     # ---- norms / activations ----
+    def mi355x_layer_norm_fwd_ex(self, y, y_low, low_dt, mean, rstd, x, g, b, rows, cols, eps, dt, stream):
+        self.mi355x_layer_norm_fwd(y, mean, rstd, x, g, b, rows, cols, eps, dt, stream)
+        if y_low:
+            dense(_val(y_low), DT[low_dt], (rows, cols)).copy_(dense(_val(y), DT[dt], (rows, cols)))
+        return 0
+
     def mi355x_layer_norm_fwd(self, y, mean, rstd, x, g, b, rows, cols, eps, dt, stream):
         X = dense(_val(x), DT[dt], (rows, cols)).float()
         mu = X.mean(1, keepdim=True)

@@ -204,6 +204,14 @@ def test_layer_norm_fwd_bwd(kernels, dtype, rows, cols):
     mean = torch.empty(rows, device="cuda")
     rstd = torch.empty(rows, device="cuda")
     call("mi355x_layer_norm_fwd", p(y), p(mean), p(rstd), p(tx), p(tg), p(tb), rows, cols, 1e-5, CODE[dtype], None)
+    if dtype == torch.float32:
+        # the autocast variant: the same y plus its bf16 rounding from the same kernel
+        y2 = torch.empty_like(y)
+        low = torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda")
+        call("mi355x_layer_norm_fwd_ex", p(y2), p(low), CODE[torch.bfloat16], None, None, p(tx), p(tg), p(tb),
+             rows, cols, 1e-5, CODE[dtype], None)
+        assert torch.equal(host(y2), host(y))
+        assert torch.equal(host(low), host(y).bfloat16())
     ey, em, er = O.layer_norm(xq.double().numpy(), gq.double().numpy(), bq.double().numpy())
     atol = 1e-4 if dtype == torch.float32 else 2e-2
     tol_close(np64(y), ey, atol=atol, rtol=atol, what="ln y")

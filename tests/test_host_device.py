@@ -218,6 +218,44 @@ def _counting_library():
     return inner, Counting(), calls
 
 
+def test_layer_norm_low_copy_feeds_autocast_linear(mojo):
+    """Under autocast the f32 layer norm also writes its output in bf16 and
+    the linear's cast takes that copy instead of a cast kernel; the copy is
+    used once and never after the output is modified."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(6, 16, generator=g)
+    w, b = torch.randn(8, 16, generator=g), torch.randn(8, generator=g)
+    lw, lb = torch.randn(16, generator=g), torch.randn(16, generator=g)
+    xm, wm, bm, lwm, lbm = (t.to("mojo") for t in (x, w, b, lw, lb))
+    inner, counting, calls = _counting_library()
+    ek.set_library_for_tests(counting)
+    try:
+        with torch.autocast("mojo", dtype=torch.bfloat16):
+            y = F.layer_norm(xm, (16,), lwm, lbm)
+            assert y.dtype == torch.float32
+            casts = calls["mi355x_copy"]
+            out = F.linear(y, wm, bm)
+            assert calls["mi355x_layer_norm_fwd_ex"] == 1
+            # only the weight and bias casts, not the activation's
+            assert calls["mi355x_copy"] - casts == 2
+            y2 = y.bfloat16()  # the copy went to the linear: this one is a fresh cast
+            assert calls["mi355x_copy"] - casts == 3
+            z = F.layer_norm(xm, (16,), lwm, lbm)
+            z.mul_(2.0)  # modified: its copy is stale
+            before = calls["mi355x_copy"]
+            z2 = z.bfloat16()
+            assert calls["mi355x_copy"] == before + 1
+    finally:
+        ek.set_library_for_tests(inner)
+    yr = F.layer_norm(x, (16,), lw, lb)
+    ref = yr.bfloat16().float() @ w.bfloat16().float().t() + b.bfloat16().float()
+    assert torch.allclose(out.float().cpu(), ref, atol=2e-2, rtol=2e-2)
+    assert torch.equal(y2.cpu(), yr.bfloat16()) or torch.allclose(y2.float().cpu(), yr, atol=1e-2)
+    assert torch.allclose(z2.float().cpu(), 2 * yr, atol=3e-2)
+
+
 def test_window_mask_tag_and_gqa_route(mojo):
     from torch_mojo_backend import eager_kernels as ek
     from torch_mojo_backend.masks import sliding_window_causal_mask, window_of

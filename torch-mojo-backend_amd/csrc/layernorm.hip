@@ -24,11 +24,13 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxBwdBlocks = 1024;
 
-template <typename T, int NV>
+// y_low (optional, element type TL): a second copy of y rounded to a 16-bit
+// type, the operand an autocast matmul consumes next.
+template <typename T, typename TL, int NV>
 __global__ void __launch_bounds__(kThreads)
-    ln_fwd_wave(T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
-                const T* __restrict__ x, const T* __restrict__ gamma, const T* __restrict__ beta,
-                int64_t rows, int cols, float eps) {
+    ln_fwd_wave(T* __restrict__ y, TL* __restrict__ y_low, float* __restrict__ mean_out,
+                float* __restrict__ rstd_out, const T* __restrict__ x, const T* __restrict__ gamma,
+                const T* __restrict__ beta, int64_t rows, int cols, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -73,6 +75,7 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - mu) * r * g[e] + b[e];
       Vec4<T>::store(yr + c, o);
+      if (y_low) Vec4<TL>::store(y_low + row * cols + c, o);
     }
   }
   if (lane == 0) {
@@ -82,11 +85,11 @@ __global__ void __launch_bounds__(kThreads)
 }
 
 // Any `cols`: one block per row, three passes over the row.
-template <typename T>
+template <typename T, typename TL>
 __global__ void __launch_bounds__(kThreads)
-    ln_fwd_block(T* __restrict__ y, float* __restrict__ mean_out, float* __restrict__ rstd_out,
-                 const T* __restrict__ x, const T* __restrict__ gamma, const T* __restrict__ beta,
-                 int64_t rows, int64_t cols, float eps) {
+    ln_fwd_block(T* __restrict__ y, TL* __restrict__ y_low, float* __restrict__ mean_out,
+                 float* __restrict__ rstd_out, const T* __restrict__ x, const T* __restrict__ gamma,
+                 const T* __restrict__ beta, int64_t rows, int64_t cols, float eps) {
   __shared__ float red[kWaves];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * cols;
@@ -106,6 +109,7 @@ __global__ void __launch_bounds__(kThreads)
     if (gamma) o *= to_f32(gamma[c]);
     if (beta) o += to_f32(beta[c]);
     yr[c] = from_f32<T>(o);
+    if (y_low) y_low[row * cols + c] = from_f32<TL>(o);
   }
   if (threadIdx.x == 0) {
     if (mean_out) mean_out[row] = mu;
@@ -414,19 +418,23 @@ int bwd_blocks(int64_t rows) {
   return rows > 0 ? (int)((rows + rpb - 1) / rpb) : 1;
 }
 
-template <typename T>
-int fwd_impl(T* y, float* mean, float* rstd, const T* x, const T* g, const T* b, int64_t rows,
+template <typename T, typename TL>
+int fwd_impl(T* y, TL* y_low, float* mean, float* rstd, const T* x, const T* g, const T* b, int64_t rows,
              int64_t cols, float eps, hipStream_t s) {
   const size_t al = 4 * sizeof(T);
-  const int nv = (aligned(x, al) && aligned(y, al) && aligned(g, al) && aligned(b, al)) ? wave_nv(cols) : 0;
+  const int nv = (aligned(x, al) && aligned(y, al) && aligned(g, al) && aligned(b, al) &&
+                  aligned(y_low, 4 * sizeof(TL))) ? wave_nv(cols) : 0;
   const unsigned grid = ceil_div(rows, kWaves);
   switch (nv) {
-    case 1: ln_fwd_wave<T, 1><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
-    case 2: ln_fwd_wave<T, 2><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
-    case 3: ln_fwd_wave<T, 3><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
-    case 4: ln_fwd_wave<T, 4><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
-    case 8: ln_fwd_wave<T, 8><<<grid, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, (int)cols, eps); break;
-    default: ln_fwd_block<T><<<(unsigned)rows, kThreads, 0, s>>>(y, mean, rstd, x, g, b, rows, cols, eps);
+#define LN_FWD_CASE(V) \
+    case V: ln_fwd_wave<T, TL, V><<<grid, kThreads, 0, s>>>(y, y_low, mean, rstd, x, g, b, rows, (int)cols, eps); break;
+    LN_FWD_CASE(1)
+    LN_FWD_CASE(2)
+    LN_FWD_CASE(3)
+    LN_FWD_CASE(4)
+    LN_FWD_CASE(8)
+#undef LN_FWD_CASE
+    default: ln_fwd_block<T, TL><<<(unsigned)rows, kThreads, 0, s>>>(y, y_low, mean, rstd, x, g, b, rows, cols, eps);
   }
   return check_launch("mi355x_layer_norm_fwd");
 }
@@ -504,26 +512,37 @@ int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* m
 
 using namespace mi;
 
-extern "C" int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,
-                                     const void* gamma, const void* beta, int64_t rows,
-                                     int64_t cols, double eps, int dtype, mi355x_stream_t stream) {
+extern "C" int mi355x_layer_norm_fwd_ex(void* y, void* y_low, int low_dtype, float* mean, float* rstd,
+                                        const void* x, const void* gamma, const void* beta, int64_t rows,
+                                        int64_t cols, double eps, int dtype, mi355x_stream_t stream) {
   MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_layer_norm_fwd: bad shape [%lld, %lld]",
              (long long)rows, (long long)cols);
   if (rows == 0) return MI355X_OK;
   MI_REQUIRE(y && x, "mi355x_layer_norm_fwd: null pointer");
+  MI_REQUIRE(!y_low || (dtype == MI355X_F32 && (low_dtype == MI355X_BF16 || low_dtype == MI355X_F16)),
+             "mi355x_layer_norm_fwd: the low-precision copy needs f32 input and a bf16/f16 copy");
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case MI355X_F32:
-      return fwd_impl<float>((float*)y, mean, rstd, (const float*)x, (const float*)gamma,
-                             (const float*)beta, rows, cols, (float)eps, s);
+      if (y_low && low_dtype == MI355X_F16)
+        return fwd_impl<float, f16>((float*)y, (f16*)y_low, mean, rstd, (const float*)x, (const float*)gamma,
+                                    (const float*)beta, rows, cols, (float)eps, s);
+      return fwd_impl<float, bf16>((float*)y, (bf16*)y_low, mean, rstd, (const float*)x, (const float*)gamma,
+                                   (const float*)beta, rows, cols, (float)eps, s);
     case MI355X_BF16:
-      return fwd_impl<bf16>((bf16*)y, mean, rstd, (const bf16*)x, (const bf16*)gamma,
-                            (const bf16*)beta, rows, cols, (float)eps, s);
+      return fwd_impl<bf16, bf16>((bf16*)y, nullptr, mean, rstd, (const bf16*)x, (const bf16*)gamma,
+                                  (const bf16*)beta, rows, cols, (float)eps, s);
     case MI355X_F16:
-      return fwd_impl<f16>((f16*)y, mean, rstd, (const f16*)x, (const f16*)gamma,
-                           (const f16*)beta, rows, cols, (float)eps, s);
+      return fwd_impl<f16, f16>((f16*)y, nullptr, mean, rstd, (const f16*)x, (const f16*)gamma,
+                                (const f16*)beta, rows, cols, (float)eps, s);
   }
   return fail(MI355X_EUNSUPPORTED, "mi355x_layer_norm_fwd: unsupported dtype %d", dtype);
+}
+
+extern "C" int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,
+                                     const void* gamma, const void* beta, int64_t rows,
+                                     int64_t cols, double eps, int dtype, mi355x_stream_t stream) {
+  return mi355x_layer_norm_fwd_ex(y, nullptr, 0, mean, rstd, x, gamma, beta, rows, cols, eps, dtype, stream);
 }
 
 extern "C" int64_t mi355x_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t cols) {

@@ -20,7 +20,7 @@ from pathlib import Path
 
 LIB_NAME = "libmi355x_kernels.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 c_int = ctypes.c_int
 c_i64 = ctypes.c_int64
@@ -84,6 +84,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mi355x_layer_norm_fwd": (
         c_int,
         [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],
+    ),
+    "mi355x_layer_norm_fwd_ex": (
+        c_int,
+        [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],
     ),
     "mi355x_layer_norm_bwd_workspace_bytes": (c_i64, [c_i64, c_i64]),
     "mi355x_layer_norm_bwd": (

@@ -262,6 +262,10 @@ def fast_aten__to_copy(
         if target.index != dev:
             host = t._to_cpu_tensor()
             return upload(host.to(dtype), target.index)
+    if dtype != t._dtype and memory_format in (None, torch.preserve_format, torch.contiguous_format):
+        low = _take_low_copy(t, dtype)
+        if low is not None:
+            return low
     if memory_format in (None, torch.preserve_format):
         out = _empty_like_layout(t, dtype)
     else:
@@ -1283,10 +1287,57 @@ def ws_ptr_or_none(p):
 # fused linear (the autocast linear path: casts, GEMMs and the bias
 # gradient as direct kernel calls, without per-view dispatches)
 # ---------------------------------------------------------------------------
+_LOW_ATTR = "_mojo_low_copy"
+
+
+def _take_low_copy(t: MT, dtype):
+    """The 16-bit copy of t that the kernel producing t wrote alongside it (a
+    layer norm under autocast, whose f32 output the next linear casts), if t
+    has not been modified since.  Each copy is handed out once, so the caller
+    owns it like a fresh cast."""
+    low = t.__dict__.pop(_LOW_ATTR, None) if hasattr(t, "__dict__") else None
+    if low is None:
+        return None
+    copy, version = low
+    if copy._dtype != dtype or t._version != version:
+        return None
+    return copy
+
+
+# The autocast lower-precision dtype while an f32-policy op (layer norm) runs
+# under autocast; set by the AutocastPrivateUse1 wrapper, since autocast
+# reads as off below the Python dispatch key.
+_autocast_low = None
+
+
+def autocast_low_scope(dtype):
+    """Context manager that marks an f32-policy op as running under autocast
+    with lower-precision dtype `dtype`."""
+    import contextlib
+
+    @contextlib.contextmanager
+    def scope():
+        global _autocast_low
+        prev, _autocast_low = _autocast_low, dtype
+        try:
+            yield
+        finally:
+            _autocast_low = prev
+
+    return scope()
+
+
+def _autocast_low_dtype():
+    return _autocast_low if _autocast_low in (torch.bfloat16, torch.float16) else None
+
+
 def cast_to(t: MT, dtype) -> MT:
     """t in `dtype` (t itself when it already is)."""
     if t._dtype == dtype:
         return t
+    low = _take_low_copy(t, dtype)
+    if low is not None:
+        return low
     out = _alloc(t._shape, dtype, t._device)
     return copy_into(out, t)
 
@@ -1427,14 +1478,21 @@ def fast_aten_native_layer_norm(input, normalized_shape, weight, bias, eps):
     stat_shape = tuple(a._shape[:-k]) + (1,) * k
     mean = _alloc(stat_shape, torch.float32, a._device)
     rstd = _alloc(stat_shape, torch.float32, a._device)
+    # Under autocast an f32 layer norm feeds a lower-precision matmul: the
+    # kernel also writes y in that dtype, which the cast then takes.
+    low_dt = _autocast_low_dtype() if a._dtype == torch.float32 else None
+    low = _alloc(a._shape, low_dt, a._device) if (low_dt is not None and rows and cols) else None
     if rows and cols:
         check(
-            "mi355x_layer_norm_fwd",
-            lib().mi355x_layer_norm_fwd(
-                out._ptr, mean._ptr, rstd._ptr, x._ptr, g._ptr if g is not None else None,
+            "mi355x_layer_norm_fwd_ex",
+            lib().mi355x_layer_norm_fwd_ex(
+                out._ptr, low._ptr if low is not None else None, _code(low_dt) if low is not None else 0,
+                mean._ptr, rstd._ptr, x._ptr, g._ptr if g is not None else None,
                 b._ptr if b is not None else None, rows, cols, float(eps), _code(a._dtype), _STREAM,
             ),
         )
+    if low is not None:
+        setattr(out, _LOW_ATTR, (low, out._version))
     if a._dtype != torch.float32:
         # ATen returns the statistics in the input dtype (aten_fast.py:5228-5245)
         mean = materialize_contiguous(mean, a._dtype)

@@ -41,12 +41,22 @@ def _cast_mojo_floating(value, dtype):
     return value
 
 
-def _policy_wrapper(op, dtype_getter):
+def _policy_wrapper(op, dtype_getter, mark_low=False):
+    """Run op with its floating mojo arguments cast to dtype_getter().  With
+    mark_low (the f32 layer norms) the op also learns the autocast dtype, so
+    its kernel can write the lower-precision copy of its output that the
+    next autocast matmul casts to."""
     @functools.wraps(op)
     def wrapper(*args, **kwargs):
         with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYSET):
             dtype = dtype_getter()
-            return op(*_cast_mojo_floating(args, dtype), **_cast_mojo_floating(kwargs, dtype))
+            cargs, ckwargs = _cast_mojo_floating(args, dtype), _cast_mojo_floating(kwargs, dtype)
+            if mark_low:
+                from ..eager_kernels import aten_fast
+
+                with aten_fast.autocast_low_scope(torch.get_autocast_dtype("mojo")):
+                    return op(*cargs, **ckwargs)
+            return op(*cargs, **ckwargs)
 
     return wrapper
 
@@ -77,7 +87,8 @@ def register_autocast_ops() -> None:
             op._schema.name, _policy_wrapper(op, lambda: torch.get_autocast_dtype("mojo"))
         )
     for op in fp32:
-        _aten_library.impl(op._schema.name, _policy_wrapper(op, lambda: torch.float32))
+        norm = "layer_norm" in op._schema.name
+        _aten_library.impl(op._schema.name, _policy_wrapper(op, lambda: torch.float32, mark_low=norm))
     _aten_library.impl("linear", _linear_autocast)
     _registered = True
 
