@@ -392,6 +392,18 @@ class HostStandIn:
         return 0
 
     # ---- optimizer ----
+    def mi355x_fused_adamw_ex(self, descs, lows, low_dt, n, lr, lr_ptr, b1, b2, wd, eps, flags, gs, fi, stream):
+        if fi and dense(_val(fi), torch.float32, ()).item() != 0:
+            return 0
+        self.mi355x_fused_adamw(descs, n, lr, lr_ptr, b1, b2, wd, eps, flags, gs, fi, stream)
+        if lows:
+            arr = ctypes.cast(lows, ctypes.POINTER(ctypes.c_void_p))
+            for i in range(n):
+                if arr[i]:
+                    m = descs[i].numel
+                    dense(arr[i], DT[low_dt], (m,)).copy_(dense(descs[i].param, torch.float32, (m,)))
+        return 0
+
     def mi355x_fused_adamw(self, descs, n, lr, lr_ptr, b1, b2, wd, eps, flags, gs, fi, stream):
         if fi and dense(_val(fi), torch.float32, ()).item() != 0:
             return 0

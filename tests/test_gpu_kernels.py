@@ -396,7 +396,19 @@ def test_fused_adamw_matches_oracle(kernels, amsgrad, maximize, wd):
     steps = [dev(torch.tensor(step)) for _ in sizes]
     d = _adam_descs(tp, tg, tm, tv, steps, tvm)
     flags = (1 if amsgrad else 0) | (2 if maximize else 0)
-    call("mi355x_fused_adamw", d, len(sizes), 6e-4, None, 0.9, 0.95, wd, 1e-8, flags, None, None, None)
+    if amsgrad:
+        call("mi355x_fused_adamw", d, len(sizes), 6e-4, None, 0.9, 0.95, wd, 1e-8, flags, None, None, None)
+        lows = None
+    else:
+        # the variant that also writes bf16 copies of the updated params (every other one here)
+        lows = [torch.empty(s_, dtype=torch.bfloat16, device="cuda") if i % 2 == 0 else None
+                for i, s_ in enumerate(sizes)]
+        lp = (ctypes.c_void_p * len(sizes))(*[p(x) if x is not None else None for x in lows])
+        call("mi355x_fused_adamw_ex", d, lp, CODE[torch.bfloat16], len(sizes), 6e-4, None, 0.9, 0.95, wd, 1e-8,
+             flags, None, None, None)
+        for i, x in enumerate(lows):
+            if x is not None:
+                assert torch.equal(host(x), host(tp[i]).bfloat16()), i
     for i in range(len(sizes)):
         exp = O.adamw_step(ps[i].numpy(), gs[i].numpy(), ms[i].numpy(), vs[i].numpy(), step, 6e-4, 0.9, 0.95,
                            wd, 1e-8, maximize, amsgrad, vm[i].numpy() if amsgrad else None)

@@ -256,6 +256,56 @@ def test_layer_norm_low_copy_feeds_autocast_linear(mojo):
     assert torch.allclose(z2.float().cpu(), 2 * yr, atol=3e-2)
 
 
+def test_adamw_parameter_copies_feed_next_autocast_forward(mojo):
+    """The fused AdamW step writes the bf16 copy of every parameter the
+    autocast forward casts; the next forward uses it with no cast kernel.  A
+    write into a parameter (in place, or through .data) drops its copy."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(16, 8).to("mojo")
+    opt = torch.optim.AdamW(lin.parameters(), lr=1e-2, fused=True)
+    x = torch.randn(4, 16).to("mojo")
+
+    def step():
+        with torch.autocast("mojo", dtype=torch.bfloat16):
+            out = lin(x)
+        out.float().sum().backward()
+        opt.step()
+        opt.zero_grad()
+
+    def forward_counting():
+        inner, counting, calls = _counting_library()
+        ek.set_library_for_tests(counting)
+        try:
+            with torch.autocast("mojo", dtype=torch.bfloat16):
+                out = lin(x)
+        finally:
+            ek.set_library_for_tests(inner)
+        return out, calls["mi355x_copy"]
+
+    def expected():
+        w, b = lin.weight.detach().cpu(), lin.bias.detach().cpu()
+        return x.cpu().bfloat16().float() @ w.bfloat16().float().t() + b.bfloat16().float()
+
+    step()  # the first forward casts; this step writes the copies
+    out, casts = forward_counting()
+    assert casts == 1  # only the f32 input x; weight and bias come from the optimizer
+    assert torch.allclose(out.float().cpu(), expected(), atol=2e-2, rtol=2e-2)
+    step()
+    with torch.no_grad():
+        lin.weight.data.mul_(2.0)  # a write the version counter does not see
+    out, casts = forward_counting()
+    assert casts == 2  # x and the weight again; the bias copy is still current
+    assert torch.allclose(out.float().cpu(), expected(), atol=2e-2, rtol=2e-2)
+    step()
+    with torch.no_grad():
+        lin.bias.copy_(torch.randn(8).to("mojo"))  # an in-place op on the parameter itself
+    out, casts = forward_counting()
+    assert casts == 2
+    assert torch.allclose(out.float().cpu(), expected(), atol=2e-2, rtol=2e-2)
+
+
 def test_window_mask_tag_and_gqa_route(mojo):
     from torch_mojo_backend import eager_kernels as ek
     from torch_mojo_backend.masks import sliding_window_causal_mask, window_of

@@ -15,7 +15,8 @@
 // with t read from the device step tensor (already incremented by the
 // caller's _foreach_add_), lr from a device scalar if given, and the whole
 // update skipped when *found_inf != 0.  HBM traffic per element: 16 B read
-// (p, g, m, v) + 12 B written (p, m, v) = 28 B.
+// (p, g, m, v) + 12 B written (p, m, v) = 28 B, + 2 B when the kernel also
+// writes the parameter's bf16/f16 copy for the next autocast forward.
 #include <math.h>
 
 #include "common.h"
@@ -29,6 +30,7 @@ constexpr int64_t kAdamChunk = 16384;
 
 struct AdamBatch {
   mi355x_adamw_tensor t[kAdamBatch];
+  void* low[kAdamBatch];  // optional 16-bit copy of each updated param (element type TL)
   int64_t chunk_start[kAdamBatch + 1];
   int n;
 };
@@ -47,6 +49,14 @@ struct AdamScalars {
   const float* found_inf;
 };
 
+template <typename TL>
+__device__ __forceinline__ void store_low4(TL* dst, const float4& p) {
+  typedef TL tl4 __attribute__((ext_vector_type(4)));
+  tl4 v;
+  v[0] = (TL)p.x, v[1] = (TL)p.y, v[2] = (TL)p.z, v[3] = (TL)p.w;
+  *(tl4*)dst = v;
+}
+
 __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v, float* vmax,
                                           float lr, float b1, float b2, float wd, float eps,
                                           float step_size, float bc2_sqrt, bool decay) {
@@ -62,11 +72,13 @@ __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
   p -= step_size * m / denom;
 }
 
+template <typename TL>
 __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalars s) {
   if (s.found_inf && *s.found_inf != 0.f) return;
   const int64_t chunk = blockIdx.x;
   const int k = find_tensor(b.chunk_start, b.n, chunk);
   const mi355x_adamw_tensor& t = b.t[k];
+  TL* const low = (TL*)b.low[k];
   const int64_t begin = (chunk - b.chunk_start[k]) * kAdamChunk;
   const int64_t end = min(t.numel, begin + kAdamChunk);
   const float lr = s.lr_ptr ? *s.lr_ptr : s.lr;
@@ -79,8 +91,8 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
   const bool maximize = s.flags & MI355X_ADAMW_MAXIMIZE;
   const float inv_scale = s.grad_scale ? 1.f / *s.grad_scale : 1.f;
   const bool vec = ((((uintptr_t)t.param | (uintptr_t)t.grad | (uintptr_t)t.exp_avg |
-                      (uintptr_t)t.exp_avg_sq) & 15) == 0) && t.max_exp_avg_sq == nullptr &&
-                   (begin % 4 == 0);
+                      (uintptr_t)t.exp_avg_sq) & 15) == 0) && (((uintptr_t)low & 7) == 0) &&
+                   t.max_exp_avg_sq == nullptr && (begin % 4 == 0);
   int64_t i = begin;
   if (vec) {
     const int64_t nv = (end - begin) / 4;
@@ -113,12 +125,17 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
       P[q] = p0, P[q2] = p1;
       M[q] = m0, M[q2] = m1;
       V[q] = v0, V[q2] = v1;
+      if (low) {
+        store_low4(low + begin + q * 4, p0);
+        store_low4(low + begin + q2 * 4, p1);
+      }
     }
     if (q < nv) {
       float4 p0 = P[q], m0 = M[q], v0 = V[q];
       const float4 g0 = G[q];
       update(p0, g0, m0, v0);
       P[q] = p0, M[q] = m0, V[q] = v0;
+      if (low) store_low4(low + begin + q * 4, p0);
     }
     i = begin + nv * 4;
   }
@@ -131,6 +148,7 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
     t.param[e] = p;
     t.exp_avg[e] = m;
     t.exp_avg_sq[e] = v;
+    if (low) low[e] = (TL)p;
   }
 }
 
@@ -299,12 +317,13 @@ int64_t chunks_of(int64_t numel, int64_t chunk) { return (numel + chunk - 1) / c
 
 using namespace mi;
 
-extern "C" int mi355x_fused_adamw(const mi355x_adamw_tensor* tensors, int n, double lr,
-                                  const float* lr_ptr, double beta1, double beta2,
-                                  double weight_decay, double eps, int flags,
-                                  const float* grad_scale, const float* found_inf,
-                                  mi355x_stream_t stream) {
+extern "C" int mi355x_fused_adamw_ex(const mi355x_adamw_tensor* tensors, void* const* param_low, int low_dtype,
+                                     int n, double lr, const float* lr_ptr, double beta1, double beta2,
+                                     double weight_decay, double eps, int flags, const float* grad_scale,
+                                     const float* found_inf, mi355x_stream_t stream) {
   MI_REQUIRE(n >= 0 && (n == 0 || tensors), "mi355x_fused_adamw: bad tensor list");
+  MI_REQUIRE(!param_low || low_dtype == MI355X_BF16 || low_dtype == MI355X_F16,
+             "mi355x_fused_adamw: the parameter copies must be bf16 or f16");
   hipStream_t s = (hipStream_t)stream;
   AdamScalars sc{(float)lr, (float)beta1, (float)beta2, (float)weight_decay, (float)eps, flags,
                  lr_ptr, grad_scale, found_inf};
@@ -320,6 +339,7 @@ extern "C" int mi355x_fused_adamw(const mi355x_adamw_tensor* tensors, int n, dou
       MI_REQUIRE(!(flags & MI355X_ADAMW_AMSGRAD) || t.numel == 0 || t.max_exp_avg_sq,
                  "mi355x_fused_adamw: amsgrad needs max_exp_avg_sq (tensor %d)", j);
       b.t[b.n] = t;
+      b.low[b.n] = param_low ? param_low[j] : nullptr;
       if (!(flags & MI355X_ADAMW_AMSGRAD)) b.t[b.n].max_exp_avg_sq = nullptr;
       b.chunk_start[b.n] = chunks;
       chunks += chunks_of(t.numel, kAdamChunk);
@@ -327,11 +347,21 @@ extern "C" int mi355x_fused_adamw(const mi355x_adamw_tensor* tensors, int n, dou
     }
     b.chunk_start[b.n] = chunks;
     if (chunks == 0) continue;
-    adamw_kernel<<<(unsigned)chunks, kThreads, 0, s>>>(b, sc);
+    if (low_dtype == MI355X_F16) adamw_kernel<f16><<<(unsigned)chunks, kThreads, 0, s>>>(b, sc);
+    else adamw_kernel<bf16><<<(unsigned)chunks, kThreads, 0, s>>>(b, sc);
     int rc = check_launch("mi355x_fused_adamw");
     if (rc) return rc;
   }
   return MI355X_OK;
+}
+
+extern "C" int mi355x_fused_adamw(const mi355x_adamw_tensor* tensors, int n, double lr,
+                                  const float* lr_ptr, double beta1, double beta2,
+                                  double weight_decay, double eps, int flags,
+                                  const float* grad_scale, const float* found_inf,
+                                  mi355x_stream_t stream) {
+  return mi355x_fused_adamw_ex(tensors, nullptr, 0, n, lr, lr_ptr, beta1, beta2, weight_decay, eps, flags,
+                               grad_scale, found_inf, stream);
 }
 
 extern "C" int64_t mi355x_foreach_norm_workspace_bytes(const int64_t* numels, int n) {

@@ -126,6 +126,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_double, c_double, c_int, c_vp, c_vp, c_vp,
         ],
     ),
+    "mi355x_fused_adamw_ex": (
+        c_int,
+        [
+            ctypes.POINTER(AdamWTensor), c_vp, c_int, c_int, c_double, c_vp, c_double, c_double,
+            c_double, c_double, c_int, c_vp, c_vp, c_vp,
+        ],
+    ),
     "mi355x_foreach_norm_workspace_bytes": (c_i64, [P_i64, c_int]),
     "mi355x_foreach_norm": (
         c_int,

@@ -1331,6 +1331,71 @@ def _autocast_low_dtype():
     return _autocast_low if _autocast_low in (torch.bfloat16, torch.float16) else None
 
 
+# Parameters the autocast forward casts (leaves that require grad): the
+# fused AdamW step also writes each one's 16-bit copy, and the next forward's
+# cast returns that copy.  A copy is dropped by any op that writes into the
+# parameter's storage (see drop_param_copies_written_by) and is checked
+# against the parameter's storage, address and version before each use.
+_CAST_DTYPE_ATTR = "_mojo_autocast_dtype"
+_PARAM_LOW_ATTR = "_mojo_param_low"
+_param_low_by_holder: dict = {}  # id(storage holder) -> weakref to the parameter
+
+
+def _param_low_copy(t: MT, dtype):
+    rec = t.__dict__.get(_PARAM_LOW_ATTR) if hasattr(t, "__dict__") else None
+    if rec is None:
+        return None
+    copy, holder, ptr, version = rec
+    if copy._dtype != dtype or t._holder is not holder or t._ptr != ptr or t._version != version:
+        drop_param_copy(t)
+        return None
+    return copy
+
+
+def drop_param_copy(t) -> None:
+    rec = t.__dict__.pop(_PARAM_LOW_ATTR, None)
+    if rec is not None:
+        _param_low_by_holder.pop(id(rec[1]), None)
+
+
+def _set_param_copy(p: MT, copy: MT) -> None:
+    import weakref
+
+    drop_param_copy(p)
+    p.__dict__[_PARAM_LOW_ATTR] = (copy, p._holder, p._ptr, p._version)
+    _param_low_by_holder[id(p._holder)] = weakref.ref(p)
+
+
+_written_args: dict = {}  # OpOverload -> tuple of (position, name) of written arguments
+
+
+def drop_param_copies_written_by(func, args, kwargs) -> None:
+    """Drop the parameter copies whose storage the op `func` writes."""
+    spec = _written_args.get(func)
+    if spec is None:
+        spec = tuple(
+            (i, a.name) for i, a in enumerate(func._schema.arguments)
+            if a.alias_info is not None and a.alias_info.is_write
+        )
+        _written_args[func] = spec
+    for i, name in spec:
+        v = args[i] if i < len(args) else kwargs.get(name)
+        for t in (v if isinstance(v, (list, tuple)) else (v,)):
+            holder = getattr(t, "_holder", None)
+            if holder is not None:
+                ref = _param_low_by_holder.get(id(holder))
+                if ref is not None:
+                    prm = ref()
+                    if prm is None:
+                        _param_low_by_holder.pop(id(holder), None)
+                    else:
+                        drop_param_copy(prm)
+
+
+def param_copies_active() -> bool:
+    return bool(_param_low_by_holder)
+
+
 def cast_to(t: MT, dtype) -> MT:
     """t in `dtype` (t itself when it already is)."""
     if t._dtype == dtype:
@@ -1338,6 +1403,11 @@ def cast_to(t: MT, dtype) -> MT:
     low = _take_low_copy(t, dtype)
     if low is not None:
         return low
+    if dtype in (torch.bfloat16, torch.float16) and t.requires_grad and t.is_leaf:
+        low = _param_low_copy(t, dtype)
+        if low is not None:
+            return low
+        t.__dict__[_CAST_DTYPE_ATTR] = dtype
     out = _alloc(t._shape, dtype, t._device)
     return copy_into(out, t)
 
@@ -2115,14 +2185,29 @@ def fast_aten__fused_adamw_(
         gs = materialize_contiguous(gs, torch.float32)
     if fi is not None and fi._dtype != torch.float32:
         fi = materialize_contiguous(fi, torch.float32)
+    # parameters the autocast forward casts get their 16-bit copy from this step
+    low_dt = None
+    lows = [None] * n
+    for i, prm in enumerate(params):
+        dt = prm.__dict__.get(_CAST_DTYPE_ATTR) if hasattr(prm, "__dict__") else None
+        if dt is not None and (low_dt is None or dt == low_dt):
+            low_dt = dt
+            lows[i] = _alloc(prm._shape, dt, prm._device)
+    low_ptrs = (ctypes.c_void_p * n)(*[x._ptr if x is not None else None for x in lows]) if low_dt else None
     check(
-        "mi355x_fused_adamw",
-        lib().mi355x_fused_adamw(
-            descs, n, lr_value, lr_t._ptr if lr_t is not None else None, float(beta1), float(beta2),
-            float(weight_decay), float(eps), flags, gs._ptr if gs is not None else None,
-            fi._ptr if fi is not None else None, _STREAM,
+        "mi355x_fused_adamw_ex",
+        lib().mi355x_fused_adamw_ex(
+            descs, low_ptrs, _code(low_dt) if low_dt else 0, n, lr_value, lr_t._ptr if lr_t is not None else None,
+            float(beta1), float(beta2), float(weight_decay), float(eps), flags,
+            gs._ptr if gs is not None else None, fi._ptr if fi is not None else None, _STREAM,
         ),
     )
+    if fi is not None:
+        # a skipped step (found_inf) leaves the copies unwritten: do not publish them
+        lows = [None] * n
+    for prm, low in zip(params, lows):
+        if low is not None:
+            _set_param_copy(prm, low)
     return None
 
 

@@ -12,6 +12,8 @@ from __future__ import annotations
 
 import torch
 
+from ..eager_kernels import aten_fast as _aten_fast
+
 # OpOverload -> python implementation (filled by register_mojo_devices)
 DIRECT: dict = {}
 
@@ -19,6 +21,8 @@ _DISABLE = torch._C._DisableTorchDispatch
 
 
 def dispatch(func, args, kwargs):
+    if _aten_fast.param_copies_active() and func._schema.is_mutable:
+        _aten_fast.drop_param_copies_written_by(func, args, kwargs)
     impl = DIRECT.get(func)
     if impl is not None:
         return impl(*args, **kwargs)
