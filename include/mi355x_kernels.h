@@ -476,8 +476,8 @@ int mi355x_attn_fwd_ex(void* o, const int64_t* o_bhs, float* lse, const void* q,
                        const void* v, const int64_t* v_bhs, int64_t batch, int64_t heads,
                        int64_t kv_heads, int64_t sq, int64_t skv, int64_t d, double scale,
                        int causal, int64_t window, int dtype, mi355x_stream_t stream);
-/* dQ, dK, dV (written, never accumulated).  workspace holds the f32 row
- * terms D_i = sum(dO*O) and f32 dQ partials. */
+/* dQ, dK, dV (written, never accumulated).  workspace holds two f32 row
+ * terms per query: D_i = sum(dO*O) and LSE_i * log2(e). */
 int64_t mi355x_attn_bwd_workspace_bytes(int64_t batch, int64_t heads,
                                         int64_t sq, int64_t skv, int64_t d);
 int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk,

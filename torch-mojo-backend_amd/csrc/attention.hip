@@ -40,6 +40,10 @@
 #ifndef ATTN_FWD_BLOCKS
 #define ATTN_FWD_BLOCKS 2
 #endif
+// Backward (D = 64): waves per SIMD the dK/dV and dQ kernels are compiled for.
+#ifndef ATTN_BWD_WAVES
+#define ATTN_BWD_WAVES 2
+#endif
 #ifndef ATTN_ASM_DMA
 #define ATTN_ASM_DMA 1
 #endif
@@ -130,9 +134,17 @@ __device__ __forceinline__ typename Mfma<T>::frag perm_frag(const T* tr, int row
 struct BlockCoord {
   int64_t x, h, b;
 };
-__device__ __forceinline__ BlockCoord block_coord() {
-  const uint32_t nx = gridDim.x, ny = gridDim.y, n = nx * ny * gridDim.z;
-  const uint32_t l = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+// A block's linear id and the (x, y, z) grid it is placed in.  Kernels that
+// serve two grids from one launch pass a virtual id here.
+struct GridPos {
+  uint32_t nx, ny, nz, l;
+};
+__device__ __forceinline__ GridPos hw_grid() {
+  return GridPos{gridDim.x, gridDim.y, gridDim.z, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)};
+}
+__device__ __forceinline__ BlockCoord block_coord(GridPos g) {
+  const uint32_t nx = g.nx, ny = g.ny, n = nx * ny * g.nz;
+  const uint32_t l = g.l;
   BlockCoord c;
   if ((n & 7) == 0 && ((n >> 3) % nx) == 0) {
     const uint32_t pairs = (n >> 3) / nx;  // (b, h) pairs per XCD
@@ -149,6 +161,7 @@ __device__ __forceinline__ BlockCoord block_coord() {
   }
   return c;
 }
+__device__ __forceinline__ BlockCoord block_coord() { return block_coord(hw_grid()); }
 
 // Reductions over the four 16-lane groups of a wave (the key rows of an
 // S^T tile): v_permlane16_swap / v_permlane32_swap with both operands = x
@@ -646,6 +659,7 @@ struct AttnBwdArgs {
   void* dk; int64_t dk_b, dk_h, dk_s;
   void* dv; int64_t dv_b, dv_h, dv_s;
   float* delta;  // [B, H, Sq]
+  float* lse2;   // [B, H, Sq]: LSE * log2(e), written by attn_bwd_delta
 };
 
 // D_i = sum_d dO[i, d] * O[i, d]: D/8 lanes per row, one 16-byte load of
@@ -668,7 +682,10 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_delta(AttnBwdArgs p) {
   }
 #pragma unroll
   for (int off = CPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (row < total && ch == 0) p.delta[row] = acc;
+  if (row < total && ch == 0) {
+    p.delta[row] = acc;
+    p.lse2[row] = p.f.lse[row] * kLog2e;
+  }
 }
 
 
@@ -875,25 +892,29 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dq(AttnBwdArgs p) {
 // and V, computes S^T and dP^T (key tile = MFMA rows, queries = columns) and
 // accumulates dQ^T += K^T dS^T with K^T read transposed.
 // ---------------------------------------------------------------------------
+template <int D>
+constexpr int kDkvLds = 2 * (2 * KvLayout<D>::TILE + 512);  // 2 stages of Q, dO, LSE[64], D[64]
+template <int D>
+constexpr int kDqLds = 2 * (2 * KvLayout<D>::TILE);  // 2 stages of K, V
+
 template <typename T, int D>
-__global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(AttnBwdArgs p) {
+__device__ __forceinline__ void dkv_body(const AttnBwdArgs& p, GridPos gp, char* lds) {
   typedef typename Mfma<T>::frag frag;
   typedef KvLayout<D> L;
   constexpr int KS = D / 32, DT = D / 16;
   constexpr int STAGE = 2 * L::TILE + 512;  // Q tile, dO tile, LSE[64], D[64]
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
   const AttnArgs& f = p.f;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
-  const BlockCoord bc = block_coord();
+  const BlockCoord bc = block_coord(gp);
   const int64_t k0 = bc.x * 128;
   const int64_t b = bc.b, h = bc.h;
   const char* Q = (const char*)((const T*)f.q + b * f.q_b + h * f.q_h);
   const T* K = (const T*)f.k + b * f.k_b + h * f.k_h;
   const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
   const char* dO = (const char*)((const T*)p.dout + b * p.do_b + h * p.do_h);
-  const float* LSE = f.lse + (b * f.H + h) * f.Sq;
+  const float* LSE = p.lse2 + (b * f.H + h) * f.Sq;
   const float* DEL = p.delta + (b * f.H + h) * f.Sq;
   const int64_t qs_b = f.q_s * (int64_t)sizeof(T), dos_b = p.do_s * (int64_t)sizeof(T);
 
@@ -964,11 +985,11 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
           }
           const float4 l4 = *(const float4*)(lse_s + qt * 16 + 4 * lg);
           const float4 d4 = *(const float4*)(del_s + qt * 16 + 4 * lg);
-          const float lv[4] = {l4.x * kLog2e, l4.y * kLog2e, l4.z * kLog2e, l4.w * kLog2e};
-          const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+            // dP - D: the accumulator of dO V^T starts at -D
+            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {-d4.x, -d4.y, -d4.z, -d4.w};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               sa = Mfma<T>::mma(qa[ks], kf[t][ks], sa);
@@ -983,7 +1004,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
                 if (qr >= q_lim || kr >= k_lim || (f.causal && kq + kr > qr)) pv = 0.f;
               }
               pt[u][t][e] = pv;
-              ds[u][t][e] = pv * (pa[e] - dv[e]);
+              ds[u][t][e] = pv * pa[e];
             }
           }
         }
@@ -1042,18 +1063,17 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dkv_v2(Att
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(AttnBwdArgs p) {
+__device__ __forceinline__ void dq_body(const AttnBwdArgs& p, GridPos gp, char* lds) {
   typedef typename Mfma<T>::frag frag;
   typedef KvLayout<D> L;
   constexpr int KS = D / 32, DT = D / 16;
   constexpr int STAGE = 2 * L::TILE;  // K tile, V tile
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
   const AttnArgs& f = p.f;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
-  const BlockCoord bc = block_coord();
-  const int64_t qblock = f.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
+  const BlockCoord bc = block_coord(gp);
+  const int64_t qblock = f.causal ? (int64_t)gp.nx - 1 - bc.x : bc.x;
   const int64_t q0 = qblock * 128;
   const int64_t b = bc.b, h = bc.h;
   const T* Q = (const T*)f.q + b * f.q_b + h * f.q_h;
@@ -1074,8 +1094,8 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
       qf[u][ks] = ok ? *(const frag*)(Q + qi * f.q_s + ks * 32 + lg * 8) : zero_frag<T>();
       df[u][ks] = ok ? *(const frag*)(dO + qi * p.do_s + ks * 32 + lg * 8) : zero_frag<T>();
     }
-    lse2[u] = ok ? f.lse[(b * f.H + h) * f.Sq + qi] * kLog2e : 0.f;
-    dlt[u] = ok ? p.delta[(b * f.H + h) * f.Sq + qi] : 0.f;
+    lse2[u] = ok ? p.lse2[(b * f.H + h) * f.Sq + qi] : 0.f;
+    dlt[u] = ok ? -p.delta[(b * f.H + h) * f.Sq + qi] : 0.f;  // -D, the start of dP - D
   }
   f32x4 dqa[DT][2];
 #pragma unroll
@@ -1123,7 +1143,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
           }
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {0.f, 0.f, 0.f, 0.f};
+            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {dlt[u], dlt[u], dlt[u], dlt[u]};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               sa = Mfma<T>::mma(ka[ks], qf[u][ks], sa);
@@ -1137,7 +1157,7 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
                 const int kr = kt * 16 + 4 * lg + e;
                 if (qr >= q_lim || kr >= k_lim || (f.causal && kr > qk + qr)) pv = 0.f;
               }
-              ds[v2][u][e] = pv * (pa[e] - dlt[u]);
+              ds[v2][u][e] = pv * pa[e];
             }
           }
         }
@@ -1179,6 +1199,32 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? 2 : 1) attn_bwd_dq_v2(Attn
       *(V4<T>*)(dQ + dt * 16 + lg * 4) = q4;
     }
   }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, D == 64 ? ATTN_BWD_WAVES : 1) attn_bwd_dkv_v2(AttnBwdArgs p) {
+  __shared__ __attribute__((aligned(1024))) char lds[kDkvLds<D>];
+  dkv_body<T, D>(p, hw_grid(), lds);
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, D == 64 ? ATTN_BWD_WAVES : 1) attn_bwd_dq_v2(AttnBwdArgs p) {
+  __shared__ __attribute__((aligned(1024))) char lds[kDqLds<D>];
+  dq_body<T, D>(p, hw_grid(), lds);
+}
+
+// dK/dV and dQ blocks from one launch over a 1-D grid of 2 x (tiles x H x B)
+// blocks.  The two kinds alternate inside each XCD's share of the grid, so
+// both keep their XCD-aware, heaviest-first order and the light blocks of
+// one kind fill the causal tail left by the heavy blocks of the other.
+// Block l runs on XCD l % 8; its slot i = l / 8 within that XCD carries the
+// kind in bit 0, and virtual id (i / 2) * 8 + l % 8 keeps the XCD.
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, D == 64 ? ATTN_BWD_WAVES : 1) attn_bwd_dkv_dq(AttnBwdArgs p, uint32_t nkx, uint32_t nqx) {
+  __shared__ __attribute__((aligned(1024))) char lds[kDkvLds<D> > kDqLds<D> ? kDkvLds<D> : kDqLds<D>];
+  const uint32_t l = blockIdx.x, i = l >> 3, v = (i >> 1) * 8 + (l & 7);
+  if (i & 1) dq_body<T, D>(p, GridPos{nqx, (uint32_t)p.f.H, (uint32_t)p.f.B, v}, lds);
+  else dkv_body<T, D>(p, GridPos{nkx, (uint32_t)p.f.H, (uint32_t)p.f.B, v}, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -1236,10 +1282,14 @@ int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
   const int64_t rows = a.f.B * a.f.H * a.f.Sq;
   attn_bwd_delta<T, D><<<ceil_div(rows, kThreads / (D / 8)), kThreads, 0, s>>>(a);
   if constexpr (D == 64 || D == 128) {
-    dim3 gk(ceil_div(a.f.Skv, 128), (unsigned)a.f.H, (unsigned)a.f.B);
-    attn_bwd_dkv_v2<T, D><<<gk, kThreads, 0, s>>>(a);
-    dim3 gq(ceil_div(a.f.Sq, 128), (unsigned)a.f.H, (unsigned)a.f.B);
-    attn_bwd_dq_v2<T, D><<<gq, kThreads, 0, s>>>(a);
+    const uint32_t nkx = (uint32_t)ceil_div(a.f.Skv, 128), nqx = (uint32_t)ceil_div(a.f.Sq, 128);
+    const int64_t hb = a.f.H * a.f.B;
+    if (nkx == nqx && (hb * nkx) % 8 == 0) {
+      attn_bwd_dkv_dq<T, D><<<(unsigned)(2 * hb * nkx), kThreads, 0, s>>>(a, nkx, nqx);
+    } else {
+      attn_bwd_dkv_v2<T, D><<<dim3(nkx, (unsigned)a.f.H, (unsigned)a.f.B), kThreads, 0, s>>>(a);
+      attn_bwd_dq_v2<T, D><<<dim3(nqx, (unsigned)a.f.H, (unsigned)a.f.B), kThreads, 0, s>>>(a);
+    }
   } else {
     dim3 gk(ceil_div(a.f.Skv, 64), (unsigned)a.f.H, (unsigned)a.f.B);
     attn_bwd_dkv<T, D><<<gk, kThreads, 0, s>>>(a);
@@ -1312,7 +1362,7 @@ extern "C" int mi355x_attn_fwd(void* o, const int64_t* o_bhs, float* lse, const 
 extern "C" int64_t mi355x_attn_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t sq,
                                                    int64_t skv, int64_t d) {
   (void)skv; (void)d;
-  return batch * heads * sq * (int64_t)sizeof(float) + 256;
+  return 2 * batch * heads * sq * (int64_t)sizeof(float) + 256;
 }
 
 extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs,
@@ -1342,5 +1392,6 @@ extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const 
   a.dk = dk; a.dk_b = dk_bhs[0]; a.dk_h = dk_bhs[1]; a.dk_s = dk_bhs[2];
   a.dv = dv; a.dv_b = dv_bhs[0]; a.dv_h = dv_bhs[1]; a.dv_s = dv_bhs[2];
   a.delta = (float*)workspace;
+  a.lse2 = a.delta + batch * heads * sq;
   MI_ATTN_DISPATCH(dtype, d, bwd_launch, a, (hipStream_t)stream);
 }
