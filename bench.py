@@ -49,11 +49,24 @@ def _events():
 
 def time_gpu(fn, iters, warmup=2):
     """Average milliseconds per call of fn() with HIP events on the default
-    stream (the stream every mojo kernel is launched on)."""
+    stream (the stream every mojo kernel is launched on).
+
+    A spin kernel (about 2 ms) is queued before the start event, so the host
+    has enqueued the timed calls before the GPU reaches them: launches of
+    20-80 us kernels are then timed back to back, not at the pace of the
+    Python code that issues them.  (A longer spin lets the clocks drop
+    before the timed launches.)"""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    # keep the GPU busy for about 0.3 s first: its clocks ramp up under load
+    t_end = time.perf_counter() + 0.3
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
     a, b = _events()
+    torch.cuda._sleep(5_000_000)
     a.record()
     for _ in range(iters):
         fn()
@@ -96,15 +109,50 @@ def bench_model(args):
 
 
 def bench_sdpa(iters):
-    """Config 1: causal SDPA fwd+bwd [8,12,1024,64] bf16 through the product path."""
+    """Config 1: causal SDPA fwd+bwd [8,12,1024,64] bf16.
+
+    The roofline figure times the kernels through the C ABI on preallocated
+    [B,S,H,D]-strided outputs (the layout the model hands over) and one
+    workspace, back to back on the null stream.  `*_op_ms` times the same
+    work through the aten-level functions, which allocate fresh outputs per
+    call."""
     from torch_mojo_backend.eager_kernels import aten_fast as F
+    from torch_mojo_backend.eager_kernels import lib
 
     B, H, S, D = 8, 12, 1024, 64
     g = torch.Generator().manual_seed(0)
-    q, k, v, do = (torch.randn(B, H, S, D, generator=g).bfloat16().to("mojo") for _ in range(4))
-    out, lse = F.fused_flash_attention_forward(q, k, v, True, None)
-    fwd_ms = time_gpu(lambda: F.fused_flash_attention_forward(q, k, v, True, None), iters)
-    bwd_ms = time_gpu(lambda: F.fused_flash_attention_backward(do, q, k, v, out, lse, True, None), iters)
+    q, k, v, do = (F.alloc_bthd(B, H, S, D, torch.bfloat16, 0) for _ in range(4))
+    for t in (q, k, v, do):
+        t._holder.view(torch.bfloat16).copy_(torch.randn(B * S * H * D, generator=g).bfloat16())
+    o = F.alloc_bthd(B, H, S, D, torch.bfloat16, 0)
+    dq, dk, dv = (F.alloc_bthd(B, H, S, D, torch.bfloat16, 0) for _ in range(3))
+    lse = torch.empty(B, H, S, dtype=torch.float32, device="cuda")
+    ws_n = lib().mi355x_attn_bwd_workspace_bytes(B, H, S, S, D)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    scale, bf = 1.0 / math.sqrt(D), F._code(torch.bfloat16)
+    bhs = F._bhs
+
+    def fwd():
+        F.check("mi355x_attn_fwd", lib().mi355x_attn_fwd(
+            o._ptr, bhs(o), lse.data_ptr(), q._ptr, bhs(q), k._ptr, bhs(k), v._ptr, bhs(v),
+            B, H, S, S, D, scale, 1, bf, None))
+
+    def bwd():
+        F.check("mi355x_attn_bwd", lib().mi355x_attn_bwd(
+            dq._ptr, bhs(dq), dk._ptr, bhs(dk), dv._ptr, bhs(dv), do._ptr, bhs(do), q._ptr, bhs(q),
+            k._ptr, bhs(k), v._ptr, bhs(v), o._ptr, bhs(o), lse.data_ptr(), B, H, S, S, D, scale, 1, bf,
+            ws.data_ptr(), ws_n, None))
+
+    fwd()
+    # at least 50 timed launches after 10 untimed ones
+    n = max(iters, 50)
+    fwd_ms = time_gpu(fwd, n, warmup=10)
+    bwd_ms = time_gpu(bwd, n, warmup=10)
+    qm, km, vm, dom = (F._fa_head_contig(t) for t in (q, k, v, do))
+    out, lse2 = F.fused_flash_attention_forward(qm, km, vm, True, None)
+    fwd_op_ms = time_gpu(lambda: F.fused_flash_attention_forward(qm, km, vm, True, None), n, warmup=10)
+    bwd_op_ms = time_gpu(lambda: F.fused_flash_attention_backward(dom, qm, km, vm, out, lse2, True, None), n,
+                         warmup=10)
     fwd_flop = 4.0 * B * H * S * S * D / 2
     bwd_flop = 2.5 * fwd_flop
     tot_ms = fwd_ms + bwd_ms
@@ -118,6 +166,8 @@ def bench_sdpa(iters):
         "fwd_bwd_tflops": achieved,
         "frac_of_peak": achieved / PEAK_BF16_TFLOPS,
         "gflop_per_fwd_bwd": (fwd_flop + bwd_flop) / 1e9,
+        "fwd_op_ms": fwd_op_ms,
+        "bwd_op_ms": bwd_op_ms,
     }
 
 

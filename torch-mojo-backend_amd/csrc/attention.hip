@@ -142,13 +142,21 @@ struct GridPos {
 __device__ __forceinline__ GridPos hw_grid() {
   return GridPos{gridDim.x, gridDim.y, gridDim.z, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)};
 }
-__device__ __forceinline__ BlockCoord block_coord(GridPos g) {
+constexpr uint32_t kCUsPerXCD = 32;
+__device__ __forceinline__ BlockCoord block_coord(GridPos g, bool zigzag = false) {
   const uint32_t nx = g.nx, ny = g.ny, n = nx * ny * g.nz;
   const uint32_t l = g.l;
   BlockCoord c;
   if ((n & 7) == 0 && ((n >> 3) % nx) == 0) {
     const uint32_t pairs = (n >> 3) / nx;  // (b, h) pairs per XCD
-    const uint32_t i = l >> 3;
+    uint32_t i = l >> 3;
+    // zigzag: every other round of kCUsPerXCD slots takes its tiles in
+    // reverse (light to heavy), so a CU that got a heavy tile in one round
+    // gets a light one in the next and the per-CU sums even out.
+    if (zigzag) {
+      const uint32_t r = i / kCUsPerXCD, j = r * kCUsPerXCD + (kCUsPerXCD - 1 - i % kCUsPerXCD);
+      if ((r & 1) && j < (n >> 3)) i = j;
+    }
     c.x = i / pairs;
     const uint32_t pair = (l & 7) * pairs + (i - (uint32_t)c.x * pairs);
     c.h = pair % ny;
@@ -161,7 +169,7 @@ __device__ __forceinline__ BlockCoord block_coord(GridPos g) {
   }
   return c;
 }
-__device__ __forceinline__ BlockCoord block_coord() { return block_coord(hw_grid()); }
+__device__ __forceinline__ BlockCoord block_coord(bool zigzag = false) { return block_coord(hw_grid(), zigzag); }
 
 // Reductions over the four 16-lane groups of a wave (the key rows of an
 // S^T tile): v_permlane16_swap / v_permlane32_swap with both operands = x
@@ -485,7 +493,7 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int lr = lane & 15, lg = lane >> 4;
-  const BlockCoord bc = block_coord();
+  const BlockCoord bc = block_coord(/*zigzag=*/true);
   const int64_t qblock = p.causal ? (int64_t)gridDim.x - 1 - bc.x : bc.x;
   const int64_t q0 = qblock * QPB;
   const int64_t b = bc.b, h = bc.h, hk = h / p.group;  // K/V head of this query head

@@ -117,14 +117,14 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
     int64_t q = threadIdx.x;
     for (; q + kThreads < nv; q += 2 * kThreads) {
       const int64_t q2 = q + kThreads;
-      float4 p0 = P[q], p1 = P[q2];
-      const float4 g0 = G[q], g1 = G[q2];
-      float4 m0 = M[q], m1 = M[q2], v0 = V[q], v1 = V[q2];
+      float4 p0 = ld_stream(P + q), p1 = ld_stream(P + q2);
+      const float4 g0 = ld_stream(G + q), g1 = ld_stream(G + q2);
+      float4 m0 = ld_stream(M + q), m1 = ld_stream(M + q2), v0 = ld_stream(V + q), v1 = ld_stream(V + q2);
       update(p0, g0, m0, v0);
       update(p1, g1, m1, v1);
-      P[q] = p0, P[q2] = p1;
-      M[q] = m0, M[q2] = m1;
-      V[q] = v0, V[q2] = v1;
+      st_stream(P + q, p0), st_stream(P + q2, p1);
+      st_stream(M + q, m0), st_stream(M + q2, m1);
+      st_stream(V + q, v0), st_stream(V + q2, v1);
       if (low) {
         store_low4(low + begin + q * 4, p0);
         store_low4(low + begin + q2 * 4, p1);
