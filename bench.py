@@ -213,15 +213,34 @@ def bench_hbm(iters):
     ms = time_gpu(lambda: F.fast_aten_native_layer_norm(x, (768,), w, b, 1e-5), iters)
     nbytes = 16384 * 768 * 4 * 2 + 16384 * 8
     out.append({"kernel": "layer_norm_fwd f32 [16384,768]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    _, mean, rstd = F.fast_aten_native_layer_norm(x, (768,), w, b, 1e-5)
+    dy = torch.randn(16384, 768, generator=g).to("mojo")
+    ms = time_gpu(lambda: F.fast_aten_native_layer_norm_backward(dy, x, (768,), mean, rstd, w, b,
+                                                                 [True, True, True]), iters)
+    # dy, x in; dx out; mean/rstd in; the weight/bias grads are a column
+    # reduction over the rows (their 2 x 768 floats are not counted)
+    nbytes = 16384 * 768 * 4 * 3 + 16384 * 8
+    out.append({"kernel": "layer_norm_bwd f32 [16384,768] (dx, dgamma, dbeta)", "ms": ms, "gbs": nbytes / ms / 1e6})
     h = torch.randn(16384, 3072, generator=g).bfloat16().to("mojo")
     ms = time_gpu(lambda: F.fast_aten_gelu(h), iters)
     nbytes = 16384 * 3072 * 2 * 2
     out.append({"kernel": "gelu_fwd bf16 [16384,3072]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    dh = torch.randn(16384, 3072, generator=g).bfloat16().to("mojo")
+    ms = time_gpu(lambda: F.fast_aten_gelu_backward(dh, h), iters)
+    nbytes = 16384 * 3072 * 2 * 3
+    out.append({"kernel": "gelu_bwd bf16 [16384,3072]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    del h, dh
     lg = torch.randn(16384, 50257, generator=g).bfloat16().to("mojo")
     ms = time_gpu(lambda: F.fast_aten__log_softmax(lg, 1, False), max(3, iters // 4))
     nbytes = 16384 * 50257 * 2 * 2
     out.append({"kernel": "log_softmax_fwd bf16 [16384,50257]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    lp = F.fast_aten__log_softmax(lg, 1, False)
     del lg
+    dlp = torch.randn(16384, 50257, generator=g).bfloat16().to("mojo")
+    ms = time_gpu(lambda: F.fast_aten__log_softmax_backward_data(dlp, lp, 1, torch.bfloat16), max(3, iters // 4))
+    nbytes = 16384 * 50257 * 2 * 3
+    out.append({"kernel": "log_softmax_bwd bf16 [16384,50257]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    del lp, dlp
     n = 124_439_808
     p_, g_, m_, v_ = (torch.randn(n, generator=g).to("mojo") for _ in range(4))
     v_ = v_.abs()

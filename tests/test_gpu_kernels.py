@@ -250,13 +250,21 @@ def test_gelu(kernels, dtype, approx):
               what="gelu bwd")
 
 
+# Rows longer than 1024 of one dtype run the register-resident kernels: odd
+# lengths make every row start at a different phase of its 16-byte chunks;
+# (5, 50257, f32) takes 16 chunks per thread, (3, 140001, bf16) is past their
+# capacity and takes the streaming kernels.
 @pytest.mark.parametrize("rows,cols,dtype", [(64, 50257, torch.bfloat16), (300, 1000, torch.float32),
-                                             (17, 3, torch.float32), (8, 4096, torch.float32)])
+                                             (17, 3, torch.float32), (8, 4096, torch.float32),
+                                             (5, 50257, torch.float32), (6, 1027, torch.float16),
+                                             (7, 2048, torch.bfloat16), (3, 140001, torch.bfloat16)])
 @pytest.mark.parametrize("log", [0, 1])
 def test_softmax_fwd_bwd(kernels, rows, cols, dtype, log):
     x = randn(rows, cols) * 3
     x[1, :] = float("-inf") if cols > 3 else x[1, :]
     x[2, 0] = float("-inf")
+    if rows > 3:
+        x[3, cols // 2] = float("nan")  # a NaN poisons its row only
     xq = x.to(dtype)
     tx = dev(xq)
     y = torch.empty(rows, cols, dtype=dtype, device="cuda")
