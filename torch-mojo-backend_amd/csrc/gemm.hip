@@ -706,9 +706,12 @@ int64_t rs_slots_of(int cfg, int64_t n) {
 // Pick the configuration that finishes in the least time: whole rounds of
 // the CUs' block slots (two C128 blocks or one C256 block per CU) times the
 // per-round time measured on gfx950 at K = 768..3072 (a C256 round does
-// twice a C128 round's work in 1.82x its time).  Then split K when the
-// output alone cannot fill the chip.
-Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool b_kcontig) {
+// twice a C128 round's work in 1.82x its time).  An m-contiguous A (a weight
+// gradient dY^T X) reads both operands through transposing LDS reads, which
+// C256 tiles halve per flop: when its C256 tiles fill the CUs it takes them
+// (the 50304 x 768 embedding gradient: 1.72 -> 1.53 ms).  Then split K when
+// the output alone cannot fill the chip.
+Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool a_kcontig, bool b_kcontig) {
   Plan best{0, 1, k};
   const int64_t t128 = tiles_of(0, batch, m, n), t256 = tiles_of(1, batch, m, n), t192 = tiles_of(2, batch, m, n);
   const double c128 = (double)((t128 + 2 * kCUs - 1) / (2 * kCUs));
@@ -717,6 +720,7 @@ Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool b_kcontig) {
   double cbest = c128;
   if (t256 >= kCUs && c256 < cbest) best.cfg = 1, cbest = c256;
   if (b_kcontig && t192 >= kCUs && c192 < cbest) best.cfg = 2, cbest = c192;
+  if (!a_kcontig && t256 >= kCUs) best.cfg = 1;
   static const char* forced = getenv("MI355X_GEMM_TILE");  // tuning override: "128", "192" or "256"
   if (forced) {
     const int f = atoi(forced);
@@ -855,7 +859,7 @@ WsLayout ws_layout(int64_t batch, int64_t m, int64_t n, int64_t k, const void* a
   w.pack_a = !in_place(a, a_rs, a_cs, a_bs, m) || (a_cs != 1 && (double)m < small_rows);
   // B as [n rows][k]: row stride b_cs, k stride b_rs
   w.pack_b = !in_place(b, b_cs, b_rs, b_bs, n) || (b_rs != 1 && (double)n < small_rows);
-  w.plan = plan_gemm(batch, m, n, k, w.pack_b || b_rs == 1);
+  w.plan = plan_gemm(batch, m, n, k, w.pack_a || a_cs == 1, w.pack_b || b_rs == 1);
   auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
   // split-K partials of C, then of the optional row sums of A
   w.part_bytes = w.plan.splits > 1 ? up((int64_t)w.plan.splits * batch * m * n * 4) +
