@@ -366,6 +366,46 @@ __device__ __forceinline__ void store_tile(CT* __restrict__ C, int c_rs, const f
     }
 }
 
+// Full wave tiles without beta: the accumulators go through a per-wave LDS
+// slab 16 rows at a time (one MFMA row of tiles, f32, rows padded by 2
+// floats) and leave as row-contiguous 16-byte stores: 8 bf16/f16 or 4 f32
+// per lane instead of one element per store.  The slab holds 16 x (WN + 2)
+// floats; `lane` is the wave lane.  Requires 16-byte aligned rows of C.
+template <typename CT, typename T, bool ROUND, int TM, int TN>
+__device__ __forceinline__ void store_tile_lds(CT* __restrict__ C, int c_rs, const f32x4 (&acc)[TM][TN],
+                                               const float (&bias)[TN], float* slab, int lr, int lg, int lane) {
+  constexpr int WN = TN * 16, LD = WN + 2;       // slab row stride in floats
+  constexpr int E = 16 / sizeof(CT);             // elements per 16-byte store
+  constexpr int CHUNKS = 16 * WN / E;            // 16-byte chunks per 16-row slab
+  static_assert(WN % E == 0 && CHUNKS % 64 == 0, "slab shape");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = acc[i][j][e] + bias[j];
+        if (ROUND) v = (float)(T)v;
+        slab[(lg * 4 + e) * LD + j * 16 + lr] = v;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int it = 0; it < CHUNKS / 64; ++it) {
+      const int ch = it * 64 + lane, r = ch / (WN / E), c = (ch % (WN / E)) * E;
+      const float* src = slab + r * LD + c;
+      struct alignas(16) Out { CT v[E]; } out;
+#pragma unroll
+      for (int e = 0; e < E; ++e) out.v[e] = (CT)src[e];
+      *(Out*)(C + (i * 16 + r) * c_rs + c) = out;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 template <typename CT, typename T, int TM, int TN>
 __device__ __forceinline__ void store_any(CT* C, int c_rs, const f32x4 (&acc)[TM][TN], const float (&bias)[TN],
                                           bool beta, bool round, int rows_left, int cols_left, int lr, int lg) {
@@ -502,6 +542,9 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
     cur = cur == S - 1 ? 0 : cur + 1;
   }
 
+  // every wave is past its last LDS read: the stages become store slabs
+  __syncthreads();
+  float* const slab = (float*)lds + wave * (16 * (WN + 2));
   const int64_t row0 = m0 + wm * WM, col0 = n0 + wn * WN;
   if (RS && rs_on && lr == 0) {
     // lane (lg, 0) holds rows 4*lg .. 4*lg+3 of each 16-row fragment
@@ -527,7 +570,10 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
 #pragma unroll
     for (int j = 0; j < TN; ++j) bias[j] = 0.f;
     float* P = g.part + ((int64_t)split * g.batch + bidx) * g.m * g.n + row0 * g.n + col0;
-    store_any<float, T>(P, (int)g.n, acc, bias, false, false, rows_left, cols_left, lr, lg);
+    if (rows_left == WM && cols_left == WN && (g.n & 3) == 0 && ((uintptr_t)g.part & 15) == 0)
+      store_tile_lds<float, T, false>(P, (int)g.n, acc, bias, slab, lr, lg, lane);
+    else
+      store_any<float, T>(P, (int)g.n, acc, bias, false, false, rows_left, cols_left, lr, lg);
     return;
   }
 #pragma unroll
@@ -539,6 +585,15 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   char* Cb = (char*)g.c + ((int64_t)bidx * g.c_bs + row0 * g.c_rs + col0) * c_es;
   const int c_rs = (int)g.c_rs;
   const bool rnd = g.round_c && g.c_dt == MI355X_F32;  // 16-bit outputs are already rounded
+  const bool full = rows_left == WM && cols_left == WN && !g.beta && ((uintptr_t)g.c & 15) == 0 &&
+                    (c_rs * c_es) % 16 == 0 && (g.c_bs * c_es) % 16 == 0;
+  if (full) {
+    if (g.c_dt == MI355X_BF16) store_tile_lds<bf16, T, false>((bf16*)Cb, c_rs, acc, bias, slab, lr, lg, lane);
+    else if (g.c_dt == MI355X_F16) store_tile_lds<f16, T, false>((f16*)Cb, c_rs, acc, bias, slab, lr, lg, lane);
+    else if (rnd) store_tile_lds<float, T, true>((float*)Cb, c_rs, acc, bias, slab, lr, lg, lane);
+    else store_tile_lds<float, T, false>((float*)Cb, c_rs, acc, bias, slab, lr, lg, lane);
+    return;
+  }
   if (g.c_dt == MI355X_BF16) store_any<bf16, T>((bf16*)Cb, c_rs, acc, bias, g.beta, false, rows_left, cols_left, lr, lg);
   else if (g.c_dt == MI355X_F32) store_any<float, T>((float*)Cb, c_rs, acc, bias, g.beta, rnd, rows_left, cols_left, lr, lg);
   else store_any<f16, T>((f16*)Cb, c_rs, acc, bias, g.beta, false, rows_left, cols_left, lr, lg);
