@@ -189,3 +189,18 @@ def test_gemma_shaped_prefill_matches_cpu(mojo):
         want = ref(idx)
     err = (got - want).abs().max().item()
     assert err <= 5e-2 * want.abs().max().item() + 5e-2, err
+
+
+@pytest.mark.parametrize("dtype,bits", [(torch.float32, torch.int32), (torch.bfloat16, torch.int16)])
+def test_stack_and_cat_of_many_pieces_are_bit_exact(mojo, dtype, bits):
+    """stack/cat of many contiguous pieces (clip_grad_norm_ stacks one norm
+    per parameter) run as one multi-tensor launch; signed zeros, NaN,
+    infinities and subnormals must come through bit for bit."""
+    vals = torch.tensor([0.0, -0.0, float("nan"), float("inf"), -float("inf"), 1e-40, -3.5, 2.0 ** 100] * 3)
+    pieces = [v.clone().to(dtype) for v in vals]
+    got = torch.stack([x.to("mojo") for x in pieces]).cpu()
+    assert torch.equal(got.view(bits), torch.stack(pieces).view(bits))
+    rows = [torch.randn(5 + i).to(dtype) for i in range(10)]
+    rows[3][2] = -0.0
+    got = torch.cat([r.to("mojo") for r in rows]).cpu()
+    assert torch.equal(got.view(bits), torch.cat(rows).view(bits))

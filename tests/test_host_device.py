@@ -427,3 +427,22 @@ def test_checkpoints_pickle_as_cpu_tensors(mojo, tmp_path):
     assert loaded["t"].device.type == "cpu" and torch.equal(loaded["t"], torch.arange(6.0))
     for k, v in ref.items():
         assert loaded["model"][k].device.type == "cpu" and torch.equal(loaded["model"][k], v)
+
+
+@pytest.mark.parametrize("dtype,bits", [(torch.float32, torch.int32), (torch.bfloat16, torch.int16)])
+def test_stack_and_cat_of_many_pieces_are_bit_exact(mojo, dtype, bits):
+    """The multi-tensor path of stack/cat (8 or more contiguous pieces)
+    keeps signed zeros and infinities bit for bit.  (The host stand-in's
+    x86 arithmetic may return a different NaN payload; the GPU test checks
+    NaN bits too.)"""
+    vals = torch.tensor([0.0, -0.0, float("nan"), float("inf"), -float("inf"), 1e-40, -3.5, 2.0 ** 100] * 3)
+    pieces = [v.clone().to(dtype) for v in vals]
+    got = torch.stack([x.to("mojo") for x in pieces]).cpu()
+    exp = torch.stack(pieces)
+    nan = torch.isnan(exp)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got[~nan].view(bits), exp[~nan].view(bits))
+    rows = [torch.randn(5 + i).to(dtype) for i in range(10)]
+    rows[3][2] = -0.0
+    got = torch.cat([r.to("mojo") for r in rows]).cpu()
+    assert torch.equal(got.view(bits), torch.cat(rows).view(bits))
