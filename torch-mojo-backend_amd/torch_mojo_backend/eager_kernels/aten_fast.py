@@ -1399,6 +1399,10 @@ def drop_param_copies_written_by(func, args, kwargs) -> None:
             (i, a.name) for i, a in enumerate(func._schema.arguments)
             if a.alias_info is not None and a.alias_info.is_write
         )
+        if func._schema.name in ("aten::_fused_adamw_", "aten::_fused_adam_"):
+            # only the parameter list can hold parameter storage: the other
+            # written lists are gradients, moments and step counters
+            spec = tuple(x for x in spec if x[0] == 0)
         _written_args[func] = spec
     for i, name in spec:
         v = args[i] if i < len(args) else kwargs.get(name)
@@ -2182,20 +2186,24 @@ def fast_aten__fused_adamw_(
     if amsgrad and len(max_exp_avg_sqs) != n:
         raise RuntimeError("_fused_adamw_: max_exp_avg_sqs must match params when amsgrad=True")
     descs = (AdamWTensor * n)()
+    f32 = torch.float32
+    P, G, M, V, S = ([_require(t) for t in lst] for lst in lists)
     for i in range(n):
-        p, g, m, v, s = (_require(x[i]) for x in lists)
-        for name, t in (("param", p), ("grad", g), ("exp_avg", m), ("exp_avg_sq", v)):
-            if t._dtype != torch.float32 or not t._is_contiguous:
-                return NOT_HANDLED
-            if t._numel != p._numel:
-                raise RuntimeError(f"_fused_adamw_: {name} {i} has {t._numel} elements, param has {p._numel}")
-        if s._dtype != torch.float32 or s._numel != 1:
+        p, g, m, v, s = P[i], G[i], M[i], V[i], S[i]
+        pn = p._numel
+        if not (p._dtype == f32 and g._dtype == f32 and m._dtype == f32 and v._dtype == f32
+                and p._is_contiguous and g._is_contiguous and m._is_contiguous and v._is_contiguous):
+            return NOT_HANDLED
+        if g._numel != pn or m._numel != pn or v._numel != pn:
+            name, t = next((nm, t) for nm, t in (("grad", g), ("exp_avg", m), ("exp_avg_sq", v)) if t._numel != pn)
+            raise RuntimeError(f"_fused_adamw_: {name} {i} has {t._numel} elements, param has {pn}")
+        if s._dtype != f32 or s._numel != 1:
             return NOT_HANDLED
         d = descs[i]
         d.param, d.grad, d.exp_avg, d.exp_avg_sq = p._ptr, g._ptr, m._ptr, v._ptr
         d.max_exp_avg_sq = _require(max_exp_avg_sqs[i])._ptr if amsgrad else None
         d.step = s._ptr
-        d.numel = p._numel
+        d.numel = pn
     lr_t = _t(lr)
     lr_value = 0.0 if lr_t is not None else float(lr)
     if lr_t is not None and lr_t._dtype != torch.float32:
