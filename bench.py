@@ -394,7 +394,7 @@ def main():
     if "sdpa" in res:
         s = res["sdpa"]
         line["roofline"] = {
-            "kernel": "causal flash attention fwd+bwd (attn_fwd + bwd_delta + bwd_dkv + bwd_dq), cfg 1",
+            "kernel": "causal flash attention fwd+bwd (attn_fwd_v2 + attn_bwd_delta + attn_bwd_dkv_dq), cfg 1",
             "bound": "mfma",
             "achieved": s["fwd_bwd_tflops"],
             "peak": PEAK_BF16_TFLOPS,

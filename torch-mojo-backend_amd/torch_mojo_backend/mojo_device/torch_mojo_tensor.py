@@ -141,6 +141,7 @@ class TorchMojoTensor(torch.Tensor):
     def _make(cls, holder, ptr, shape, strides, offset, dtype, device, contiguous=None):
         shape = tuple(shape)
         strides = tuple(strides)
+        tdev = torch_device_of(device)
         res = torch.Tensor._make_wrapper_subclass(
             cls,
             shape,
@@ -148,7 +149,7 @@ class TorchMojoTensor(torch.Tensor):
             storage_offset=offset,
             dtype=dtype,
             layout=torch.strided,
-            device=torch_device_of(device),
+            device=tdev,
             requires_grad=False,
         )
         res._holder = holder
@@ -160,7 +161,7 @@ class TorchMojoTensor(torch.Tensor):
         res._itemsize = dtype.itemsize
         res._numel = math.prod(shape)
         res._device = device
-        res._torch_device = torch_device_of(device)
+        res._torch_device = tdev
         res._is_contiguous = (
             compute_contiguous(shape, strides) if contiguous is None else contiguous
         )
