@@ -58,6 +58,11 @@ int mi355x_abi_version(void);
 const char* mi355x_last_error(void);
 /* Offload target the code object was built for ("gfx950"). */
 const char* mi355x_target(void);
+/* Digest of the sources and flags the library was built from (no
+ * counterpart in the reference, whose kernels are JIT-built per variant:
+ * the loader compares it with the sources beside the package and refuses a
+ * stale prebuilt library). */
+const char* mi355x_source_hash(void);
 
 /* ---- data movement (tensor_holder.mojo:144-657 CopyStrided / cast
  *      _CastSpecExtension aten_fast.py:1232, PermuteCopy

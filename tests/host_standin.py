@@ -84,6 +84,9 @@ class HostStandIn:
     def mi355x_target(self):
         return b"host"
 
+    def mi355x_source_hash(self):
+        return b"host"
+
     # ---- data movement ----
     def mi355x_copy(self, dst, ddt, dst_st, src, sdt, src_st, shape, ndim, stream):
         shp = _arr(shape, ndim)

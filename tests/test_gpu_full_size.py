@@ -1,0 +1,104 @@
+"""Parity at the BASELINE configs' real sizes, through the C ABI.
+
+Config 1 (causal SDPA [8,12,1024,64] bf16): O, LSE, dQ, dK and dV of three
+(batch, head) slices against the f64 oracle.  The slices sit on different
+XCDs of the XCD-aware block map (each XCD owns 12 consecutive (b, h) pairs
+at this shape) and take different places in its heaviest-first tile order,
+so the one-launch dK/dV + dQ grid is pinned where it is timed.
+
+Config 2 (GEMMs at M = 16384): every (K, N) of the sweep, in the three
+launches of a linear layer as the autocast model issues them -- forward
+x W^T + b (bf16 out), dX = dY W (f32 out rounded to bf16), dW = dY^T X (f32
+out rounded to bf16) with the bias gradient as the row sums of dY^T -- each
+against the f64 oracle on sampled rows that cross every row tile and every
+column of the output, so each tile plan (tile size, split-K count) the
+planner picks at these shapes is checked.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from abi import CODE, bhs, call, dev, host, lib, np64, p, tol_close, workspace  # noqa: F401
+from oracle import ops as O
+from test_gpu_gemm_attention import _attn_bwd, _attn_fwd
+
+pytestmark = pytest.mark.gpu
+
+
+def test_attention_cfg1_slices_match_oracle(kernels):
+    B, H, S, D = 8, 12, 1024, 64
+    g = torch.Generator().manual_seed(101)
+    q, k, v, do = (torch.randn(B, H, S, D, generator=g).bfloat16() for _ in range(4))
+    tq, tk, tv, tdo = dev(q), dev(k), dev(v), dev(do)
+    o, lse = _attn_fwd(tq, tk, tv, True)
+    dq, dk, dv = _attn_bwd(tdo, tq, tk, tv, o, lse, True)
+    got = {name: host(t) for name, t in (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv))}
+    for b, h in ((0, 0), (4, 5), (7, 11)):  # pairs 0, 53, 95: XCDs 0, 4, 7
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        qs, ks, vs, dos = (t[sl].double().numpy() for t in (q, k, v, do))
+        eo, el = O.sdpa_forward(qs, ks, vs, causal=True)
+        what = f"cfg1 b{b} h{h}"
+        tol_close(got["o"][sl].double().numpy(), eo, atol=2e-2, rtol=2e-2, what=f"O {what}")
+        tol_close(got["lse"][sl].double().numpy(), el, atol=1e-3, rtol=1e-3, what=f"LSE {what}")
+        # backward from the device's own O and LSE, as the autograd pair runs it
+        edq, edk, edv = O.sdpa_backward(dos, qs, ks, vs, got["o"][sl].double().numpy(),
+                                        got["lse"][sl].double().numpy(), causal=True)
+        tol_close(got["dv"][sl].double().numpy(), edv, atol=3e-2, rtol=2e-2, what=f"dV {what}")
+        tol_close(got["dk"][sl].double().numpy(), edk, atol=3e-2, rtol=2e-2, what=f"dK {what}")
+        tol_close(got["dq"][sl].double().numpy(), edq, atol=3e-2, rtol=2e-2, what=f"dQ {what}")
+
+
+def _gemm_ex(c, c_rs, a, ars, acs, b, brs, bcs, m, n, k, bias=None, flags=0, rowsum=None):
+    ws_n = lib().mi355x_gemm_workspace_bytes(p(a), ars, acs, 0, p(b), brs, bcs, 0, CODE[torch.bfloat16], 1, m, n, k)
+    ws = workspace(ws_n) if ws_n else None
+    call("mi355x_gemm_ex", p(c), CODE[c.dtype], c_rs, 0, p(a), ars, acs, 0, p(b), brs, bcs, 0,
+         CODE[torch.bfloat16], p(bias), CODE[bias.dtype] if bias is not None else 0, flags,
+         p(rowsum), CODE[torch.float32] if rowsum is not None else 0, 1, m, n, k, p(ws), ws_n, None)
+
+
+def _rows(total, step):
+    r = np.arange(0, total, step)
+    return np.unique(np.concatenate([r, [total - 1]]))
+
+
+@pytest.mark.parametrize("K,N", [(768, 2304), (768, 768), (768, 3072), (3072, 768), (768, 50304)])
+def test_gemm_cfg2_linear_launches_match_oracle(kernels, K, N):
+    M = 16384
+    g = torch.Generator().manual_seed(K * 7 + N)
+    X = torch.randn(M, K, generator=g).bfloat16()
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    bias = (torch.randn(N, generator=g) * 0.02).bfloat16()
+    dY = torch.randn(M, N, generator=g).bfloat16()
+    tx, tw, tb, tdy = dev(X), dev(W), dev(bias), dev(dY)
+    rows = _rows(M, 41)  # 401 rows: every 128- and 256-row tile, at varying offsets
+    Xr, Wd, dYr = X[rows].double().numpy(), W.double().numpy(), dY[rows].double().numpy()
+
+    # forward: y = x W^T + b, B = W^T read in place (k-contiguous)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _gemm_ex(y, N, tx, K, 1, tw, 1, K, M, N, K, bias=tb)
+    tol_close(host(y[rows]).double().numpy(), O.addmm(Xr, Wd.T, bias.double().numpy()),
+              atol=2e-2, rtol=2e-2, what=f"fwd {K}->{N}")
+    del y
+
+    # dX = dY W, f32 out holding bf16-rounded values
+    dx = torch.empty(M, K, dtype=torch.float32, device="cuda")
+    _gemm_ex(dx, K, tdy, N, 1, tw, K, 1, M, K, N, flags=2)
+    got = host(dx[rows])
+    assert torch.equal(got, got.bfloat16().float())
+    tol_close(got.double().numpy(), O.addmm(dYr, Wd), atol=2e-2, rtol=2e-2, what=f"dX {K}->{N}")
+    del dx
+
+    # dW = dY^T X (A = dY^T: m-contiguous), db = row sums of dY^T
+    dw = torch.empty(N, K, dtype=torch.float32, device="cuda")
+    db = torch.empty(N, dtype=torch.float32, device="cuda")
+    _gemm_ex(dw, K, tdy, 1, N, tx, K, 1, N, K, M, flags=2, rowsum=db)
+    wrows = _rows(N, max(1, N // 256))
+    got = host(dw[wrows])
+    assert torch.equal(got, got.bfloat16().float())
+    dyc = dY[:, wrows].double().numpy()
+    tol_close(got.double().numpy(), O.addmm(dyc.T, X.double().numpy()), atol=5e-2, rtol=1e-2,
+              what=f"dW {K}->{N}")
+    tol_close(host(db).double().numpy(), dY.sum(0, dtype=torch.float64).numpy(), atol=5e-2, rtol=1e-2, what=f"db {K}->{N}")

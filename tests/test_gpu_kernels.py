@@ -457,6 +457,28 @@ def test_foreach_norm_and_apply(kernels):
         assert torch.equal(host(t), x * 0.25)
 
 
+@pytest.mark.parametrize("ord_", [float("inf"), 2.0, 1.0])
+def test_foreach_norm_propagates_nan(kernels, ord_):
+    """A NaN anywhere gives a NaN norm, as torch's does, for every order:
+    in a 16-byte-aligned chunk, in the scalar tail and in a second 32768-
+    element chunk of a multi-chunk tensor (clip_grad_norm_(norm_type=inf,
+    error_if_nonfinite=True) must see NaN gradients)."""
+    sizes = [3 * 32768 + 5, 1001, 40000]
+    xs = [randn(s) for s in sizes]
+    xs[0][70000] = float("nan")   # third chunk, aligned body
+    xs[1][1000] = float("nan")    # scalar tail of a 1001-element tensor
+    tx = [dev(x) for x in xs]
+    n = len(sizes)
+    outs = [torch.empty((), device="cuda") for _ in sizes]
+    numels = i64(*sizes)
+    ws_n = lib().mi355x_foreach_norm_workspace_bytes(numels, n)
+    ws = workspace(ws_n)
+    ptr = lambda ts: (ctypes.c_void_p * n)(*[p(t) for t in ts])  # noqa: E731
+    call("mi355x_foreach_norm", ptr(outs), 0, ptr(tx), 0, numels, n, ord_, p(ws), ws_n, None)
+    got = [host(o).item() for o in outs]
+    assert math.isnan(got[0]) and math.isnan(got[1]) and math.isfinite(got[2]), got
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_foreach_norm_orders_and_apply_ops(kernels, dtype):
     """Every norm order and the list/scalar forms of ADD, ADDCMUL, LERP and

@@ -446,3 +446,49 @@ def test_stack_and_cat_of_many_pieces_are_bit_exact(mojo, dtype, bits):
     rows[3][2] = -0.0
     got = torch.cat([r.to("mojo") for r in rows]).cpu()
     assert torch.equal(got.view(bits), torch.cat(rows).view(bits))
+
+
+@pytest.mark.parametrize("n_pieces", [3, 9])
+def test_cat_rejects_mismatched_shapes(mojo, n_pieces):
+    """torch.cat's shape checks on the device (both the per-piece path and
+    the multi-tensor path of 8 or more pieces): a piece whose size differs
+    outside the cat dim, or whose rank differs, raises instead of writing
+    past the output."""
+    pieces = [torch.randn(2, 3).to("mojo") for _ in range(n_pieces - 1)]
+    with pytest.raises(RuntimeError, match="Sizes of tensors must match"):
+        torch.cat(pieces + [torch.randn(2, 5).to("mojo")])
+    with pytest.raises(RuntimeError, match="same number of dimensions"):
+        torch.cat(pieces + [torch.randn(2, 3, 1).to("mojo")])
+    ok = [torch.randn(2, 3) for _ in range(n_pieces)]
+    assert torch.equal(torch.cat([x.to("mojo") for x in ok], 1).cpu(), torch.cat(ok, 1))
+
+
+@pytest.mark.parametrize("case", ["noncontig", "mixed_dtype", "dim1"])
+def test_cat_of_many_pieces_off_the_fast_path(mojo, case):
+    """Conditions that keep cat off its multi-tensor path (a non-contiguous
+    piece, mixed dtypes, a cat dim with leading extent > 1) still give
+    torch.cat's result."""
+    g = torch.Generator().manual_seed(5)
+    pieces = [torch.randn(4, 6, generator=g) for _ in range(9)]
+    dim = 0
+    if case == "noncontig":
+        pieces[4] = torch.randn(6, 4, generator=g).t()
+    elif case == "mixed_dtype":
+        pieces[2] = pieces[2].bfloat16()
+    else:
+        dim = 1
+    got = torch.cat([x.to("mojo") for x in pieces], dim).cpu()
+    exp = torch.cat(pieces, dim)
+    assert got.dtype == exp.dtype and torch.equal(got, exp)
+
+
+def test_fused_adamw_checks_the_amsgrad_state(mojo):
+    """max_exp_avg_sqs gets the same numel check as the other state lists
+    (a short buffer would be read and written past its end)."""
+    p = torch.randn(10).to("mojo")
+    g, m, v = (torch.randn(10).to("mojo") for _ in range(3))
+    step = torch.zeros(()).to("mojo")
+    short = torch.zeros(7).to("mojo")
+    with pytest.raises(RuntimeError, match="max_exp_avg_sq 0 has 7 elements"):
+        torch._fused_adamw_([p], [g], [m], [v.abs()], [short], [step], lr=1e-3, beta1=0.9, beta2=0.99,
+                            weight_decay=0.0, eps=1e-8, amsgrad=True, maximize=False)

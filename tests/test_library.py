@@ -54,6 +54,17 @@ def test_abi_version_and_target(raw):
     assert raw.mi355x_target() == b"gfx950"
 
 
+def test_library_matches_its_sources(raw):
+    """The built library carries the digest of the sources it was built
+    from, and the loader's digest of the tree agrees (a stale prebuilt .so
+    would be refused with a rebuild message)."""
+    from torch_mojo_backend.eager_kernels import _expected_source_hash
+
+    raw.mi355x_source_hash.restype = ctypes.c_char_p
+    built = raw.mi355x_source_hash().decode()
+    assert built != "unknown" and built == _expected_source_hash()
+
+
 def test_host_side_validation_reports_errors(raw):
     """Argument checks fail before any launch, with a message."""
     from torch_mojo_backend.eager_kernels import SIGNATURES

@@ -40,6 +40,20 @@ COMMON_FLAGS = [
 ]
 
 
+def _hash_flags() -> list[str]:
+    """The flags the digest covers (paths excluded: the tree may move)."""
+    return [f for f in COMMON_FLAGS if not f.startswith("-I")]
+
+
+def _source_hash() -> str:
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_mi355x_srchash", PKG_DIR / "torch_mojo_backend" / "_srchash.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.source_hash(_hash_flags())
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -53,15 +67,16 @@ def _deps_mtime() -> float:
     return max(p.stat().st_mtime for p in deps if p.exists())
 
 
-def _compile(src: Path, force: bool) -> Path:
+def _compile(src: Path, force: bool, defines: tuple[str, ...] = ()) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
     if (
         not force
+        and not defines
         and obj.exists()
         and obj.stat().st_mtime >= max(src.stat().st_mtime, _deps_mtime())
     ):
         return obj
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *defines, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"compiling {src.name} failed:\n{proc.stderr}")
@@ -75,8 +90,10 @@ def build(force: bool = True, jobs: int | None = None) -> Path:
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = jobs or min(8, os.cpu_count() or 4)
+    # runtime.hip carries the source digest, so it is rebuilt every time
+    digest = (f'-DMI355X_SOURCE_HASH="{_source_hash()}"',)
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(s, force), sources))
+        objs = list(pool.map(lambda s: _compile(s, force, digest if s.name == "runtime.hip" else ()), sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -65,7 +65,7 @@ __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
   v = b2 * v + (1.f - b2) * g * g;
   float vv = v;
   if (vmax) {
-    *vmax = fmaxf(*vmax, v);
+    *vmax = nan_max(*vmax, v);
     vv = *vmax;
   }
   const float denom = sqrtf(vv) / bc2_sqrt + eps;
@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(kThreads) norm_partial(NormBatch b, int kind, 
   auto take = [&](float v) {
     if (kind == 0) acc += v * v;
     else if (kind == 1) acc += fabsf(v);
-    else acc = fmaxf(acc, fabsf(v));
+    else acc = nan_max(acc, fabsf(v));
   };
   int64_t e0 = begin;
   if ((((uintptr_t)x) & 15) == 0) {
@@ -206,12 +206,12 @@ __global__ void __launch_bounds__(kThreads) norm_partial(NormBatch b, int kind, 
   }
   for (int64_t e = e0 + threadIdx.x; e < end; e += kThreads) take(to_f32(x[e]));
   if (kind == 2) {
-    acc = wave_max(acc);
+    acc = wave_max_nan(acc);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
     __syncthreads();
     acc = red[0];
-    for (int w = 1; w < kThreads / 64; ++w) acc = fmaxf(acc, red[w]);
+    for (int w = 1; w < kThreads / 64; ++w) acc = nan_max(acc, red[w]);
   } else {
     acc = block_sum(acc, red);
   }
@@ -225,14 +225,14 @@ __global__ void __launch_bounds__(kThreads) norm_final(NormBatch b, int kind, co
   const int64_t c0 = b.chunk_start[k], c1 = b.chunk_start[k + 1];
   float acc = 0.f;
   for (int64_t c = c0 + threadIdx.x; c < c1; c += kThreads)
-    acc = kind == 2 ? fmaxf(acc, part[c]) : acc + part[c];
+    acc = kind == 2 ? nan_max(acc, part[c]) : acc + part[c];
   if (kind == 2) {
-    acc = wave_max(acc);
+    acc = wave_max_nan(acc);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
     __syncthreads();
     acc = red[0];
-    for (int w = 1; w < kThreads / 64; ++w) acc = fmaxf(acc, red[w]);
+    for (int w = 1; w < kThreads / 64; ++w) acc = nan_max(acc, red[w]);
   } else {
     acc = block_sum(acc, red);
   }

@@ -42,4 +42,9 @@ const char* mi355x_last_error(void) { return mi::g_error; }
 
 const char* mi355x_target(void) { return "gfx950"; }
 
+#ifndef MI355X_SOURCE_HASH
+#define MI355X_SOURCE_HASH "unknown"
+#endif
+const char* mi355x_source_hash(void) { return MI355X_SOURCE_HASH; }
+
 }  // extern "C"

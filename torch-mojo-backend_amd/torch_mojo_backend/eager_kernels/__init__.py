@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mi355x_abi_version": (c_int, []),
     "mi355x_last_error": (c_char_p, []),
     "mi355x_target": (c_char_p, []),
+    "mi355x_source_hash": (c_char_p, []),
     "mi355x_copy": (c_int, [c_vp, c_int, P_i64, c_vp, c_int, P_i64, P_i64, c_int, c_vp]),
     "mi355x_fill": (c_int, [c_vp, c_int, P_i64, P_i64, c_int, c_double, c_vp]),
     "mi355x_arange": (c_int, [c_vp, c_int, c_i64, c_double, c_double, c_vp]),
@@ -230,7 +231,28 @@ def _load() -> ctypes.CDLL:
     version = lib.mi355x_abi_version()
     if version != ABI_VERSION:
         raise KernelLibraryError(f"{path} has ABI {version}, expected {ABI_VERSION}: rebuild it")
+    built = lib.mi355x_source_hash().decode()
+    expected = _expected_source_hash()
+    if expected is not None and built != expected:
+        raise KernelLibraryError(
+            f"{path} was built from other sources (digest {built}, sources {expected}): rebuild it with"
+            " `python torch-mojo-backend_amd/build.py`"
+        )
     return lib
+
+
+def _expected_source_hash():
+    """Digest of csrc/ + include/ beside the package (None when absent)."""
+    from .._srchash import source_hash
+
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_mi355x_build_flags", Path(__file__).resolve().parents[2] / "build.py")
+    if spec is None or not Path(spec.origin).exists():
+        return None
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return source_hash(mod._hash_flags())
 
 
 def lib() -> ctypes.CDLL:

@@ -1107,6 +1107,22 @@ def fast_aten_cat(tensors, dim=0):
     dtype = ts_nonempty[0]._dtype
     for x in ts_nonempty[1:]:
         dtype = torch.promote_types(dtype, x._dtype)
+    # torch.cat's own checks (a __torch_dispatch__ subclass gets no meta
+    # shape check first): same rank, same size in every dim but d
+    for i, x in enumerate(ts):
+        if len(x._shape) == 1 and x._shape[0] == 0:
+            continue  # torch.cat skips legacy empty 1-D pieces
+        if len(x._shape) != nd:
+            raise RuntimeError(
+                f"Tensors must have same number of dimensions: got {nd} and {len(x._shape)}"
+            )
+        for j in range(nd):
+            if j != d and x._shape[j] != ref._shape[j]:
+                raise RuntimeError(
+                    f"Sizes of tensors must match except in dimension {d}. Expected size"
+                    f" {ref._shape[j]} but got size {x._shape[j]} for tensor number {i}"
+                    " in the list."
+                )
     shape = list(ref._shape)
     shape[d] = sum(x._shape[d] for x in ts_nonempty)
     out = _alloc(shape, dtype, ref._device)
@@ -1114,8 +1130,9 @@ def fast_aten_cat(tensors, dim=0):
             and all(x._dtype == dtype and x._is_contiguous for x in ts_nonempty)):
         # Many pieces that are whole contiguous chunks of the output (e.g.
         # clip_grad_norm_'s stack of per-parameter norms): one multi-tensor
-        # launch instead of one copy per piece.  chunk_i = -0.0 + 1 * x_i is
-        # exact for every x_i, signed zeros and NaNs included.
+        # launch instead of one copy per piece.  chunk_i = -0.0 + 1 * x_i
+        # equals x_i for every finite or infinite x_i and for signed zeros; a
+        # NaN stays NaN (a signalling NaN comes out quieted).
         fill_(out, -0.0)
         ptrs, off = [], 0
         for x in ts_nonempty:
@@ -2201,7 +2218,15 @@ def fast_aten__fused_adamw_(
             return NOT_HANDLED
         d = descs[i]
         d.param, d.grad, d.exp_avg, d.exp_avg_sq = p._ptr, g._ptr, m._ptr, v._ptr
-        d.max_exp_avg_sq = _require(max_exp_avg_sqs[i])._ptr if amsgrad else None
+        if amsgrad:
+            mx = _require(max_exp_avg_sqs[i])
+            if mx._dtype != f32 or not mx._is_contiguous:
+                return NOT_HANDLED
+            if mx._numel != pn:
+                raise RuntimeError(f"_fused_adamw_: max_exp_avg_sq {i} has {mx._numel} elements, param has {pn}")
+            d.max_exp_avg_sq = mx._ptr
+        else:
+            d.max_exp_avg_sq = None
         d.step = s._ptr
         d.numel = pn
     lr_t = _t(lr)

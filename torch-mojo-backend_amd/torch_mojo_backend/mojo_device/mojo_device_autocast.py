@@ -11,94 +11,95 @@ through.  Casts are ordinary ``_to_copy`` ops on the device, except for
 from __future__ import annotations
 
 import functools
-from collections.abc import Mapping
 
 import torch
+from torch.utils._pytree import tree_map
 
-_registered = False
-_fallback_library = None
-_aten_library = None
+_EXCLUDE_AUTOCAST = torch._C.DispatchKeySet(torch._C.DispatchKey.AutocastPrivateUse1)
 
-_AUTOCAST_KEYSET = torch._C.DispatchKeySet(torch._C.DispatchKey.AutocastPrivateUse1)
-
-
-def _cast_mojo_floating(value, dtype):
-    if isinstance(value, torch.Tensor):
-        if (
-            value.device.type == "mojo"
-            and value.is_floating_point()
-            and value.dtype != torch.float64
-            and value.dtype != dtype
-        ):
-            return value.to(dtype=dtype)
-        return value
-    if isinstance(value, tuple):
-        return tuple(_cast_mojo_floating(v, dtype) for v in value)
-    if isinstance(value, list):
-        return [_cast_mojo_floating(v, dtype) for v in value]
-    if isinstance(value, Mapping):
-        return {k: _cast_mojo_floating(v, dtype) for k, v in value.items()}
-    return value
+# Policy table (the drop-in contract): "low" runs the op in the active
+# autocast dtype, "f32" in float32; unlisted ops fall through unchanged.
+_POLICY = {
+    "low": ("addmm", "bmm", "matmul", "mm", "scaled_dot_product_attention",
+            "_scaled_dot_product_flash_attention"),
+    "f32": ("layer_norm", "native_layer_norm", "nll_loss", "nll_loss_forward"),
+}
+# f32 ops whose kernels also write the autocast-dtype copy of their output
+_WRITES_LOW_COPY = frozenset({"layer_norm", "native_layer_norm"})
 
 
-def _policy_wrapper(op, dtype_getter, mark_low=False):
-    """Run op with its floating mojo arguments cast to dtype_getter().  With
-    mark_low (the f32 layer norms) the op also learns the autocast dtype, so
-    its kernel can write the lower-precision copy of its output that the
-    next autocast matmul casts to."""
+def _autocast_dtype():
+    return torch.get_autocast_dtype("mojo")
+
+
+def _retype(dtype):
+    """Leaf function for tree_map: a floating mojo tensor below float64 that
+    is not already `dtype` becomes a `dtype` copy; everything else passes."""
+    def leaf(x):
+        if (isinstance(x, torch.Tensor) and x.device.type == "mojo" and x.dtype != dtype
+                and x.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+            return x.to(dtype)
+        return x
+
+    return leaf
+
+
+def _under_policy(op, target, low_copy=False):
+    """op's AutocastPrivateUse1 kernel: retype the floating mojo arguments to
+    target() and call op below the autocast key.  low_copy (the f32 layer
+    norms) also tells the kernel the autocast dtype, so it writes the
+    lower-precision copy of its output that the next autocast matmul would
+    otherwise cast."""
     @functools.wraps(op)
-    def wrapper(*args, **kwargs):
-        with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYSET):
-            dtype = dtype_getter()
-            cargs, ckwargs = _cast_mojo_floating(args, dtype), _cast_mojo_floating(kwargs, dtype)
-            if mark_low:
-                from ..eager_kernels import aten_fast
+    def kernel(*args, **kwargs):
+        with torch._C._ExcludeDispatchKeyGuard(_EXCLUDE_AUTOCAST):
+            args, kwargs = tree_map(_retype(target()), (args, kwargs))
+            if not low_copy:
+                return op(*args, **kwargs)
+            from ..eager_kernels import aten_fast
 
-                with aten_fast.autocast_low_scope(torch.get_autocast_dtype("mojo")):
-                    return op(*cargs, **ckwargs)
-            return op(*cargs, **ckwargs)
+            with aten_fast.autocast_low_scope(_autocast_dtype()):
+                return op(*args, **kwargs)
 
-    return wrapper
+    return kernel
+
+
+class _AutocastRegistry:
+    """Owns the torch.library handles (they unregister when collected)."""
+
+    def __init__(self) -> None:
+        self.libs: list = []
+
+    def install(self) -> None:
+        fall = torch.library.Library("_", "IMPL", "AutocastPrivateUse1")
+        fall.fallback(torch.library.fallthrough_kernel)
+        aten = torch.library.Library("aten", "IMPL", "AutocastPrivateUse1")
+        targets = {"low": _autocast_dtype, "f32": lambda: torch.float32}
+        for kind, names in _POLICY.items():
+            for name in names:
+                op = getattr(torch.ops.aten, name).default
+                aten.impl(name, _under_policy(op, targets[kind], low_copy=name in _WRITES_LOW_COPY))
+        aten.impl("linear", _linear_autocast)
+        self.libs = [fall, aten]
+
+
+_registry: _AutocastRegistry | None = None
 
 
 def register_autocast_ops() -> None:
-    global _registered, _fallback_library, _aten_library
-    if _registered:
-        return
-    _fallback_library = torch.library.Library("_", "IMPL", "AutocastPrivateUse1")
-    _fallback_library.fallback(torch.library.fallthrough_kernel)
-    _aten_library = torch.library.Library("aten", "IMPL", "AutocastPrivateUse1")
-    lower = (
-        torch.ops.aten.addmm.default,
-        torch.ops.aten.bmm.default,
-        torch.ops.aten.matmul.default,
-        torch.ops.aten.mm.default,
-        torch.ops.aten.scaled_dot_product_attention.default,
-        torch.ops.aten._scaled_dot_product_flash_attention.default,
-    )
-    fp32 = (
-        torch.ops.aten.layer_norm.default,
-        torch.ops.aten.native_layer_norm.default,
-        torch.ops.aten.nll_loss.default,
-        torch.ops.aten.nll_loss_forward.default,
-    )
-    for op in lower:
-        _aten_library.impl(
-            op._schema.name, _policy_wrapper(op, lambda: torch.get_autocast_dtype("mojo"))
-        )
-    for op in fp32:
-        norm = "layer_norm" in op._schema.name
-        _aten_library.impl(op._schema.name, _policy_wrapper(op, lambda: torch.float32, mark_low=norm))
-    _aten_library.impl("linear", _linear_autocast)
-    _registered = True
+    global _registry
+    if _registry is None:
+        reg = _AutocastRegistry()
+        reg.install()
+        _registry = reg
 
 
 def _linear_autocast(input, weight, bias=None):
     from .mojo_device_autograd import fused_linear, fused_linear_inputs
 
-    with torch._C._ExcludeDispatchKeyGuard(_AUTOCAST_KEYSET):
-        dt = torch.get_autocast_dtype("mojo")
+    with torch._C._ExcludeDispatchKeyGuard(_EXCLUDE_AUTOCAST):
+        dt = _autocast_dtype()
         if fused_linear_inputs(input, weight, bias, dt):
             return fused_linear(input, weight, bias, dt)
-        args = _cast_mojo_floating((input, weight, bias), dt)
-        return torch.ops.aten.linear.default(*args)
+        input, weight, bias = tree_map(_retype(dt), (input, weight, bias))
+        return torch.ops.aten.linear.default(input, weight, bias)

@@ -10,6 +10,7 @@ of time and issued directly).
 
 from __future__ import annotations
 
+import struct
 import threading
 
 import torch
@@ -17,11 +18,6 @@ import torch
 from . import torch_mojo_tensor as _tensor_mod
 
 _current_device = 0
-_UINT64_MASK = (1 << 64) - 1
-_DEFAULT_RNG_SEED = 67_280_421_310_721
-_rng_default_seed = _DEFAULT_RNG_SEED
-_rng_states: dict[int, tuple[int, int]] = {}
-_rng_lock = threading.Lock()
 
 
 def _is_in_bad_fork():
@@ -103,21 +99,61 @@ def synchronize(device=None) -> None:
         torch.cuda.synchronize(idx)
 
 
-def _normalize_rng_seed(seed) -> int:
-    value = int(seed)
-    if value < -(1 << 63) or value > _UINT64_MASK:
-        raise ValueError("Overflow when unpacking long long")
-    return value & _UINT64_MASK
+class _Generator:
+    """One device's RNG state: a 64-bit seed and a 64-bit offset counter,
+    serialised as 16 little-endian bytes (seed, then counter) -- the state
+    format of the reference's device module, so saved states interchange."""
+
+    __slots__ = ("seed", "offset")
+    _FMT = struct.Struct("<QQ")
+
+    def __init__(self, seed: int, offset: int = 0) -> None:
+        self.seed, self.offset = seed, offset
+
+    def to_tensor(self) -> torch.Tensor:
+        raw = self._FMT.pack(self.seed, self.offset)
+        return torch.frombuffer(bytearray(raw), dtype=torch.uint8).clone()
+
+    @classmethod
+    def from_tensor(cls, t: torch.Tensor) -> "_Generator":
+        raw = t.detach().to("cpu").contiguous().view(-1)
+        if raw.dtype != torch.uint8 or raw.numel() != cls._FMT.size:
+            raise ValueError(f"a mojo RNG state is {cls._FMT.size} uint8 values, got {raw.numel()} of {raw.dtype}")
+        return cls(*cls._FMT.unpack(raw.numpy().tobytes()))
+
+
+# Default seed of a device nobody seeded (the reference's value, so the
+# initial states agree).
+_DEFAULT_SEED = 67_280_421_310_721
+_generators: dict[int, _Generator] = {}
+_seed_for_new = _DEFAULT_SEED
+_gen_lock = threading.Lock()
+
+
+def _as_u64(seed) -> int:
+    """A seed as torch.manual_seed takes it: any int in [-2^63, 2^64), kept
+    modulo 2^64."""
+    v = int(seed)
+    if not -(1 << 63) <= v < (1 << 64):
+        raise ValueError(f"seed {v} does not fit in 64 bits")
+    return v % (1 << 64)
+
+
+def _generator(index: int) -> _Generator:
+    g = _generators.get(index)
+    if g is None:
+        g = _generators[index] = _Generator(_seed_for_new)
+    return g
 
 
 def manual_seed_all(seed) -> None:
-    global _rng_default_seed
-    normalized = _normalize_rng_seed(seed)
-    with _rng_lock:
-        _rng_default_seed = normalized
-        _rng_states.clear()
-        for index in range(max(device_count(), 1)):
-            _rng_states[index] = (normalized, 0)
+    global _seed_for_new
+    v = _as_u64(seed)
+    with _gen_lock:
+        _seed_for_new = v
+        _generators.clear()
+        for i in range(max(device_count(), 1)):
+            _generators[i] = _Generator(v)
 
 
 def manual_seed(seed) -> None:
@@ -125,26 +161,16 @@ def manual_seed(seed) -> None:
 
 
 def get_rng_state(device=None) -> torch.Tensor:
-    index = _index_of(device)
-    with _rng_lock:
-        seed, counter = _rng_states.setdefault(index, (_rng_default_seed, 0))
-    encoded = seed.to_bytes(8, "little") + counter.to_bytes(8, "little")
-    return torch.tensor(list(encoded), dtype=torch.uint8)
+    with _gen_lock:
+        return _generator(_index_of(device)).to_tensor()
 
 
 def set_rng_state(new_state, device=None) -> None:
     if not isinstance(new_state, torch.Tensor):
-        raise TypeError("Mojo RNG state must be a torch.Tensor")
-    state = new_state.detach().cpu().contiguous()
-    if state.dtype != torch.uint8 or state.numel() != 16:
-        raise ValueError("Mojo RNG state must be a 16-element uint8 tensor")
-    encoded = bytes(state.reshape(-1).tolist())
-    index = _index_of(device)
-    with _rng_lock:
-        _rng_states[index] = (
-            int.from_bytes(encoded[:8], "little"),
-            int.from_bytes(encoded[8:], "little"),
-        )
+        raise TypeError(f"set_rng_state expects a torch.Tensor, got {type(new_state).__name__}")
+    g = _Generator.from_tensor(new_state)
+    with _gen_lock:
+        _generators[_index_of(device)] = g
 
 
 def get_amp_supported_dtype():
