@@ -494,6 +494,21 @@ int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk,
                     int64_t heads, int64_t sq, int64_t skv, int64_t d,
                     double scale, int causal, int dtype, void* workspace,
                     int64_t ws_bytes, mi355x_stream_t stream);
+/* mi355x_attn_bwd without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The row terms live in a fixed 32 MiB device array per GPU,
+ * which limits batch * heads * sq to 4,194,272 query rows (larger shapes
+ * return MI355X_EINVAL).  Every call on one GPU shares that array: calls
+ * that overlap on one GPU (different streams or threads) race. */
+int mi355x_attn_bwd_noalloc(void* dq, const int64_t* dq_bhs, void* dk,
+                            const int64_t* dk_bhs, void* dv, const int64_t* dv_bhs,
+                            const void* dout, const int64_t* do_bhs, const void* q,
+                            const int64_t* q_bhs, const void* k, const int64_t* k_bhs,
+                            const void* v, const int64_t* v_bhs, const void* o,
+                            const int64_t* o_bhs, const float* lse, int64_t batch,
+                            int64_t heads, int64_t sq, int64_t skv, int64_t d,
+                            double scale, int causal, int dtype, mi355x_stream_t stream);
 
 #ifdef __cplusplus
 }

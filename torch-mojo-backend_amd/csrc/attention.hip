@@ -28,6 +28,8 @@
 //          blocks, recomputing S^T and dP^T, and accumulates dQ^T = K^T dS^T.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "mfma.h"
 
@@ -1373,6 +1375,41 @@ extern "C" int64_t mi355x_attn_bwd_workspace_bytes(int64_t batch, int64_t heads,
   return 2 * batch * heads * sq * (int64_t)sizeof(float) + 256;
 }
 
+// Scratch of mi355x_attn_bwd_noalloc: the row terms D and LSE*log2(e)
+// (2 floats per query row) in a file-scope device array, so that entry
+// point needs no workspace and calls no allocator.  Each GPU the library
+// runs on holds its own copy for the life of the process; host code reaches
+// it only through the address hipGetSymbolAddress returns for the current
+// device (the array's name is a host-side stand-in, not a device address).
+constexpr int64_t kAttnScratchBytes = 32ll << 20;  // 32 MiB: up to 4M query rows (B*H*Sq)
+static __device__ __align__(256) char scratch[kAttnScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// This device's address of `scratch` (looked up once per device, with that
+// device current); nullptr with the error recorded on failure.
+void* scratch_for_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("mi355x_attn_bwd_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? ptr : nullptr;
+  });
+  if (!g_scratch_ptr[dev])
+    set_error("mi355x_attn_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+              hipGetErrorString(g_scratch_err[dev]));
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
 extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs,
                                void* dv, const int64_t* dv_bhs, const void* dout,
                                const int64_t* do_bhs, const void* q, const int64_t* q_bhs,
@@ -1402,4 +1439,30 @@ extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const 
   a.delta = (float*)workspace;
   a.lse2 = a.delta + batch * heads * sq;
   MI_ATTN_DISPATCH(dtype, d, bwd_launch, a, (hipStream_t)stream);
+}
+
+extern "C" int mi355x_attn_bwd_noalloc(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs,
+                                       void* dv, const int64_t* dv_bhs, const void* dout,
+                                       const int64_t* do_bhs, const void* q, const int64_t* q_bhs,
+                                       const void* k, const int64_t* k_bhs, const void* v,
+                                       const int64_t* v_bhs, const void* o, const int64_t* o_bhs,
+                                       const float* lse, int64_t batch, int64_t heads, int64_t sq,
+                                       int64_t skv, int64_t d, double scale, int causal, int dtype,
+                                       mi355x_stream_t stream) {
+  if (batch <= 0 || heads <= 0 || sq <= 0)
+    return fail(MI355X_EINVAL, "mi355x_attn_bwd_noalloc: bad shape");
+  const int64_t need = mi355x_attn_bwd_workspace_bytes(batch, heads, sq, skv, d);
+  if (need > kAttnScratchBytes)
+    return fail(MI355X_EINVAL,
+                "mi355x_attn_bwd_noalloc: %lld query rows need %lld bytes of scratch, more than its %lld "
+                "(at most %lld rows); use mi355x_attn_bwd with a workspace",
+                (long long)(batch * heads * sq), (long long)need, (long long)kAttnScratchBytes,
+                (long long)((kAttnScratchBytes - 256) / 8));
+  void* ws = scratch_for_current_device();
+  if (!ws) return MI355X_ELAUNCH;
+  // every scratch word the kernels read is written first by attn_bwd_delta
+  // in the same call, so nothing is cleared
+  return mi355x_attn_bwd(dq, dq_bhs, dk, dk_bhs, dv, dv_bhs, dout, do_bhs, q, q_bhs, k, k_bhs, v, v_bhs, o,
+                         o_bhs, lse, batch, heads, sq, skv, d, scale, causal, dtype, ws, kAttnScratchBytes,
+                         stream);
 }
