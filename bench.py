@@ -98,6 +98,13 @@ def bench_model(args):
     dt = time.perf_counter() - t0
     vals = [float(l.item()) for l in losses]
     tokens = args.batch * args.block * args.steps
+    # per-step relative deviation from the f32 CPU curve of the same run
+    # (tests/golden fixture; only at the fixture's batch and block size)
+    dev = None
+    fx_path = ROOT / "tests" / "golden" / "loss_curve_b16_t1024_f32cpu.json"
+    if fx_path.exists() and args.batch == 16 and args.block == 1024:
+        ref = json.loads(fx_path.read_text())["losses"]
+        dev = [abs(a - b) / abs(b) for a, b in zip(vals, ref)]
     return {
         "tokens_per_s": tokens / dt,
         "ms_per_step": 1000.0 * dt / args.steps,
@@ -105,6 +112,8 @@ def bench_model(args):
         "loss_first": vals[0],
         "loss_last": vals[-1],
         "losses": [round(v, 5) for v in vals],
+        "loss_rel_dev_vs_f32cpu": [round(v, 5) for v in dev] if dev else None,
+        "loss_max_rel_dev_vs_f32cpu": round(max(dev), 5) if dev else None,
     }
 
 

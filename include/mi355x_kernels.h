@@ -494,6 +494,30 @@ int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk,
                     int64_t heads, int64_t sq, int64_t skv, int64_t d,
                     double scale, int causal, int dtype, void* workspace,
                     int64_t ws_bytes, mi355x_stream_t stream);
+/* ---- attention for the inputs the MFMA kernels do not take (the rest of
+ *      _fused_fa_inputs' gate, aten_fast.py:7462-7530: f32 and any head_dim
+ *      up to 256; the reference runs these through its scalar kernels,
+ *      flash_attention_bwd_kernels.mojo:215-310) ----------------------
+ * f32 math; q/k/v/o/dout/grads need only a unit head_dim stride.  Grouped
+ * K/V heads and the causal sliding window as in mi355x_attn_fwd_ex; the
+ * backward's dK/dV of a K/V head sum over its query heads (the backward of
+ * grouped or windowed attention, which the reference leaves to its
+ * masked-math decomposition, aten_fast.py:9112-9123). */
+int mi355x_attn_fwd_gen(void* o, const int64_t* o_bhs, float* lse, const void* q,
+                        const int64_t* q_bhs, const void* k, const int64_t* k_bhs,
+                        const void* v, const int64_t* v_bhs, int64_t batch, int64_t heads,
+                        int64_t kv_heads, int64_t sq, int64_t skv, int64_t d, double scale,
+                        int causal, int64_t window, int dtype, mi355x_stream_t stream);
+int64_t mi355x_attn_bwd_gen_workspace_bytes(int64_t batch, int64_t heads, int64_t sq);
+int mi355x_attn_bwd_gen(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs,
+                        void* dv, const int64_t* dv_bhs, const void* dout,
+                        const int64_t* do_bhs, const void* q, const int64_t* q_bhs,
+                        const void* k, const int64_t* k_bhs, const void* v,
+                        const int64_t* v_bhs, const void* o, const int64_t* o_bhs,
+                        const float* lse, int64_t batch, int64_t heads, int64_t kv_heads,
+                        int64_t sq, int64_t skv, int64_t d, double scale, int causal,
+                        int64_t window, int dtype, void* workspace, int64_t ws_bytes,
+                        mi355x_stream_t stream);
 /* mi355x_attn_bwd without a workspace argument and without any allocation.
  * No counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid

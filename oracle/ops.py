@@ -204,19 +204,28 @@ def sdpa_forward(q, k, v, scale=None, causal=False, window=0):
     return np.einsum("...ij,...jd->...id", p, _kv_heads(q, v)), lse
 
 
-def sdpa_backward(do, q, k, v, o, lse, scale=None, causal=False):
-    """(dQ, dK, dV) recomputing P from LSE and D_i = sum(dO*O)."""
+def sdpa_backward(do, q, k, v, o, lse, scale=None, causal=False, window=0):
+    """(dQ, dK, dV) recomputing P from LSE and D_i = sum(dO*O).  With grouped
+    K/V heads (K/V with H/g heads), dK and dV of K/V head h sum the
+    contributions of query heads h*g .. h*g+g-1; `window` as in
+    sdpa_forward."""
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d) if scale is None else scale
-    s = _scores(q, k, scale, causal)
+    s = _scores(q, k, scale, causal, window)
     p = np.exp(s - _f64(lse)[..., None])
     do, o = _f64(do), _f64(o)
+    kk, vv = _kv_heads(q, k), _kv_heads(q, v)
     dv = np.einsum("...ij,...id->...jd", p, do)
-    dp = np.einsum("...id,...jd->...ij", do, _f64(v))
+    dp = np.einsum("...id,...jd->...ij", do, vv)
     delta = (do * o).sum(-1, keepdims=True)
     ds = p * (dp - delta)
-    dq = scale * np.einsum("...ij,...jd->...id", ds, _f64(k))
+    dq = scale * np.einsum("...ij,...jd->...id", ds, kk)
     dk = scale * np.einsum("...ij,...id->...jd", ds, _f64(q))
+    hk = np.asarray(k).shape[-3]
+    if hk != q.shape[-3]:  # fold the query heads of each group onto their K/V head
+        g = q.shape[-3] // hk
+        dk = dk.reshape(dk.shape[:-3] + (hk, g) + dk.shape[-2:]).sum(-3)
+        dv = dv.reshape(dv.shape[:-3] + (hk, g) + dv.shape[-2:]).sum(-3)
     return dq, dk, dv
 
 

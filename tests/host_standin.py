@@ -573,6 +573,43 @@ class HostStandIn:
         dense(_val(lse), torch.float32, (B, H, Sq)).copy_(L)
         return 0
 
+    def mi355x_attn_fwd_gen(self, o, obhs, lse, q, qbhs, k, kbhs, v, vbhs, B, H, Hk, Sq, Skv, D, scale, causal,
+                            window, dt, stream):
+        return self.mi355x_attn_fwd_ex(o, obhs, lse, q, qbhs, k, kbhs, v, vbhs, B, H, Hk, Sq, Skv, D, scale,
+                                       causal, window, dt, stream)
+
+    def mi355x_attn_bwd_gen_workspace_bytes(self, B, H, Sq):
+        return 16
+
+    def mi355x_attn_bwd_gen(self, dq, dqs, dk, dks, dv, dvs, do, dos, q, qs, k, ks, v, vs, o, os_, lse,
+                            B, H, Hk, Sq, Skv, D, scale, causal, window, dt, ws, wsb, stream):
+        def t(p, st, h, s):
+            return view(_val(p), DT[dt], (B, h, s, D), (st[0], st[1], st[2], 1))
+
+        g = H // Hk
+        Q = t(q, qs, H, Sq).float()
+        K = t(k, ks, Hk, Skv).float().repeat_interleave(g, dim=1)
+        V = t(v, vs, Hk, Skv).float().repeat_interleave(g, dim=1)
+        O, DO = t(o, os_, H, Sq).float(), t(do, dos, H, Sq).float()
+        L = dense(_val(lse), torch.float32, (B, H, Sq))
+        S = Q @ K.transpose(-1, -2) * scale
+        if causal:
+            i = torch.arange(Sq)[:, None]
+            j = torch.arange(Skv)[None, :]
+            keep = j <= i
+            if window:
+                keep = keep & (i - j < window)
+            S = S.masked_fill(~keep, float("-inf"))
+        P = torch.exp(S - L[..., None])
+        Dr = (DO * O).sum(-1, keepdim=True)
+        dS = P * (DO @ V.transpose(-1, -2) - Dr)
+        t(dq, dqs, H, Sq).copy_(dS @ K * scale)
+        dK = (dS.transpose(-1, -2) @ Q * scale).view(B, Hk, g, Skv, D).sum(2)
+        dV = (P.transpose(-1, -2) @ DO).view(B, Hk, g, Skv, D).sum(2)
+        t(dk, dks, Hk, Skv).copy_(dK)
+        t(dv, dvs, Hk, Skv).copy_(dV)
+        return 0
+
     def mi355x_attn_bwd_workspace_bytes(self, B, H, Sq, Skv, D):
         return 16
 

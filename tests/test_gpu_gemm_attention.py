@@ -324,3 +324,56 @@ def test_attention_fwd_ex_rejects_bad_arguments(kernels):
     rc = lib().mi355x_attn_fwd_ex(p(o), bhs(o), p(lse), p(q), bhs(q), p(q), bhs(q), p(q), bhs(q),
                                   1, 3, 3, 64, 64, 64, 0.125, 0, 16, CODE[torch.bfloat16], None)
     assert rc != 0 and b"needs causal" in lib().mi355x_last_error()
+
+
+# ---------------------------------------------------------------------------
+# f32 kernels: f32 inputs, any head_dim up to 256, grouped / windowed backward
+# ---------------------------------------------------------------------------
+def _attn_gen(q, k, v, do, causal, window, scale=None):
+    B, H, Sq, D = q.shape
+    Hk, Skv = k.shape[1], k.shape[2]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    dt = CODE[q.dtype]
+    o = torch.empty(B, Sq, H, D, dtype=q.dtype, device="cuda").transpose(1, 2)
+    lse = torch.empty(B, H, Sq, device="cuda")
+    call("mi355x_attn_fwd_gen", p(o), bhs(o), p(lse), p(q), bhs(q), p(k), bhs(k), p(v), bhs(v),
+         B, H, Hk, Sq, Skv, D, scale, int(causal), window, dt, None)
+    dq = torch.empty(B, Sq, H, D, dtype=q.dtype, device="cuda").transpose(1, 2)
+    dk = torch.empty(B, Skv, Hk, D, dtype=q.dtype, device="cuda").transpose(1, 2)
+    dv = torch.empty(B, Skv, Hk, D, dtype=q.dtype, device="cuda").transpose(1, 2)
+    ws_n = lib().mi355x_attn_bwd_gen_workspace_bytes(B, H, Sq)
+    ws = workspace(ws_n)
+    call("mi355x_attn_bwd_gen", p(dq), bhs(dq), p(dk), bhs(dk), p(dv), bhs(dv), p(do), bhs(do),
+         p(q), bhs(q), p(k), bhs(k), p(v), bhs(v), p(o), bhs(o), p(lse),
+         B, H, Hk, Sq, Skv, D, scale, int(causal), window, dt, p(ws), ws_n, None)
+    return o, lse, dq, dk, dv
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 3, 3, 70, 70, 40), (1, 2, 2, 33, 90, 64), (1, 4, 2, 100, 100, 96),
+                                   (1, 4, 1, 64, 64, 200), (2, 2, 2, 50, 50, 256), (1, 1, 1, 1, 1, 8)])
+@pytest.mark.parametrize("mode", ["full", "causal", "window"])
+def test_attention_f32_kernels_match_oracle(kernels, dtype, shape, mode):
+    """mi355x_attn_fwd_gen / mi355x_attn_bwd_gen (f32 math) against the f64
+    oracle: f32 and bf16 inputs, head_dims the MFMA path does not take
+    (40, 96, 200, 256), Sq != Skv, grouped K/V heads (dK/dV summed over each
+    group) and a causal sliding window."""
+    B, H, Hk, Sq, Skv, D = shape
+    causal = mode != "full"
+    window = 17 if mode == "window" else 0
+    if window and Sq != Skv:
+        pytest.skip("windows are defined for Sq == Skv")
+    g = torch.Generator().manual_seed(hash((shape, mode)) % 1000)
+    q, do = (torch.randn(B, H, Sq, D, generator=g).to(dtype) for _ in range(2))
+    k, v = (torch.randn(B, Hk, Skv, D, generator=g).to(dtype) for _ in range(2))
+    o, lse, dq, dk, dv = _attn_gen(dev(q), dev(k), dev(v), dev(do), causal, window)
+    n = lambda t: t.double().numpy()  # noqa: E731
+    eo, el = O.sdpa_forward(n(q), n(k), n(v), causal=causal, window=window)
+    tol = dict(atol=1e-4, rtol=1e-4) if dtype == torch.float32 else dict(atol=2e-2, rtol=2e-2)
+    tol_close(np64(o), eo, what="O", **tol)
+    tol_close(np64(lse), el, atol=1e-4, rtol=1e-4, what="LSE")
+    edq, edk, edv = O.sdpa_backward(n(do), n(q), n(k), n(v), np64(o), np64(lse), causal=causal, window=window)
+    gtol = dict(atol=2e-4, rtol=2e-4) if dtype == torch.float32 else dict(atol=3e-2, rtol=2e-2)
+    tol_close(np64(dv), edv, what="dV", **gtol)
+    tol_close(np64(dk), edk, what="dK", **gtol)
+    tol_close(np64(dq), edq, what="dQ", **gtol)

@@ -116,24 +116,35 @@ def test_nanogpt_loss_curve_f32_matches_cpu_fixture(mojo):
 
 
 def test_nanogpt_loss_curve_bf16_autocast_tracks_cpu_fixture(mojo):
-    """bf16 autocast: within 0.1% relative of the f32 curve on every step
-    before the run's first loss spike (steps 0-4), and within 5% on every
-    one of the 50 steps (no divergence, no NaN).
+    """bf16 autocast on the device against the f32 CPU curve, bounded by what
+    bf16 rounding does to this run in stock PyTorch.
 
-    From the spike at step 5 on, this 2-batch memorisation run amplifies
-    rounding noise: with the initial weights scaled by (1 + 1e-6 N(0,1))
-    under six seeds, stock torch-ROCm bf16 autocast lands up to 3.4% from
-    the f32 curve and the device up to 4.6%, in either direction; which
-    realisation a run follows depends on last-bit differences (summation
-    order, exp rounding), so a tighter per-step bound there would test the
-    seed.  Kernel parity is pinned by the f32 curve test above and by the
-    per-op parity tests; the device's per-parameter gradient error against
-    f32 equals torch's bf16 error at init and at step 7."""
+    tests/golden/loss_envelope_b16_t1024_bf16_torch.json holds stock
+    PyTorch-ROCm bf16-autocast curves of the same run (as is, and with the
+    initial weights scaled by 1 + 1e-6 N(0,1) under twelve seeds;
+    tests/golden/make_bf16_envelope.py).  On every step the device's loss
+    must lie within 1% (of the f32 loss) of that envelope joined with the
+    f32 loss: stock torch stays within 0.1% of f32 for the first ~30 steps,
+    where this is a 1% bound around the f32 curve, and spreads to about 4%
+    by step 48 as the two-batch memorisation run amplifies rounding noise
+    (one more realisation of that noise may land just outside a sampled
+    envelope, hence the 1% margin there too).  Before the run's first loss spike (steps
+    0-4) the device must also be within 0.1%."""
+    import json
+    from pathlib import Path
+
+    env = json.loads((Path(__file__).parent / "golden" / "loss_envelope_b16_t1024_bf16_torch.json").read_text())
     got, ref = _loss_curve(amp=True)
-    rel = [abs(a - b) / abs(b) for a, b in zip(got, ref)]
     assert all(math.isfinite(v) for v in got)
+    rel = [abs(a - b) / abs(b) for a, b in zip(got, ref)]
     assert max(rel[:5]) <= 1e-3, max(enumerate(rel[:5]), key=lambda t: t[1])
-    assert max(rel) <= 5e-2, max(enumerate(rel), key=lambda t: t[1])
+    bad = []
+    for i, (g, f, lo, hi) in enumerate(zip(got, ref, env["lo"], env["hi"])):
+        if not (min(lo, f) - 0.01 * f <= g <= max(hi, f) + 0.01 * f):
+            bad.append((i, round(g, 4), round(f, 4), round(lo, 4), round(hi, 4)))
+    print("bf16 device vs f32: max rel %.4f at step %d; per-step rel: %s"
+          % (max(rel), rel.index(max(rel)), [round(r, 4) for r in rel]))
+    assert not bad, f"steps more than 1% outside the stock-torch bf16 envelope (step, dev, f32, lo, hi): {bad}"
 
 
 @pytest.mark.parametrize("shape,bias,strided", [((96, 200), True, False), ((3, 70, 200), True, False),
@@ -204,3 +215,56 @@ def test_stack_and_cat_of_many_pieces_are_bit_exact(mojo, dtype, bits):
     rows[3][2] = -0.0
     got = torch.cat([r.to("mojo") for r in rows]).cpu()
     assert torch.equal(got.view(bits), torch.cat(rows).view(bits))
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.float32, 64), (torch.bfloat16, 256), (torch.float32, 80)])
+def test_sdpa_autograd_f32_and_wide_heads_use_the_flash_pair(mojo, dtype, d):
+    """f32 inputs and head_dims beyond the MFMA backward's (the fused gate
+    takes f32 and head_dim up to 256, aten_fast.py:7462-7530) go through the
+    flash pair, not the decomposition, and match torch CPU autograd."""
+    g = torch.Generator().manual_seed(d)
+    q, k, v = (torch.randn(2, 3, 77, d, generator=g).to(dtype) for _ in range(3))
+    qm, km, vm = (t.to("mojo").requires_grad_() for t in (q, k, v))
+    out = F.scaled_dot_product_attention(qm, km, vm, is_causal=True)
+    assert type(out.grad_fn).__name__ == "ScaledDotProductFlashAttentionBackward0"
+    dout = torch.randn(out.shape, generator=g).to(dtype)
+    out.backward(dout.to("mojo"))
+    qc, kc, vc = (t.double().requires_grad_() for t in (q, k, v))
+    ref = F.scaled_dot_product_attention(qc, kc, vc, is_causal=True)
+    ref.backward(dout.double())
+    tol = 1e-4 if dtype == torch.float32 else 3e-2
+    assert torch.allclose(out.detach().double().cpu(), ref.detach(), atol=tol, rtol=tol)
+    for a, b in ((qm, qc), (km, kc), (vm, vc)):
+        assert torch.allclose(a.grad.double().cpu(), b.grad, atol=2 * tol, rtol=2 * tol)
+
+
+@pytest.mark.parametrize("window", [0, 40])
+def test_gqa_window_attention_backward_is_fused(mojo, window):
+    """Gemma-3-shaped attention under autograd (4 query heads on 1 K/V head,
+    head_dim 256, sliding window from torch_mojo_backend.masks): the fused
+    backward (dK/dV summed over the group) matches torch CPU autograd of the
+    same masked SDPA."""
+    from torch_mojo_backend.masks import sliding_window_causal_mask
+
+    g = torch.Generator().manual_seed(window + 1)
+    T = 150
+    q = torch.randn(1, 4, T, 256, generator=g).bfloat16()
+    k, v = (torch.randn(1, 1, T, 256, generator=g).bfloat16() for _ in range(2))
+    qm, km, vm = (t.to("mojo").requires_grad_() for t in (q, k, v))
+    if window:
+        mask = sliding_window_causal_mask(T, window, device="mojo")
+        out = F.scaled_dot_product_attention(qm, km, vm, attn_mask=mask, enable_gqa=True)
+    else:
+        out = F.scaled_dot_product_attention(qm, km, vm, is_causal=True, enable_gqa=True)
+    assert type(out.grad_fn).__name__ == "_FusedAttentionBackward"
+    dout = torch.randn(out.shape, generator=g).bfloat16()
+    out.backward(dout.to("mojo"))
+    qc, kc, vc = (t.double().requires_grad_() for t in (q, k, v))
+    i, j = torch.arange(T)[:, None], torch.arange(T)[None, :]
+    keep = (j <= i) & ((i - j < window) if window else True)
+    ref = F.scaled_dot_product_attention(qc, kc, vc, attn_mask=keep, enable_gqa=True)
+    ref.backward(dout.double())
+    assert torch.allclose(out.detach().double().cpu(), ref.detach(), atol=3e-2, rtol=3e-2)
+    for a, b in ((qm, qc), (km, kc), (vm, vc)):
+        assert a.grad.shape == b.grad.shape
+        assert torch.allclose(a.grad.double().cpu(), b.grad, atol=6e-2, rtol=3e-2), (a.grad.double().cpu() - b.grad).abs().max()

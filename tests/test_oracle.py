@@ -259,6 +259,32 @@ def test_sdpa_backward_finite_differences():
         close(dv, fd_grad(lambda t: ops.sdpa_forward(q, k, t, causal=causal)[0], v, do), rtol=1e-6, atol=1e-8)
 
 
+def test_sdpa_backward_window_and_grouped_heads():
+    """Backward with a sliding window and grouped K/V heads: finite
+    differences of the forward (so dK/dV must sum each group's query heads
+    and the window must mask the same keys as the forward), plus torch CPU
+    autograd through SDPA with the equivalent boolean mask and enable_gqa."""
+    rng = np.random.default_rng(8)
+    q, do = rng.normal(size=(1, 4, 6, 3)), rng.normal(size=(1, 4, 6, 3))
+    k, v = rng.normal(size=(1, 2, 6, 3)), rng.normal(size=(1, 2, 6, 3))
+    for w in (0, 2, 4):
+        f = lambda qq, kk, vv: ops.sdpa_forward(qq, kk, vv, causal=True, window=w)[0]  # noqa: E731
+        o, lse = ops.sdpa_forward(q, k, v, causal=True, window=w)
+        dq, dk, dv = ops.sdpa_backward(do, q, k, v, o, lse, causal=True, window=w)
+        assert dk.shape == k.shape and dv.shape == v.shape
+        close(dq, fd_grad(lambda t: f(t, k, v), q, do), rtol=1e-6, atol=1e-8)
+        close(dk, fd_grad(lambda t: f(q, t, v), k, do), rtol=1e-6, atol=1e-8)
+        close(dv, fd_grad(lambda t: f(q, k, t), v, do), rtol=1e-6, atol=1e-8)
+        tq, tk, tv = (torch.tensor(a, requires_grad=True) for a in (q, k, v))
+        i, j = torch.arange(6)[:, None], torch.arange(6)[None, :]
+        keep = (j <= i) & ((i - j < w) if w else True)
+        out = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=keep, enable_gqa=True)
+        out.backward(torch.tensor(do))
+        close(dq, tq.grad.numpy(), rtol=1e-10, atol=1e-12)
+        close(dk, tk.grad.numpy(), rtol=1e-10, atol=1e-12)
+        close(dv, tv.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
 def test_sdpa_live_torch_rect_top_left():
     g = torch.Generator().manual_seed(7)
     q, k, v = torch.randn(2, 2, 5, 3, generator=g), torch.randn(2, 2, 7, 3, generator=g), torch.randn(2, 2, 7, 3, generator=g)

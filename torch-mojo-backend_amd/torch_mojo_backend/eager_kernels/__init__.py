@@ -195,6 +195,23 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_vp, c_i64, c_vp,
         ],
     ),
+    "mi355x_attn_fwd_gen": (
+        c_int,
+        [
+            c_vp, P_i64, c_vp, c_vp, P_i64, c_vp, P_i64, c_vp, P_i64,
+            c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_double, c_int, c_i64, c_int, c_vp,
+        ],
+    ),
+    "mi355x_attn_bwd_gen_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
+    "mi355x_attn_bwd_gen": (
+        c_int,
+        [
+            c_vp, P_i64, c_vp, P_i64, c_vp, P_i64, c_vp, P_i64,
+            c_vp, P_i64, c_vp, P_i64, c_vp, P_i64, c_vp, P_i64, c_vp,
+            c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_double, c_int, c_i64, c_int,
+            c_vp, c_i64, c_vp,
+        ],
+    ),
     "mi355x_attn_bwd_noalloc": (
         c_int,
         [

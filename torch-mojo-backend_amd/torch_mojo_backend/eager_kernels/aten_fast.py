@@ -1884,23 +1884,28 @@ def fast_aten_embedding_dense_backward(grad_output, indices, num_weights, paddin
 # ---------------------------------------------------------------------------
 # scaled dot-product attention (aten_fast.py:7462-7839, 9102-9211)
 # ---------------------------------------------------------------------------
-_FUSED_FA_HEAD_DIMS = (32, 64, 128)
-
-
 def _bhs(t: MT):
     return _i64(t._strides[:3])
 
 
+_FUSED_FA_HEAD_DIMS = (32, 64, 128)  # the MFMA forward + backward
+_MFMA_EX_HEAD_DIMS = (64, 128, 256)   # the MFMA forward with grouped K/V heads / a window
+_FUSED_FA_MAX_HEAD_DIM = 256          # the fused gate (aten_fast.py:7420)
+
+
 def fused_fa_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa):
-    """Eligible [B,H,S,D] q/k/v for the fused kernels, or None (metadata only;
-    same gate as aten_fast.py:7462-7530 minus the gfx942 check)."""
+    """Eligible [B,H,S,D] q/k/v for the fused flash pair, or None (metadata
+    only; the gate of aten_fast.py:7462-7530 minus its gfx942 check: f32,
+    bf16 or f16, head_dim up to 256, no mask, dropout or grouped heads).
+    bf16/f16 at head_dim 32, 64 or 128 run on MFMA; the rest on the f32
+    kernels of csrc/attention_generic.hip."""
     q, k, v = _t(query), _t(key), _t(value)
     if (
         q is None or k is None or v is None
         or attn_mask is not None or enable_gqa
         or float(dropout_p) != 0.0
         or q._device != k._device or q._device != v._device
-        or q._dtype not in _MFMA_DTYPES
+        or q._dtype not in _FLOAT_DTYPES
         or q._dtype != k._dtype or q._dtype != v._dtype
         or len(q._shape) != 4 or len(k._shape) != 4 or len(v._shape) != 4
     ):
@@ -1909,7 +1914,7 @@ def fused_fa_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, e
         return None
     b, h, sq, d = q._shape
     skv = k._shape[2]
-    if min(b, h, sq, skv, d) <= 0 or d not in _FUSED_FA_HEAD_DIMS:
+    if min(b, h, sq, skv, d) <= 0 or d > _FUSED_FA_MAX_HEAD_DIM:
         return None
     if scale is not None and not math.isfinite(float(scale)):
         return None
@@ -1917,13 +1922,19 @@ def fused_fa_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, e
 
 
 def _fa_head_contig(t: MT) -> MT:
-    """t itself when the kernels can read it in place (unit head_dim stride,
-    16-byte aligned base, (b, h, s) strides multiples of 8 elements), else a
-    contiguous copy."""
+    """t itself when the MFMA kernels can read it in place (unit head_dim
+    stride, 16-byte aligned base, (b, h, s) strides multiples of 8
+    elements), else a contiguous copy."""
     st = t._strides
     if st[3] == 1 and t._ptr % 16 == 0 and st[0] % 8 == 0 and st[1] % 8 == 0 and st[2] % 8 == 0:
         return t
     return materialize_contiguous(t)
+
+
+def _unit_head_stride(t: MT) -> MT:
+    """t itself when its head_dim stride is 1 (all the f32 kernels need), else
+    a contiguous copy."""
+    return t if t._strides[3] == 1 or t._shape[3] == 1 else materialize_contiguous(t)
 
 
 def alloc_bthd(b, h, s, d, dtype, device) -> MT:
@@ -1933,46 +1944,96 @@ def alloc_bthd(b, h, s, d, dtype, device) -> MT:
     return MT._view_of(dense, (b, h, s, d), (s * h * d, d, h * d, 1), 0)
 
 
-def fused_flash_attention_forward(q: MT, k: MT, v: MT, is_causal, scale):
-    q, k, v = _fa_head_contig(q), _fa_head_contig(k), _fa_head_contig(v)
+def _mfma_fwd_ok(q: MT, group, window) -> bool:
+    d = q._shape[3]
+    if q._dtype not in _MFMA_DTYPES:
+        return False
+    if group == 1 and window == 0 and d in _FUSED_FA_HEAD_DIMS:
+        return True
+    return d in _MFMA_EX_HEAD_DIMS
+
+
+def _mfma_bwd_ok(q: MT, group, window) -> bool:
+    return q._dtype in _MFMA_DTYPES and group == 1 and window == 0 and q._shape[3] in _FUSED_FA_HEAD_DIMS
+
+
+def attention_forward(q: MT, k: MT, v: MT, causal, window, scale):
+    """(out [B,H,Sq,D] over BTHD storage, lse f32 [B,H,Sq]) of causal / full
+    attention with optional grouped K/V heads (k, v with H / g heads) and a
+    causal sliding window: MFMA kernels where they apply, else the f32
+    kernels."""
     b, h, sq, d = q._shape
-    skv = k._shape[2]
+    hk, skv = k._shape[1], k._shape[2]
     scale_value = float(scale) if scale is not None else 1.0 / math.sqrt(d)
     out = alloc_bthd(b, h, sq, d, q._dtype, q._device)
     lse = _alloc((b, h, sq), torch.float32, q._device)
-    check(
-        "mi355x_attn_fwd",
-        lib().mi355x_attn_fwd(out._ptr, _bhs(out), lse._ptr, q._ptr, _bhs(q), k._ptr, _bhs(k),
-                              v._ptr, _bhs(v), b, h, sq, skv, d, scale_value, int(bool(is_causal)),
-                              _code(q._dtype), _STREAM),
-    )
+    if _mfma_fwd_ok(q, h // hk, window):
+        q, k, v = _fa_head_contig(q), _fa_head_contig(k), _fa_head_contig(v)
+        check(
+            "mi355x_attn_fwd_ex",
+            lib().mi355x_attn_fwd_ex(out._ptr, _bhs(out), lse._ptr, q._ptr, _bhs(q), k._ptr, _bhs(k),
+                                     v._ptr, _bhs(v), b, h, hk, sq, skv, d, scale_value, int(bool(causal)),
+                                     int(window), _code(q._dtype), _STREAM),
+        )
+    else:
+        q, k, v = _unit_head_stride(q), _unit_head_stride(k), _unit_head_stride(v)
+        check(
+            "mi355x_attn_fwd_gen",
+            lib().mi355x_attn_fwd_gen(out._ptr, _bhs(out), lse._ptr, q._ptr, _bhs(q), k._ptr, _bhs(k),
+                                      v._ptr, _bhs(v), b, h, hk, sq, skv, d, scale_value, int(bool(causal)),
+                                      int(window), _code(q._dtype), _STREAM),
+        )
     return out, lse
 
 
-def fused_flash_attention_backward(grad_out, q, k, v, out, lse, is_causal, scale):
-    q, k, v = _fa_head_contig(q), _fa_head_contig(k), _fa_head_contig(v)
-    out = _fa_head_contig(out)
-    dout = _fa_head_contig(grad_out)
-    if dout._dtype != q._dtype:
-        dout = materialize_contiguous(dout, q._dtype)
-    lse = _contig(lse)
+def attention_backward(grad_out, q: MT, k: MT, v: MT, out: MT, lse: MT, causal, window, scale):
+    """(dq, dk, dv) of attention_forward: dk/dv have k's heads (the query
+    heads of each group summed)."""
     b, h, sq, d = q._shape
-    skv = k._shape[2]
+    hk, skv = k._shape[1], k._shape[2]
     scale_value = float(scale) if scale is not None else 1.0 / math.sqrt(d)
+    if grad_out._dtype != q._dtype:
+        grad_out = materialize_contiguous(grad_out, q._dtype)
+    lse = _contig(lse)
     dq = alloc_bthd(b, h, sq, d, q._dtype, q._device)
-    dk = alloc_bthd(b, h, skv, d, q._dtype, q._device)
-    dv = alloc_bthd(b, h, skv, d, q._dtype, q._device)
-    ws = lib().mi355x_attn_bwd_workspace_bytes(b, h, sq, skv, d)
-    hold, wptr = _workspace(ws, q._device)
-    check(
-        "mi355x_attn_bwd",
-        lib().mi355x_attn_bwd(
-            dq._ptr, _bhs(dq), dk._ptr, _bhs(dk), dv._ptr, _bhs(dv), dout._ptr, _bhs(dout),
-            q._ptr, _bhs(q), k._ptr, _bhs(k), v._ptr, _bhs(v), out._ptr, _bhs(out), lse._ptr,
-            b, h, sq, skv, d, scale_value, int(bool(is_causal)), _code(q._dtype), wptr, ws, _STREAM,
-        ),
-    )
+    dk = alloc_bthd(b, hk, skv, d, q._dtype, q._device)
+    dv = alloc_bthd(b, hk, skv, d, q._dtype, q._device)
+    if _mfma_bwd_ok(q, h // hk, window):
+        q, k, v = _fa_head_contig(q), _fa_head_contig(k), _fa_head_contig(v)
+        out, dout = _fa_head_contig(out), _fa_head_contig(grad_out)
+        ws = lib().mi355x_attn_bwd_workspace_bytes(b, h, sq, skv, d)
+        hold, wptr = _workspace(ws, q._device)
+        check(
+            "mi355x_attn_bwd",
+            lib().mi355x_attn_bwd(
+                dq._ptr, _bhs(dq), dk._ptr, _bhs(dk), dv._ptr, _bhs(dv), dout._ptr, _bhs(dout),
+                q._ptr, _bhs(q), k._ptr, _bhs(k), v._ptr, _bhs(v), out._ptr, _bhs(out), lse._ptr,
+                b, h, sq, skv, d, scale_value, int(bool(causal)), _code(q._dtype), wptr, ws, _STREAM,
+            ),
+        )
+    else:
+        q, k, v = _unit_head_stride(q), _unit_head_stride(k), _unit_head_stride(v)
+        out, dout = _unit_head_stride(out), _unit_head_stride(grad_out)
+        ws = lib().mi355x_attn_bwd_gen_workspace_bytes(b, h, sq)
+        hold, wptr = _workspace(ws, q._device)
+        check(
+            "mi355x_attn_bwd_gen",
+            lib().mi355x_attn_bwd_gen(
+                dq._ptr, _bhs(dq), dk._ptr, _bhs(dk), dv._ptr, _bhs(dv), dout._ptr, _bhs(dout),
+                q._ptr, _bhs(q), k._ptr, _bhs(k), v._ptr, _bhs(v), out._ptr, _bhs(out), lse._ptr,
+                b, h, hk, sq, skv, d, scale_value, int(bool(causal)), int(window), _code(q._dtype),
+                wptr, ws, _STREAM,
+            ),
+        )
     return dq, dk, dv
+
+
+def fused_flash_attention_forward(q: MT, k: MT, v: MT, is_causal, scale):
+    return attention_forward(q, k, v, is_causal, 0, scale)
+
+
+def fused_flash_attention_backward(grad_out, q, k, v, out, lse, is_causal, scale):
+    return attention_backward(grad_out, q, k, v, out, lse, is_causal, 0, scale)
 
 
 def fast_aten__scaled_dot_product_flash_attention(
@@ -2039,9 +2100,9 @@ def sdpa_math(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
 
 
 def fused_fa_ex_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa):
-    """Forward-only fused attention beyond the flash-pair gate: grouped K/V
-    heads (enable_gqa), head_dim 256, and a sliding-window causal mask built
-    by torch_mojo_backend.masks.  Returns (q, k, v, causal, window) or None."""
+    """Fused attention beyond the flash-pair gate: grouped K/V heads
+    (enable_gqa) and a sliding-window causal mask built by
+    torch_mojo_backend.masks.  Returns (q, k, v, causal, window) or None."""
     from ..masks import window_of
 
     q, k, v = _t(query), _t(key), _t(value)
@@ -2049,7 +2110,7 @@ def fused_fa_ex_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale
         q is None or k is None or v is None
         or float(dropout_p) != 0.0
         or q._device != k._device or q._device != v._device
-        or q._dtype not in _MFMA_DTYPES
+        or q._dtype not in _FLOAT_DTYPES
         or q._dtype != k._dtype or q._dtype != v._dtype
         or len(q._shape) != 4 or len(k._shape) != 4 or len(v._shape) != 4
     ):
@@ -2060,7 +2121,7 @@ def fused_fa_ex_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale
         return None
     if hk != h and not (enable_gqa and hk > 0 and h % hk == 0):
         return None
-    if min(b, h, sq, skv) <= 0 or d not in (64, 128, 256):
+    if min(b, h, sq, skv, d) <= 0 or d > _FUSED_FA_MAX_HEAD_DIM:
         return None
     if scale is not None and not math.isfinite(float(scale)):
         return None
@@ -2073,36 +2134,16 @@ def fused_fa_ex_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale
     return q, k, v, causal, window
 
 
-def fused_flash_attention_forward_ex(q: MT, k: MT, v: MT, causal, window, scale):
-    q, k, v = _fa_head_contig(q), _fa_head_contig(k), _fa_head_contig(v)
-    b, h, sq, d = q._shape
-    hk, skv = k._shape[1], k._shape[2]
-    scale_value = float(scale) if scale is not None else 1.0 / math.sqrt(d)
-    out = alloc_bthd(b, h, sq, d, q._dtype, q._device)
-    lse = _alloc((b, h, sq), torch.float32, q._device)
-    check(
-        "mi355x_attn_fwd_ex",
-        lib().mi355x_attn_fwd_ex(out._ptr, _bhs(out), lse._ptr, q._ptr, _bhs(q), k._ptr, _bhs(k),
-                                 v._ptr, _bhs(v), b, h, hk, sq, skv, d, scale_value, int(causal),
-                                 int(window), _code(q._dtype), _STREAM),
-    )
-    return out, lse
-
-
 def fast_aten_scaled_dot_product_attention(
     query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, *, scale=None, enable_gqa=False
 ):
-    """No-grad SDPA (aten_fast.py:9102-9211): fused kernel when eligible
-    (including grouped K/V heads, head_dim 256 and sliding-window masks from
-    torch_mojo_backend.masks), otherwise the decomposition."""
-    inputs = fused_fa_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa)
-    if inputs is not None:
-        out, _ = fused_flash_attention_forward(*inputs, is_causal, scale)
-        return out
+    """No-grad SDPA (aten_fast.py:9102-9211): fused kernels when eligible
+    (including grouped K/V heads, f32, head_dim up to 256 and sliding-window
+    masks from torch_mojo_backend.masks), otherwise the decomposition."""
     ex = fused_fa_ex_inputs(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa)
     if ex is not None:
         q, k, v, causal, window = ex
-        out, _ = fused_flash_attention_forward_ex(q, k, v, causal, window, scale)
+        out, _ = attention_forward(q, k, v, causal, window, scale)
         return out
     return sdpa_math(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa)
 

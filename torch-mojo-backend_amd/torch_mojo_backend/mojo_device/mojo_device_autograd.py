@@ -13,8 +13,12 @@ mojo_device_autograd.py:565-643), re-targeted at gfx950:
   recomputes P from the saved natural-log LSE (never the S x S matrix);
 - no grad -> ``scaled_dot_product_attention`` on the device (fused kernel or
   decomposition);
-- otherwise (masks, GQA, ...) -> the math decomposition built from device
-  ops, differentiated through its pieces.
+- grad needed with grouped K/V heads or a sliding-window mask from
+  torch_mojo_backend.masks -> ``_FusedAttention`` (fused forward, fused
+  backward with dK/dV summed over each group), where the reference takes
+  the math decomposition;
+- otherwise (other masks, dropout) -> the math decomposition built from
+  device ops, differentiated through its pieces.
 
 There is no queue to drain before these routes: kernels are issued directly.
 
@@ -63,9 +67,40 @@ def _scaled_dot_product_attention_autograd(
         return torch.ops.aten._scaled_dot_product_flash_attention.default(
             query, key, value, dropout_p, is_causal, False, scale=scale
         )[0]
+    ex = aten_fast.fused_fa_ex_inputs(
+        query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa
+    )
+    if ex is not None:
+        _, _, _, causal, window = ex
+        return _FusedAttention.apply(query, key, value, causal, window, scale)
     return aten_fast.sdpa_math(
         query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa
     )
+
+
+class _FusedAttention(torch.autograd.Function):
+    """Attention with grouped K/V heads and/or a sliding-window causal mask
+    (the Gemma-3-shaped layers), which the ATen flash pair cannot express:
+    the fused forward saves (q, k, v, out, lse) like the pair does, and the
+    fused backward recomputes P from the LSE, summing dK/dV over each
+    group's query heads.  The reference differentiates these through its
+    masked-math decomposition (aten_fast.py:9112-9123)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal, window, scale):
+        with torch._C._AutoDispatchBelowAutograd():
+            out, lse = aten_fast.attention_forward(q, k, v, causal, window, scale)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.args = (causal, window, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        q, k, v, out, lse = ctx.saved_tensors
+        causal, window, scale = ctx.args
+        with torch._C._AutoDispatchBelowAutograd():
+            dq, dk, dv = aten_fast.attention_backward(grad, q, k, v, out, lse, causal, window, scale)
+        return dq, dk, dv, None, None, None
 
 
 def register_autograd_ops() -> None:
