@@ -492,3 +492,31 @@ def test_fused_adamw_checks_the_amsgrad_state(mojo):
     with pytest.raises(RuntimeError, match="max_exp_avg_sq 0 has 7 elements"):
         torch._fused_adamw_([p], [g], [m], [v.abs()], [short], [step], lr=1e-3, beta1=0.9, beta2=0.99,
                             weight_decay=0.0, eps=1e-8, amsgrad=True, maximize=False)
+
+
+def test_cat_of_attention_gradient_slices_is_a_view(mojo):
+    """The attention backward hands out dQ, dK, dV as adjacent slices of one
+    buffer; the cat of the fused-qkv split's backward returns that buffer as
+    a view (no copy) and matches torch.  A cat of adjacent slices of an
+    unmarked buffer still copies (cat never aliases its inputs otherwise)."""
+    from torch_mojo_backend.eager_kernels import aten_fast
+
+    g = torch.Generator().manual_seed(4)
+    B, T, H, D = 2, 16, 2, 8
+    qkv = torch.randn(B, T, 3 * H * D, generator=g)
+    qkv_m = qkv.to("mojo").requires_grad_()
+    q, k, v = (t.view(B, T, H, D).transpose(1, 2) for t in qkv_m.split(H * D, dim=2))
+    out = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    dout = torch.randn(out.shape, generator=g)
+    out.backward(dout.to("mojo"))
+    qc = qkv.clone().requires_grad_()
+    qq, kk, vv = (t.view(B, T, H, D).transpose(1, 2) for t in qc.split(H * D, dim=2))
+    F.scaled_dot_product_attention(qq, kk, vv, is_causal=True).backward(dout)
+    assert torch.allclose(qkv_m.grad.cpu(), qc.grad, atol=1e-5, rtol=1e-4)
+    # unmarked storage: a copy, so writing the result leaves the pieces alone
+    base = torch.randn(4, 6).to("mojo")
+    a, b = base[:, :3], base[:, 3:]
+    c = torch.cat([a, b], 1)
+    c.zero_()
+    assert not torch.equal(base.cpu(), torch.zeros(4, 6))
+    assert aten_fast._CAT_READY

@@ -113,11 +113,12 @@ __global__ void __launch_bounds__(256) splitk_reduce(GemmArgs g, int splits, int
 // elements: each thread sums four adjacent columns with 16-byte partial
 // loads and 32-bit index math.
 template <typename CT>
-__global__ void __launch_bounds__(256) splitk_reduce4(GemmArgs g, int splits, int nb) {
+__device__ __forceinline__ void splitk_reduce4_body(const GemmArgs& g, int splits, int nb, uint32_t blk,
+                                                    uint32_t nblk) {
   const uint32_t n4 = (uint32_t)(g.n / 4), mn4 = (uint32_t)g.m * n4;
   const uint32_t total = (uint32_t)nb * mn4;
   const float4* P = (const float4*)g.part;
-  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+  for (uint32_t i = blk * 256u + threadIdx.x; i < total; i += nblk * 256u) {
     const uint32_t bi = i / mn4, rem = i - bi * mn4;
     const uint32_t row = rem / n4, col = (rem - row * n4) * 4;
     float4 a = P[i];
@@ -143,14 +144,20 @@ __global__ void __launch_bounds__(256) splitk_reduce4(GemmArgs g, int splits, in
   }
 }
 
+template <typename CT>
+__global__ void __launch_bounds__(256) splitk_reduce4(GemmArgs g, int splits, int nb) {
+  splitk_reduce4_body<CT>(g, splits, nb, blockIdx.x, gridDim.x);
+}
+
 // Sum the row-sum partials ([slots][nb * m]) into rowsum[batch][m].  A block
 // takes 32 rows at a time with 8 threads per row, each summing every 8th
 // slot, then combines the 8 in LDS.
-__global__ void __launch_bounds__(256) rowsum_reduce(GemmArgs g, int slots, int64_t nb) {
+__device__ __forceinline__ void rowsum_reduce_body(const GemmArgs& g, int slots, int64_t nb, uint32_t blk,
+                                                   uint32_t nblk) {
   __shared__ float red[8][33];
   const int64_t total = nb * g.m;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-  for (int64_t base = (int64_t)blockIdx.x * 32; base < total; base += (int64_t)gridDim.x * 32) {
+  for (int64_t base = (int64_t)blk * 32; base < total; base += (int64_t)nblk * 32) {
     const int64_t idx = base + tx;
     float v = 0.f;
     if (idx < total) {
@@ -175,6 +182,18 @@ __global__ void __launch_bounds__(256) rowsum_reduce(GemmArgs g, int slots, int6
   }
 }
 
+__global__ void __launch_bounds__(256) rowsum_reduce(GemmArgs g, int slots, int64_t nb) {
+  rowsum_reduce_body(g, slots, nb, blockIdx.x, gridDim.x);
+}
+
+// The two finishing sums of a split-K GEMM with row sums in one launch:
+// blocks [0, nbc) sum the C partials, the rest the row-sum partials.
+template <typename CT>
+__global__ void __launch_bounds__(256) splitk_rowsum_reduce(GemmArgs g, int splits, int nb, int slots,
+                                                             uint32_t nbc) {
+  if (blockIdx.x < nbc) splitk_reduce4_body<CT>(g, splits, nb, blockIdx.x, nbc);
+  else rowsum_reduce_body(g, slots, nb, blockIdx.x - nbc, gridDim.x - nbc);
+}
 
 // k-contiguous operand tile: ROWS rows x 64 k, loaded by NT threads.  Thread
 // (wave w, lane l) handles rows r = 8*(it*WAVES + w) + l/8; with WAVES even
@@ -844,13 +863,26 @@ int launch_tile(GemmArgs g, int64_t batch, int splits, hipStream_t s) {
   return launch_layout<T, CFG, KT, false>(g, grid, s);
 }
 
-int splitk_finish(const GemmArgs& g, int64_t batch, int splits, hipStream_t s) {
+// Sum the split-K partials into C and, with rs_slots > 0, the row-sum
+// partials into the row sums; returns -1 when the C sum needs the scalar
+// kernel (then the caller sums the row sums itself).
+int splitk_finish(const GemmArgs& g, int64_t batch, int splits, int rs_slots, hipStream_t s) {
   const int64_t total = batch * g.m * g.n;
   const int64_t c_align = g.c_dt == MI355X_F32 ? 16 : 8;
   if (g.n % 4 == 0 && g.c_rs % 4 == 0 && g.c_bs % 4 == 0 && (uintptr_t)g.c % c_align == 0 &&
       (int64_t)splits * total < (1ll << 31)) {
     int64_t blocks = (total / 4 + 255) / 256;
     if (blocks > 8192) blocks = 8192;
+    if (rs_slots > 0) {
+      const int64_t rblocks = min((batch * g.m + 31) / 32, (int64_t)65536);
+      const unsigned grid = (unsigned)(blocks + rblocks);
+      switch (g.c_dt) {
+        case MI355X_F32: splitk_rowsum_reduce<float><<<grid, 256, 0, s>>>(g, splits, (int)batch, rs_slots, (uint32_t)blocks); break;
+        case MI355X_BF16: splitk_rowsum_reduce<bf16><<<grid, 256, 0, s>>>(g, splits, (int)batch, rs_slots, (uint32_t)blocks); break;
+        default: splitk_rowsum_reduce<f16><<<grid, 256, 0, s>>>(g, splits, (int)batch, rs_slots, (uint32_t)blocks); break;
+      }
+      return check_launch("mi355x_gemm splitk_rowsum_reduce");
+    }
     switch (g.c_dt) {
       case MI355X_F32: splitk_reduce4<float><<<(unsigned)blocks, 256, 0, s>>>(g, splits, (int)batch); break;
       case MI355X_BF16: splitk_reduce4<bf16><<<(unsigned)blocks, 256, 0, s>>>(g, splits, (int)batch); break;
@@ -861,7 +893,8 @@ int splitk_finish(const GemmArgs& g, int64_t batch, int splits, hipStream_t s) {
   int64_t blocks = (total + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(g, splits, batch);
-  return check_launch("mi355x_gemm splitk_reduce");
+  const int rc = check_launch("mi355x_gemm splitk_reduce");
+  return rc ? rc : -1;
 }
 
 template <typename T>
@@ -872,8 +905,10 @@ int launch_mfma(GemmArgs g, int64_t batch, const Plan& p, hipStream_t s) {
   else if (p.cfg == 2) rc = kt ? launch_tile<T, 2, true>(g, batch, p.splits, s) : launch_tile<T, 2, false>(g, batch, p.splits, s);
   else rc = kt ? launch_tile<T, 0, true>(g, batch, p.splits, s) : launch_tile<T, 0, false>(g, batch, p.splits, s);
   if (rc || !g.part) return rc;
-  rc = splitk_finish(g, batch, p.splits, s);
-  if (rc || !g.rowsum) return rc;
+  const int rs_slots = g.rowsum ? (int)(p.splits * rs_slots_of(p.cfg, g.n)) : 0;
+  rc = splitk_finish(g, batch, p.splits, rs_slots, s);
+  if (rc != -1) return rc;  // done (or failed)
+  if (!g.rowsum) return MI355X_OK;
   const int64_t blocks = min((batch * g.m + 31) / 32, (int64_t)65536);
   rowsum_reduce<<<(unsigned)blocks, 256, 0, s>>>(g, (int)(p.splits * rs_slots_of(p.cfg, g.n)), batch);
   return check_launch("mi355x_gemm rowsum_reduce");

@@ -1096,6 +1096,39 @@ def fast_aten_min_dim(self, dim, keepdim=False):
 _FOREACH_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
+_CAT_READY = "_mojo_cat_ready"
+
+
+def _mark_cat_ready(t: MT) -> None:
+    """Mark a fresh buffer whose slices are handed out as separate results
+    (the attention gradients): one cat of its adjacent slices may return a
+    view of it instead of a copy."""
+    setattr(t._holder, _CAT_READY, True)
+
+
+def _cat_in_place(ts, d, shape):
+    """A view of the buffer when `ts` are adjacent slices of one cat-ready
+    buffer laid out exactly as their concatenation along d (same strides,
+    equal to the result's contiguous strides; offsets one piece after the
+    other), else None.  The mark is consumed."""
+    first = ts[0]
+    holder = first._holder
+    if not getattr(holder, _CAT_READY, False):
+        return None
+    strides = [1] * len(shape)
+    for j in range(len(shape) - 2, -1, -1):
+        strides[j] = strides[j + 1] * shape[j + 1]
+    off = first._offset
+    for x in ts:
+        if x._holder is not holder or x._dtype != first._dtype or tuple(x._strides) != tuple(strides):
+            return None
+        if x._offset != off:
+            return None
+        off += x._shape[d] * strides[d]
+    setattr(holder, _CAT_READY, False)
+    return MT._view_of(first, tuple(shape), tuple(strides), first._offset, True)
+
+
 def fast_aten_cat(tensors, dim=0):
     ts = [_require(x) for x in tensors]
     ts_nonempty = [x for x in ts if not (len(x._shape) == 1 and x._shape[0] == 0)]
@@ -1125,6 +1158,10 @@ def fast_aten_cat(tensors, dim=0):
                 )
     shape = list(ref._shape)
     shape[d] = sum(x._shape[d] for x in ts_nonempty)
+    if len(ts_nonempty) > 1 and all(x._dtype == dtype for x in ts_nonempty):
+        view = _cat_in_place(ts_nonempty, d, shape)
+        if view is not None:
+            return view
     out = _alloc(shape, dtype, ref._device)
     if (len(ts_nonempty) >= 8 and math.prod(shape[:d]) == 1 and dtype in _FOREACH_DTYPES
             and all(x._dtype == dtype and x._is_contiguous for x in ts_nonempty)):
@@ -1995,9 +2032,18 @@ def attention_backward(grad_out, q: MT, k: MT, v: MT, out: MT, lse: MT, causal, 
     if grad_out._dtype != q._dtype:
         grad_out = materialize_contiguous(grad_out, q._dtype)
     lse = _contig(lse)
-    dq = alloc_bthd(b, h, sq, d, q._dtype, q._device)
-    dk = alloc_bthd(b, hk, skv, d, q._dtype, q._device)
-    dv = alloc_bthd(b, hk, skv, d, q._dtype, q._device)
+    if hk == h and skv == sq:
+        # dQ, dK, dV side by side in one [B, S, 3, H, D] buffer: the backward of
+        # the fused qkv projection's split is then a cat of adjacent slices,
+        # which fast_aten_cat returns as a view of this buffer (no copies)
+        dense = _alloc((b, sq, 3, h, d), q._dtype, q._device)
+        st = (sq * 3 * h * d, d, 3 * h * d, 1)
+        dq, dk, dv = (MT._view_of(dense, (b, h, sq, d), st, i * h * d) for i in range(3))
+        _mark_cat_ready(dense)
+    else:
+        dq = alloc_bthd(b, h, sq, d, q._dtype, q._device)
+        dk = alloc_bthd(b, hk, skv, d, q._dtype, q._device)
+        dv = alloc_bthd(b, hk, skv, d, q._dtype, q._device)
     if _mfma_bwd_ok(q, h // hk, window):
         q, k, v = _fa_head_contig(q), _fa_head_contig(k), _fa_head_contig(v)
         out, dout = _fa_head_contig(out), _fa_head_contig(grad_out)
