@@ -243,6 +243,18 @@ def bench_hbm(iters):
     ms = time_gpu(lambda: F.fast_aten__log_softmax(lg, 1, False), max(3, iters // 4))
     nbytes = 16384 * 50257 * 2 * 2
     out.append({"kernel": "log_softmax_fwd bf16 [16384,50257]", "ms": ms, "gbs": nbytes / ms / 1e6})
+    tgt = torch.randint(0, 50257, (16384,), generator=g).to("mojo")
+    ms = time_gpu(lambda: F.fused_cross_entropy_forward(lg, tgt, 1, -100), max(3, iters // 4))
+    nbytes = 16384 * 50257 * 2
+    out.append({"kernel": "cross_entropy_fwd bf16 [16384,50257] (fused, in the step)", "ms": ms,
+                "gbs": nbytes / ms / 1e6})
+    loss, lse, total = F.fused_cross_entropy_forward(lg, tgt, 1, -100)
+    one = torch.ones((), device="mojo")
+    ms = time_gpu(lambda: F.fused_cross_entropy_backward(one, lg, tgt, lse, total, 1, -100), max(3, iters // 4))
+    nbytes = 16384 * 50257 * 2 + 16384 * 50264 * 2
+    out.append({"kernel": "cross_entropy_bwd bf16 [16384,50257] (fused, in the step)", "ms": ms,
+                "gbs": nbytes / ms / 1e6})
+    del loss, lse, total
     lp = F.fast_aten__log_softmax(lg, 1, False)
     del lg
     dlp = torch.randn(16384, 50257, generator=g).bfloat16().to("mojo")
