@@ -280,6 +280,18 @@ int mi355x_layer_norm_fwd_ex(void* y, void* y_low, int low_dtype, float* mean,
                              float* rstd, const void* x, const void* gamma,
                              const void* beta, int64_t rows, int64_t cols,
                              double eps, int dtype, mi355x_stream_t stream);
+/* The residual add of a pre-LayerNorm block fused into the norm that reads
+ * it: x_out = a + r (a f32, r f32/bf16/f16, summed in f32 exactly as a
+ * separate add would), then y = LayerNorm(x_out) with y_low as in
+ * mi355x_layer_norm_fwd_ex.  f32 rows only, cols a multiple of 4 up to 2048
+ * with 16-byte aligned rows (else MI355X_EUNSUPPORTED: run the add and the
+ * norm separately).  Serves nanoGPT's `x = x + f(ln(x))` followed by the next
+ * ln(x): the reference runs the add (fast_aten_add, aten_fast.py:2510) and
+ * the norm (aten_fast.py:5248-5371) as two kernels. */
+int mi355x_layer_norm_fwd_add(void* y, void* y_low, int low_dtype, float* mean, float* rstd,
+                              void* x_out, const void* a, const void* r, int r_dtype,
+                              const void* gamma, const void* beta, int64_t rows, int64_t cols,
+                              double eps, int dtype, mi355x_stream_t stream);
 /* Any of dx/dgamma/dbeta may be NULL (output_mask, aten_fast.py:5475). */
 int64_t mi355x_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 int mi355x_layer_norm_bwd(void* dx, void* dgamma, void* dbeta,

@@ -249,6 +249,14 @@ class HostStandIn:
             dense(_val(y_low), DT[low_dt], (rows, cols)).copy_(dense(_val(y), DT[dt], (rows, cols)))
         return 0
 
+    def mi355x_layer_norm_fwd_add(self, y, y_low, low_dt, mean, rstd, x_out, a, r, r_dt, g, b, rows, cols, eps,
+                                  dt, stream):
+        self.fused_add_calls = getattr(self, "fused_add_calls", 0) + 1
+        A = dense(_val(a), DT[dt], (rows, cols))
+        R = dense(_val(r), DT[r_dt], (rows, cols)).float()
+        dense(_val(x_out), DT[dt], (rows, cols)).copy_(A.float() + R)
+        return self.mi355x_layer_norm_fwd_ex(y, y_low, low_dt, mean, rstd, x_out, g, b, rows, cols, eps, dt, stream)
+
     def mi355x_layer_norm_fwd(self, y, mean, rstd, x, g, b, rows, cols, eps, dt, stream):
         X = dense(_val(x), DT[dt], (rows, cols)).float()
         mu = X.mean(1, keepdim=True)

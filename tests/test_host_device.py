@@ -520,3 +520,32 @@ def test_cat_of_attention_gradient_slices_is_a_view(mojo):
     c.zero_()
     assert not torch.equal(base.cpu(), torch.zeros(4, 6))
     assert aten_fast._CAT_READY
+
+
+def test_residual_add_is_fused_into_the_next_layer_norm(mojo):
+    """A large f32 + bf16 add whose result feeds a LayerNorm runs inside the
+    norm (one pass); the sum is still materialised for its other users, and
+    any other consumer (a host read, another kernel) gets the add first."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(128, 768, generator=g)
+    d = torch.randn(128, 768, generator=g).bfloat16()
+    w, b = torch.randn(768, generator=g), torch.randn(768, generator=g)
+    xm, dm, wm, bm = (t.to("mojo") for t in (x, d, w, b))
+    s = xm + dm
+    assert ek._pending  # held back
+    y = F.layer_norm(s, (768,), wm, bm)
+    assert not ek._pending
+    ref_s = x + d.float()
+    assert torch.equal(s.cpu(), ref_s)
+    assert torch.allclose(y.cpu(), F.layer_norm(ref_s, (768,), w, b), atol=1e-5, rtol=1e-5)
+    # other consumers see the sum: another kernel, then a host read
+    s2 = xm + dm
+    assert torch.equal((s2 * 2).cpu(), ref_s * 2)
+    s3 = xm + dm
+    assert torch.equal(s3.cpu(), ref_s)
+    # the inputs may change after the add is taken: it was computed first
+    s4 = xm + dm
+    xm.mul_(0)
+    assert torch.equal(s4.cpu(), ref_s)

@@ -84,6 +84,73 @@ __global__ void __launch_bounds__(kThreads)
   }
 }
 
+// The residual add fused in front of the norm: x = a + r (r of type TR,
+// added in f32 and rounded to T exactly as the separate add would), x stored
+// to x_out, then y = LayerNorm(x) as ln_fwd_wave.  One pass over a and r
+// instead of an add (read a, r; write x) followed by a norm (read x again).
+template <typename T, typename TR, typename TL, int NV>
+__global__ void __launch_bounds__(kThreads)
+    ln_fwd_add_wave(T* __restrict__ y, TL* __restrict__ y_low, float* __restrict__ mean_out,
+                    float* __restrict__ rstd_out, T* __restrict__ x_out, const T* __restrict__ a,
+                    const TR* __restrict__ r, const T* __restrict__ gamma, const T* __restrict__ beta,
+                    int64_t rows, int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  float v[NV][4];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+      float av[4], rv[4];
+      Vec4<T>::load(a + base + c, av);
+      Vec4<TR>::load(r + base + c, rv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[j][e] = to_f32(from_f32<T>(av[e] + rv[e]));
+      Vec4<T>::store(x_out + base + c, v[j]);
+    } else {
+      v[j][0] = v[j][1] = v[j][2] = v[j][3] = 0.f;
+    }
+    s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  }
+  const float inv_n = 1.f / (float)cols;
+  const float mu = wave_sum(s) * inv_n;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[j][e] - mu;
+        q += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(q) * inv_n;
+  const float rs = 1.f / sqrtf(var + eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+      float g[4] = {1.f, 1.f, 1.f, 1.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+      if (gamma) Vec4<T>::load(gamma + c, g);
+      if (beta) Vec4<T>::load(beta + c, b);
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - mu) * rs * g[e] + b[e];
+      Vec4<T>::store(y + base + c, o);
+      if (y_low) Vec4<TL>::store(y_low + base + c, o);
+    }
+  }
+  if (lane == 0) {
+    if (mean_out) mean_out[row] = mu;
+    if (rstd_out) rstd_out[row] = rs;
+  }
+}
+
 // Any `cols`: one block per row, three passes over the row.
 template <typename T, typename TL>
 __global__ void __launch_bounds__(kThreads)
@@ -439,6 +506,31 @@ int fwd_impl(T* y, TL* y_low, float* mean, float* rstd, const T* x, const T* g, 
   return check_launch("mi355x_layer_norm_fwd");
 }
 
+template <typename T, typename TR, typename TL>
+int fwd_add_impl(T* y, TL* y_low, float* mean, float* rstd, T* x_out, const T* a, const TR* r, const T* g,
+                 const T* b, int64_t rows, int64_t cols, float eps, hipStream_t s) {
+  const size_t al = 4 * sizeof(T);
+  const int nv = (aligned(a, al) && aligned(x_out, al) && aligned(r, 4 * sizeof(TR)) && aligned(y, al) &&
+                  aligned(g, al) && aligned(b, al) && aligned(y_low, 4 * sizeof(TL))) ? wave_nv(cols) : 0;
+  const unsigned grid = ceil_div(rows, kWaves);
+  switch (nv) {
+#define LN_FWD_ADD_CASE(V)                                                                                \
+    case V:                                                                                               \
+      ln_fwd_add_wave<T, TR, TL, V><<<grid, kThreads, 0, s>>>(y, y_low, mean, rstd, x_out, a, r, g, b, rows, \
+                                                               (int)cols, eps);                          \
+      break;
+    LN_FWD_ADD_CASE(1)
+    LN_FWD_ADD_CASE(2)
+    LN_FWD_ADD_CASE(3)
+    LN_FWD_ADD_CASE(4)
+    LN_FWD_ADD_CASE(8)
+#undef LN_FWD_ADD_CASE
+    default: return fail(MI355X_EUNSUPPORTED, "mi355x_layer_norm_fwd_add: rows of %lld elements or unaligned operands",
+                         (long long)cols);
+  }
+  return check_launch("mi355x_layer_norm_fwd_add");
+}
+
 template <typename T, typename W>
 int rms_impl(T* y, float* rstd, const T* x, const W* w, int64_t rows, int64_t cols, float eps, float w_off,
              hipStream_t s) {
@@ -537,6 +629,38 @@ extern "C" int mi355x_layer_norm_fwd_ex(void* y, void* y_low, int low_dtype, flo
                                 (const f16*)beta, rows, cols, (float)eps, s);
   }
   return fail(MI355X_EUNSUPPORTED, "mi355x_layer_norm_fwd: unsupported dtype %d", dtype);
+}
+
+extern "C" int mi355x_layer_norm_fwd_add(void* y, void* y_low, int low_dtype, float* mean, float* rstd,
+                                         void* x_out, const void* a, const void* r, int r_dtype,
+                                         const void* gamma, const void* beta, int64_t rows, int64_t cols,
+                                         double eps, int dtype, mi355x_stream_t stream) {
+  MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_layer_norm_fwd_add: bad shape [%lld, %lld]", (long long)rows,
+             (long long)cols);
+  if (rows == 0) return MI355X_OK;
+  MI_REQUIRE(y && x_out && a && r, "mi355x_layer_norm_fwd_add: null pointer");
+  MI_REQUIRE(dtype == MI355X_F32, "mi355x_layer_norm_fwd_add: f32 rows only (got dtype %d)", dtype);
+  MI_REQUIRE(r_dtype == MI355X_F32 || r_dtype == MI355X_BF16 || r_dtype == MI355X_F16,
+             "mi355x_layer_norm_fwd_add: unsupported residual dtype %d", r_dtype);
+  MI_REQUIRE(!y_low || low_dtype == MI355X_BF16 || low_dtype == MI355X_F16,
+             "mi355x_layer_norm_fwd_add: the low-precision copy must be bf16 or f16");
+  hipStream_t s = (hipStream_t)stream;
+  const float e = (float)eps;
+  float* Y = (float*)y;
+  float* X = (float*)x_out;
+  const float* A = (const float*)a;
+  const float* G = (const float*)gamma;
+  const float* B = (const float*)beta;
+#define LN_ADD(TR)                                                                                           \
+  do {                                                                                                      \
+    if (y_low && low_dtype == MI355X_F16)                                                                   \
+      return fwd_add_impl<float, TR, f16>(Y, (f16*)y_low, mean, rstd, X, A, (const TR*)r, G, B, rows, cols, e, s); \
+    return fwd_add_impl<float, TR, bf16>(Y, (bf16*)y_low, mean, rstd, X, A, (const TR*)r, G, B, rows, cols, e, s); \
+  } while (0)
+  if (r_dtype == MI355X_BF16) LN_ADD(bf16);
+  if (r_dtype == MI355X_F16) LN_ADD(f16);
+  LN_ADD(float);
+#undef LN_ADD
 }
 
 extern "C" int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,

@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
 from pathlib import Path
 
 LIB_NAME = "libmi355x_kernels.so"
@@ -89,6 +90,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mi355x_layer_norm_fwd_ex": (
         c_int,
         [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],
+    ),
+    "mi355x_layer_norm_fwd_add": (
+        c_int,
+        [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],
     ),
     "mi355x_layer_norm_bwd_workspace_bytes": (c_i64, [c_i64, c_i64]),
     "mi355x_layer_norm_bwd": (
@@ -282,9 +287,61 @@ def _expected_source_hash():
     return source_hash(mod._hash_flags())
 
 
+class Deferred:
+    """A kernel launch held back so that the next kernel can absorb it (the
+    residual add that the following LayerNorm reads): `out` is the result
+    tensor it will write, `inputs` what it reads, `launch()` issues it."""
+
+    __slots__ = ("out", "inputs", "launch")
+
+    def __init__(self, out, inputs, launch):
+        self.out, self.inputs, self.launch = out, inputs, launch
+
+
+_pending: list = []
+_pending_lock = threading.RLock()
+_flushing = False
+
+
+def defer(record: Deferred) -> None:
+    """Queue a launch; it runs before the next library call, host read or
+    synchronize, in the order deferred."""
+    with _pending_lock:
+        _pending.append(record)
+
+
+def take_pending(match):
+    """Remove and return the first pending launch for which match(record)
+    holds (the caller then performs its work itself), else None."""
+    if not _pending:
+        return None
+    with _pending_lock:
+        for i, rec in enumerate(_pending):
+            if match(rec):
+                return _pending.pop(i)
+    return None
+
+
+def flush_pending() -> None:
+    """Issue every deferred launch, oldest first."""
+    global _flushing
+    if not _pending or _flushing:
+        return
+    with _pending_lock:
+        _flushing = True
+        try:
+            while _pending:
+                _pending.pop(0).launch()
+        finally:
+            _flushing = False
+
+
 def lib() -> ctypes.CDLL:
-    """The loaded kernel library (loaded on first use)."""
+    """The loaded kernel library (loaded on first use).  Deferred launches
+    are issued first, so every kernel sees them in stream order."""
     global _LIB
+    if _pending and not _flushing:
+        flush_pending()
     if _LIB is None:
         _LIB = _load()
     return _LIB

@@ -22,7 +22,7 @@ import numbers
 
 import torch
 
-from . import AdamWTensor, check, lib
+from . import AdamWTensor, Deferred, check, defer, flush_pending, lib, take_pending
 from ..mojo_device.torch_mojo_tensor import (
     DTYPE_CODE,
     TorchMojoTensor,
@@ -220,6 +220,7 @@ def fast_aten_copy_(self, src, non_blocking=False):
             nbytes = cpu.numel() * cpu.element_size()
             if nbytes:
                 begin = dst._offset * dst._itemsize
+                flush_pending()
                 dst._holder[begin : begin + nbytes].copy_(cpu.reshape(-1).view(torch.uint8))
             return self
         tmp = upload(cpu.contiguous(), dst._device)
@@ -788,7 +789,30 @@ def _binary(name, a, b, alpha=1, *, out=None, inplace=False, mode=None):
         return _map_call(opcode, res, [(fill_val, da), (tb, db)], s0, 0.0)
     if tb is None:
         return _map_call(opcode, res, [(ta, da), (None, db)], s0, sb)
+    if name == "add" and not inplace and out is None and s0 == 1.0 and _residual_add(res, ta, tb):
+        # x + f(...) of a pre-norm block: held back so that the LayerNorm
+        # reading the sum can compute it in the same pass (any other
+        # consumer issues it first)
+        defer(Deferred(res, (ta, tb), lambda: _map_call(opcode, res, [(ta, da), (tb, db)], s0, 0.0)))
+        return res
     return _map_call(opcode, res, [(ta, da), (tb, db)], s0, 0.0)
+
+
+_RESIDUAL_MIN_NUMEL = 1 << 16
+
+
+def _residual_add(res: MT, a: MT, b: MT) -> bool:
+    """Whether res = a + b has the shape a fused residual-add LayerNorm
+    takes: f32 a and res, f32/bf16/f16 b, one shape, contiguous rows of a
+    multiple of 4 (at most 2048) elements, 16-byte aligned."""
+    if res._dtype != torch.float32 or a._dtype != torch.float32 or b._dtype not in _FLOAT_DTYPES:
+        return False
+    if tuple(a._shape) != tuple(res._shape) or tuple(b._shape) != tuple(res._shape):
+        return False
+    if not (a._is_contiguous and b._is_contiguous and res._is_contiguous) or res._numel < _RESIDUAL_MIN_NUMEL:
+        return False
+    cols = res._shape[-1]
+    return cols % 4 == 0 and cols <= 2048 and a._ptr % 16 == 0 and b._ptr % 16 == 0 and res._ptr % 16 == 0
 
 
 def _unary(name, a, *, out=None, inplace=False, s0=0.0, s1=0.0, float_result=True):
@@ -1632,7 +1656,21 @@ def fast_aten_native_layer_norm(input, normalized_shape, weight, bias, eps):
     # kernel also writes y in that dtype, which the cast then takes.
     low_dt = _autocast_low_dtype() if a._dtype == torch.float32 else None
     low = _alloc(a._shape, low_dt, a._device) if (low_dt is not None and rows and cols) else None
-    if rows and cols:
+    # the input is a held-back residual add: compute it in the norm's pass
+    rec = take_pending(lambda r: r.out._holder is x._holder and r.out._ptr == x._ptr
+                       and tuple(r.out._shape) == tuple(x._shape)) if rows and cols else None
+    fused = False
+    if rec is not None:
+        ra, rr = rec.inputs
+        rc = lib().mi355x_layer_norm_fwd_add(
+            out._ptr, low._ptr if low is not None else None, _code(low_dt) if low is not None else 0,
+            mean._ptr, rstd._ptr, x._ptr, ra._ptr, rr._ptr, _code(rr._dtype), g._ptr if g is not None else None,
+            b._ptr if b is not None else None, rows, cols, float(eps), _code(a._dtype), _STREAM,
+        )
+        fused = rc == 0
+        if not fused:
+            rec.launch()  # shape the fused kernel does not take: the add, then the norm
+    if rows and cols and not fused:
         check(
             "mi355x_layer_norm_fwd_ex",
             lib().mi355x_layer_norm_fwd_ex(

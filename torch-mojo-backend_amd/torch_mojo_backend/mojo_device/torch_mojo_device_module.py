@@ -94,7 +94,10 @@ def _index_of(device) -> int:
 
 def synchronize(device=None) -> None:
     """Wait until every kernel issued on the device has finished."""
+    from ..eager_kernels import flush_pending
+
     idx = _index_of(device)
+    flush_pending()
     if _tensor_mod.storage_kind() == "cuda":
         torch.cuda.synchronize(idx)
 

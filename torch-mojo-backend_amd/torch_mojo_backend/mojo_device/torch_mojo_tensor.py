@@ -221,8 +221,9 @@ class TorchMojoTensor(torch.Tensor):
         """D2H copy into a new CPU tensor (waits for pending device work).
         A bounds error that a kernel flagged since the last host read is
         raised here."""
-        from ..eager_kernels import aten_fast
+        from ..eager_kernels import aten_fast, flush_pending
 
+        flush_pending()  # launches held back for fusion write what is read here
         aten_fast.raise_pending_device_errors()
         src = self._contig()
         out = torch.empty(src._shape, dtype=src._dtype)
