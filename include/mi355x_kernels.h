@@ -160,6 +160,14 @@ enum {
   MI355X_OP_CLAMP_MAX = 103,   /* min(a, s0) */
   MI355X_OP_RSUB = 104,        /* s0 - a*s1 */
 };
+/* out = a + r (f32 sum, as mi355x_map's add) and low = out rounded to
+ * low_dtype (bf16/f16), in one pass over n contiguous elements (n % 4 == 0,
+ * 16-byte aligned f32 vectors).  The gradient sum the autograd engine forms
+ * on a residual stream and the autocast copy of it that the next linear's
+ * backward reads: the reference runs the add (aten_fast.py:2510) and the
+ * cast (_CastSpecExtension, aten_fast.py:1232) as two kernels. */
+int mi355x_add_cast(float* out, void* low, int low_dtype, const float* a, const void* r, int r_dtype,
+                    int64_t n, mi355x_stream_t stream);
 /* out = op(in[0..nin-1]; s0, s1) over `shape`.  `strides` holds (nin+1)
  * stride vectors of `ndim` entries: out first, then each input.  A zero
  * input stride broadcasts; a NULL input pointer reads the scalar s1 instead

@@ -249,6 +249,15 @@ class HostStandIn:
             dense(_val(y_low), DT[low_dt], (rows, cols)).copy_(dense(_val(y), DT[dt], (rows, cols)))
         return 0
 
+    def mi355x_add_cast(self, out, low, low_dt, a, r, r_dt, n, stream):
+        self.add_cast_calls = getattr(self, "add_cast_calls", 0) + 1
+        A = dense(_val(a), torch.float32, (n,))
+        R = dense(_val(r), DT[r_dt], (n,)).float()
+        O = A + R
+        dense(_val(out), torch.float32, (n,)).copy_(O)
+        dense(_val(low), DT[low_dt], (n,)).copy_(O.to(DT[low_dt]))
+        return 0
+
     def mi355x_layer_norm_fwd_add(self, y, y_low, low_dt, mean, rstd, x_out, a, r, r_dt, g, b, rows, cols, eps,
                                   dt, stream):
         self.fused_add_calls = getattr(self, "fused_add_calls", 0) + 1

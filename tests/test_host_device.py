@@ -549,3 +549,21 @@ def test_residual_add_is_fused_into_the_next_layer_norm(mojo):
     s4 = xm + dm
     xm.mul_(0)
     assert torch.equal(s4.cpu(), ref_s)
+
+
+def test_held_back_sum_and_its_autocast_copy_in_one_pass(mojo):
+    """cast_to of a held-back f32 sum (the residual gradient the autograd
+    engine adds up, then cast for the next linear's backward) computes the
+    sum and the bf16 copy together; both match the separate ops."""
+    from torch_mojo_backend import eager_kernels as ek
+    from torch_mojo_backend.eager_kernels import aten_fast
+
+    g = torch.Generator().manual_seed(10)
+    a, r = torch.randn(256, 768, generator=g), torch.randn(256, 768, generator=g)
+    am, rm = a.to("mojo"), r.to("mojo")
+    s = am + rm
+    assert ek._pending
+    low = aten_fast.cast_to(s, torch.bfloat16)
+    assert not ek._pending
+    assert torch.equal(s.cpu(), a + r)
+    assert torch.equal(low.cpu(), (a + r).bfloat16())

@@ -8,6 +8,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "vec.h"
 
 namespace mi {
 namespace {
@@ -421,6 +422,24 @@ __global__ void __launch_bounds__(kThreads) cast_f32_bf16(bf16* __restrict__ out
     ((bf16x8*)out)[i] = r;
   }
 }
+// out = a + r (f32, as binary_x4's add) and low = out rounded to TL, in one
+// pass: the gradient sum the autograd engine forms for a residual stream,
+// and the copy the next autocast linear's backward casts it to.
+template <typename TR, typename TL>
+__global__ void __launch_bounds__(kThreads) add_cast_x4(float* __restrict__ out, TL* __restrict__ low,
+                                                        const float* __restrict__ a, const TR* __restrict__ r,
+                                                        int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kThreads) {
+    const float4 x = ((const float4*)a)[i];
+    const float4 y = ld4<TR, float>(r, i);
+    float4 v;
+    v.x = x.x + y.x; v.y = x.y + y.y; v.z = x.z + y.z; v.w = x.w + y.w;
+    ((float4*)out)[i] = v;
+    float o[4] = {v.x, v.y, v.z, v.w};
+    Vec4<TL>::store(low + 4 * i, o);
+  }
+}
+
 __global__ void __launch_bounds__(kThreads) cast_bf16_f32(float* __restrict__ out,
                                                           const bf16* __restrict__ in,
                                                           int64_t n8) {
@@ -605,6 +624,28 @@ extern "C" int mi355x_arange(void* dst, int dtype, int64_t n, double start, doub
   else
     arange_kernel<int64_t><<<grid_for(n), kThreads, 0, s>>>(dst, dtype, n, start, step);
   return check_launch("mi355x_arange");
+}
+
+extern "C" int mi355x_add_cast(float* out, void* low, int low_dtype, const float* a, const void* r, int r_dtype,
+                               int64_t n, mi355x_stream_t stream) {
+  MI_REQUIRE(n >= 0, "mi355x_add_cast: negative size");
+  if (n == 0) return MI355X_OK;
+  MI_REQUIRE(out && low && a && r, "mi355x_add_cast: null pointer");
+  MI_REQUIRE(low_dtype == MI355X_BF16 || low_dtype == MI355X_F16, "mi355x_add_cast: the copy must be bf16 or f16");
+  MI_REQUIRE(r_dtype == MI355X_F32 || r_dtype == MI355X_BF16, "mi355x_add_cast: r must be f32 or bf16");
+  MI_REQUIRE(n % 4 == 0 && aligned(out, 16) && aligned(a, 16) && aligned(low, 8) &&
+                 aligned(r, r_dtype == MI355X_F32 ? 16 : 8),
+             "mi355x_add_cast: needs a multiple of 4 elements and aligned vectors");
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned grid = grid_for(n / 4, 2);
+  if (r_dtype == MI355X_F32) {
+    if (low_dtype == MI355X_BF16) add_cast_x4<float, bf16><<<grid, kThreads, 0, s>>>(out, (bf16*)low, a, (const float*)r, n / 4);
+    else add_cast_x4<float, f16><<<grid, kThreads, 0, s>>>(out, (f16*)low, a, (const float*)r, n / 4);
+  } else {
+    if (low_dtype == MI355X_BF16) add_cast_x4<bf16, bf16><<<grid, kThreads, 0, s>>>(out, (bf16*)low, a, (const bf16*)r, n / 4);
+    else add_cast_x4<bf16, f16><<<grid, kThreads, 0, s>>>(out, (f16*)low, a, (const bf16*)r, n / 4);
+  }
+  return check_launch("mi355x_add_cast");
 }
 
 extern "C" int mi355x_map(int op, void* out, int out_dtype, int nin, const void* const* ins,

@@ -91,6 +91,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],
     ),
+    "mi355x_add_cast": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_int, c_i64, c_vp]),
     "mi355x_layer_norm_fwd_add": (
         c_int,
         [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],

@@ -267,6 +267,12 @@ def fast_aten__to_copy(
         low = _take_low_copy(t, dtype)
         if low is not None:
             return low
+        if dtype in (torch.bfloat16, torch.float16) and t._dtype == torch.float32:
+            # a held-back residual-gradient sum cast to the autocast dtype
+            # (the autograd engine's cast to a bf16 input's dtype)
+            low = _add_then_cast(t, dtype)
+            if low is not None:
+                return low
     if memory_format in (None, torch.preserve_format):
         out = _empty_like_layout(t, dtype)
     else:
@@ -1507,6 +1513,10 @@ def cast_to(t: MT, dtype) -> MT:
     low = _take_low_copy(t, dtype)
     if low is not None:
         return low
+    if dtype in (torch.bfloat16, torch.float16) and t._dtype == torch.float32:
+        low = _add_then_cast(t, dtype)
+        if low is not None:
+            return low
     if dtype in (torch.bfloat16, torch.float16) and t.requires_grad and t.is_leaf:
         low = _param_low_copy(t, dtype)
         if low is not None:
@@ -1514,6 +1524,25 @@ def cast_to(t: MT, dtype) -> MT:
         t.__dict__[_CAST_DTYPE_ATTR] = dtype
     out = _alloc(t._shape, dtype, t._device)
     return copy_into(out, t)
+
+
+def _add_then_cast(t: MT, dtype):
+    """When t is a held-back f32 sum a + r (f32 or bf16 r), compute it and
+    its `dtype` copy in one pass (mi355x_add_cast) and return the copy."""
+    rec = take_pending(lambda r: r.out._holder is t._holder and r.out._ptr == t._ptr
+                       and tuple(r.out._shape) == tuple(t._shape) and t._is_contiguous)
+    if rec is None:
+        return None
+    ra, rr = rec.inputs
+    if rr._dtype not in (torch.float32, torch.bfloat16):
+        rec.launch()
+        return None
+    low = _alloc(t._shape, dtype, t._device)
+    rc = lib().mi355x_add_cast(t._ptr, low._ptr, _code(dtype), ra._ptr, rr._ptr, _code(rr._dtype), t._numel, _STREAM)
+    if rc:
+        rec.launch()
+        return None
+    return low
 
 
 def _rows_view(t: MT) -> MT:
