@@ -567,3 +567,54 @@ def test_held_back_sum_and_its_autocast_copy_in_one_pass(mojo):
     assert not ek._pending
     assert torch.equal(s.cpu(), a + r)
     assert torch.equal(low.cpu(), (a + r).bfloat16())
+
+
+def test_clip_grad_norm_stacks_the_norms_as_a_view(mojo):
+    """_foreach_norm writes its per-tensor norms into one buffer; the stack
+    that clip_grad_norm_ takes of them is a view of it (no copy).  Norms and
+    clipped gradients match torch; a second stack of the same norms copies."""
+    g = torch.Generator().manual_seed(5)
+    shapes = [(7, 3), (5,), (2, 4, 3), (1,)]
+    grads = [torch.randn(s, generator=g) for s in shapes]
+    ps = [torch.zeros(s).to("mojo").requires_grad_() for s in shapes]
+    for p, gr in zip(ps, grads):
+        p.grad = gr.to("mojo")
+    norms = torch._foreach_norm([p.grad for p in ps])
+    stacked = torch.stack(norms)
+    assert stacked._ptr == norms[0]._ptr and stacked._holder is norms[0]._holder
+    assert torch.allclose(stacked.cpu(), torch.stack([gr.norm() for gr in grads]), rtol=1e-6)
+    again = torch.stack(norms)  # the mark is spent: a copy
+    assert again._holder is not stacked._holder
+    assert torch.equal(again.cpu(), stacked.cpu())
+    total = torch.nn.utils.clip_grad_norm_(ps, 1.0)
+    ref = [gr.clone().requires_grad_() for gr in grads]
+    cpu_ps = [torch.zeros(s, requires_grad=True) for s in shapes]
+    for p, gr in zip(cpu_ps, ref):
+        p.grad = gr.detach().clone()
+    ref_total = torch.nn.utils.clip_grad_norm_(cpu_ps, 1.0)
+    assert torch.allclose(total.cpu(), ref_total, rtol=1e-6)
+    for p, q in zip(ps, cpu_ps):
+        assert torch.allclose(p.grad.cpu(), q.grad, rtol=1e-5, atol=1e-7)
+
+
+def test_adamw_parameter_copies_are_aligned_slices(mojo):
+    """The bf16 parameter copies that one fused AdamW call writes are slices
+    of one allocation, each 256-byte aligned, and equal to the cast of the
+    updated parameter."""
+    from torch_mojo_backend.eager_kernels import aten_fast
+
+    torch.manual_seed(1)
+    model = torch.nn.Sequential(torch.nn.Linear(16, 33), torch.nn.Linear(33, 8)).to("mojo")
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-2, fused=True)
+    x = torch.randn(4, 16).to("mojo")
+    with torch.autocast("mojo", dtype=torch.bfloat16):
+        out = model(x)
+    out.float().sum().backward()
+    opt.step()
+    copies = [p.__dict__.get(aten_fast._PARAM_LOW_ATTR) for p in model.parameters()]
+    assert all(c is not None for c in copies)
+    holders = {id(c[0]._holder) for c in copies}
+    assert len(holders) == 1
+    for p, c in zip(model.parameters(), copies):
+        assert c[0]._ptr % 256 == 0
+        assert torch.equal(c[0].cpu(), p.detach().cpu().bfloat16())

@@ -195,31 +195,40 @@ __global__ void __launch_bounds__(256) splitk_rowsum_reduce(GemmArgs g, int spli
   else rowsum_reduce_body(g, slots, nb, blockIdx.x - nbc, gridDim.x - nbc);
 }
 
-// k-contiguous operand tile: ROWS rows x 64 k, loaded by NT threads.  Thread
-// (wave w, lane l) handles rows r = 8*(it*WAVES + w) + l/8; with WAVES even
-// the swizzled chunk of its slot, (l & 7) ^ ((r >> 1) & 7), is the same for
-// every `it`.  Rows past the operand's end reload its last row (their
-// results are never stored).
-template <int ROWS, int NT>
+// Row swizzle of a k-contiguous tile with BK-element (2*BK-byte) rows: row r
+// stores its 16-byte chunk c in slot c ^ rswz(r).  A fragment read (16 rows
+// at one chunk) then covers every bank once: BK = 64, 8 chunks, rows paired
+// by (r >> 1); BK = 32, 4 chunks, rows grouped by (r >> 2).
+template <int BK>
+__device__ __forceinline__ int rswz(int r) { return BK == 64 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
+
+// k-contiguous operand tile: ROWS rows x BK k, loaded by NT threads, one
+// 1 KB instruction per RPI rows.  Thread (wave w, lane l) handles rows
+// r = RPI*(it*WAVES + w) + l/CPR; with WAVES even the swizzled chunk of its
+// slot, (l % CPR) ^ rswz(r), is the same for every `it`.  Rows past the
+// operand's end reload its last row (their results are never stored).
+template <int ROWS, int NT, int BK>
 struct TileLoad {
+  static constexpr int CPR = BK / 8;    // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;  // rows per 1 KB instruction
   static constexpr int WAVES = NT / 64;
-  static constexpr int ITERS = ROWS / (8 * WAVES);
-  static_assert(WAVES % 2 == 0 && ITERS * 8 * WAVES == ROWS, "tile/thread mismatch");
+  static constexpr int ITERS = ROWS / (RPI * WAVES);
+  static_assert(WAVES % 2 == 0 && ITERS * RPI * WAVES == ROWS, "tile/thread mismatch");
   const char* src[ITERS];  // row base + this lane's chunk, at k = 0
   int chunk;
 
   __device__ __forceinline__ void init(const char* base, int64_t ld_bytes, int64_t row0, int64_t rows) {
     const int lane = threadIdx.x & 63, wave = wave_id();
-    const int r = wave * 8 + (lane >> 3);
-    chunk = (lane & 7) ^ ((r >> 1) & 7);
+    const int r = wave * RPI + lane / CPR;
+    chunk = (lane % CPR) ^ rswz<BK>(r);
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
-      int64_t row = row0 + r + it * 8 * WAVES;
+      int64_t row = row0 + r + it * RPI * WAVES;
       if (row > rows - 1) row = rows - 1;
       src[it] = base + row * ld_bytes + chunk * 16;
     }
   }
-  // KT: the K range may end inside this 64-k slab; a chunk starting past
+  // KT: the K range may end inside this BK slab; a chunk starting past
   // kend_bytes reloads chunk 0 (masked out of the MFMAs, address valid).
   template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0_bytes, char* dst, int64_t kend_bytes) const {
@@ -231,21 +240,21 @@ struct TileLoad {
   }
 };
 
-// m/n-contiguous operand tile: 64 k-rows of ROWS elements, 16-byte chunks
+// m/n-contiguous operand tile: BK k-rows of ROWS elements, 16-byte chunks
 // XOR-swizzled by s(k) = 2 * ((k & 3) | ((k >> 1) & 4)).  A transposing
 // fragment read serves each half-wave from 8 k-rows x 2 adjacent chunks
 // (c, c ^ 1); s takes 8 distinct even values on those k-rows, so the 16
 // (k-row, chunk) pairs land on 16 distinct 16-byte bank groups.
 __device__ __forceinline__ int kswz(int k) { return 2 * ((k & 3) | ((k >> 1) & 4)); }
 
-template <int ROWS, int NT>
+template <int ROWS, int NT, int BK>
 struct TileLoadT {
   static constexpr int ROWB = ROWS * 2;
   static constexpr int CPR = ROWS / 8;     // chunks per k-row
   static constexpr int KPI = 1024 / ROWB;  // k-rows per 1 KB instruction
   static constexpr int WAVES = NT / 64;
-  static constexpr int ITERS = 64 / KPI / WAVES;
-  static_assert(CPR >= 16 && ITERS * KPI * WAVES == 64, "tile/thread mismatch");
+  static constexpr int ITERS = BK / KPI / WAVES;
+  static_assert(CPR >= 16 && ITERS * KPI * WAVES == BK, "tile/thread mismatch");
   const char* base;
   int64_t ld;              // bytes between k-rows
   int64_t col_off[ITERS];  // byte offset of this lane's (clamped) chunk
@@ -279,20 +288,20 @@ struct TileLoadT {
   }
 };
 
-template <int ROWS, int NT, bool K_CONTIG>
+template <int ROWS, int NT, bool K_CONTIG, int BK>
 struct OperandLoad;
-template <int ROWS, int NT>
-struct OperandLoad<ROWS, NT, true> {
-  TileLoad<ROWS, NT> t;
+template <int ROWS, int NT, int BK>
+struct OperandLoad<ROWS, NT, true, BK> {
+  TileLoad<ROWS, NT, BK> t;
   __device__ __forceinline__ void init(const char* b, int64_t ld, int64_t r0, int64_t n) { t.init(b, ld, r0, n); }
   template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0, char* dst, int64_t kend) const {
     t.template issue<KT>(k0 * 2, dst, kend * 2);
   }
 };
-template <int ROWS, int NT>
-struct OperandLoad<ROWS, NT, false> {
-  TileLoadT<ROWS, NT> t;
+template <int ROWS, int NT, int BK>
+struct OperandLoad<ROWS, NT, false, BK> {
+  TileLoadT<ROWS, NT, BK> t;
   __device__ __forceinline__ void init(const char* b, int64_t ld, int64_t r0, int64_t n) { t.init(b, ld, r0, n); }
   template <bool KT>
   __device__ __forceinline__ void issue(int64_t k0, char* dst, int64_t kend) const {
@@ -341,17 +350,25 @@ template <int CFG>
 struct TileCfg;
 template <>
 struct TileCfg<0> {  // C128
-  static constexpr int BM = 128, BN = 128, WGM = 2, WGN = 2, STAGES = GEMM_STAGES_128;
-  static constexpr int MIN_BLOCKS = STAGES * (BM + BN) * 128 * 2 <= 160 * 1024 ? 2 : 1;
+  static constexpr int BM = 128, BN = 128, BK = 64, WGM = 2, WGN = 2, STAGES = GEMM_STAGES_128;
+  static constexpr int MIN_BLOCKS = STAGES * (BM + BN) * BK * 2 * 2 <= 160 * 1024 ? 2 : 1;
 };
 template <>
 struct TileCfg<1> {  // C256
-  static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 4, STAGES = 2, MIN_BLOCKS = 1;
+  static constexpr int BM = 256, BN = 256, BK = 64, WGM = 2, WGN = 4, STAGES = 2, MIN_BLOCKS = 1;
 };
 template <>
 struct TileCfg<2> {  // C192: 128x192, waves of 64x96, 40 KB per stage (k-contiguous B only)
-  static constexpr int BM = 128, BN = 192, WGM = 2, WGN = 2, STAGES = GEMM_STAGES_192;
-  static constexpr int MIN_BLOCKS = STAGES * (BM + BN) * 128 * 2 <= 160 * 1024 ? 2 : 1;
+  static constexpr int BM = 128, BN = 192, BK = 64, WGM = 2, WGN = 2, STAGES = GEMM_STAGES_192;
+  static constexpr int MIN_BLOCKS = STAGES * (BM + BN) * BK * 2 * 2 <= 160 * 1024 ? 2 : 1;
+};
+// C256 in 32-k stages, three deep (96 KB): for weight gradients, whose
+// operands are both m/n-contiguous.  Their transposing fragment reads make
+// a 64-k step long; halving it and keeping two stages in flight hides the
+// loads better (gfx950, cfg 2 shapes: 7-13% over 64-k stages).
+template <>
+struct TileCfg<3> {
+  static constexpr int BM = 256, BN = 256, BK = 32, WGM = 2, WGN = 4, STAGES = 3, MIN_BLOCKS = 1;
 };
 
 // s_waitcnt immediate for vmcnt(n), other counters not waited on.
@@ -458,7 +475,8 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   constexpr int NT = 64 * C::WGM * C::WGN;
   constexpr int WM = BM / C::WGM, WN = BN / C::WGN;
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int A_BYTES = BM * 128, STAGE = A_BYTES + BN * 128, S = C::STAGES;
+  constexpr int BK = C::BK, ROWB = BK * 2;  // k per stage, bytes of a k-contiguous row
+  constexpr int A_BYTES = BM * ROWB, STAGE = A_BYTES + BN * ROWB, S = C::STAGES;
   char* const lds = gemm_smem;
 
   // XCD-aware tile order within one (split, batch) plane.
@@ -490,8 +508,8 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  OperandLoad<BM, NT, A_K> la;
-  OperandLoad<BN, NT, B_K> lb;
+  OperandLoad<BM, NT, A_K, BK> la;
+  OperandLoad<BN, NT, B_K, BK> lb;
   constexpr int PER_STAGE = decltype(la.t)::ITERS + decltype(lb.t)::ITERS;  // DMA instructions per stage
   static_assert(S == 2 || (S - 2) * PER_STAGE < 64, "vmcnt range");
   la.init(A, a_ldb, m0, g.m);
@@ -499,13 +517,13 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   // Prologue: stages 0 .. S-2 in flight.
 #pragma unroll
   for (int st = 0; st < S - 1; ++st) {
-    if (kbeg + st * 64 < kend) {
-      la.template issue<KT>(kbeg + st * 64, lds + st * STAGE, kend);
-      lb.template issue<KT>(kbeg + st * 64, lds + st * STAGE + A_BYTES, kend);
+    if (kbeg + st * BK < kend) {
+      la.template issue<KT>(kbeg + st * BK, lds + st * STAGE, kend);
+      lb.template issue<KT>(kbeg + st * BK, lds + st * STAGE + A_BYTES, kend);
     }
   }
   // k-contiguous fragment rows (.. + lr) share the swizzle of lr
-  const int sw = (lr >> 1) & 7;
+  const int sw = rswz<BK>(lr);
   const int rs_slots = g.part ? g.tiles_n * C::WGN : 1;
   const int rs_slot = g.part ? (int)tn * C::WGN + wn : 0;
   const bool rs_on = RS && (g.part || (tn == 0 && wn == 0));
@@ -518,23 +536,23 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   for (int e = 0; e < 8; ++e) ones[e] = (T)1.0f;
 
   int cur = 0;
-  for (int64_t k0 = kbeg; k0 < kend; k0 += 64) {
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
     // This step's tiles have landed when at most the later stages' loads
     // (S-2 stages, if issued) are still outstanding.
-    if (S > 2 && k0 + (S - 2) * 64 < kend) __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * PER_STAGE));
+    if (S > 2 && k0 + (S - 2) * BK < kend) __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * PER_STAGE));
     else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
-    if (k0 + (S - 1) * 64 < kend) {
+    if (k0 + (S - 1) * BK < kend) {
       // the slot read in the previous step; every wave is past it
       char* nxt = lds + (cur == 0 ? S - 1 : cur - 1) * STAGE;
-      la.template issue<KT>(k0 + (S - 1) * 64, nxt, kend);
-      lb.template issue<KT>(k0 + (S - 1) * 64, nxt + A_BYTES, kend);
+      la.template issue<KT>(k0 + (S - 1) * BK, nxt, kend);
+      lb.template issue<KT>(k0 + (S - 1) * BK, nxt + A_BYTES, kend);
     }
     const char* at = lds + cur * STAGE;
     const char* bt = at + A_BYTES;
-    const bool tail = KT && k0 + 64 > kend;
+    const bool tail = KT && k0 + BK > kend;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < BK / 32; ++ks) {
       const bool rs_now = rs_on && rs_q == rs_slot;
       if (RS && ++rs_q == rs_slots) rs_q = 0;
       const int coff = ((ks * 4 + lg) ^ sw) * 16;
@@ -544,13 +562,13 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
       if constexpr (!A_K) mn_frags<T, BM, TM>(at, wm * WM, ks, afr);
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        if constexpr (B_K) bfr[j] = *(const frag*)(bt + (wn * WN + j * 16 + lr) * 128 + coff);
+        if constexpr (B_K) bfr[j] = *(const frag*)(bt + (wn * WN + j * 16 + lr) * ROWB + coff);
         if (tail) mask_k(bfr[j], kfrag, kend);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         frag af;
-        if constexpr (A_K) af = *(const frag*)(at + (wm * WM + i * 16 + lr) * 128 + coff);
+        if constexpr (A_K) af = *(const frag*)(at + (wm * WM + i * 16 + lr) * ROWB + coff);
         else af = afr[i];
         if (tail) mask_k(af, kfrag, kend);
         if (RS && rs_now) rsum[i] = Mfma<T>::mma(af, ones, rsum[i]);
@@ -761,19 +779,21 @@ __global__ void __launch_bounds__(256) gemm_f32(GemmArgs g) {
 // planning
 // ---------------------------------------------------------------------------
 struct Plan {
-  int cfg;  // 0 = C128, 1 = C256, 2 = C192
+  int cfg;  // 0 = C128, 1 = C256, 2 = C192, 3 = C256 in 32-k stages
   int splits;
   int64_t kchunk;
 };
 
 int64_t tiles_of(int cfg, int64_t batch, int64_t m, int64_t n) {
-  const int64_t bm = cfg == 1 ? 256 : 128, bn = cfg == 1 ? 256 : (cfg == 2 ? 192 : 128);
+  const bool c256 = cfg == 1 || cfg == 3;
+  const int64_t bm = c256 ? 256 : 128, bn = c256 ? 256 : (cfg == 2 ? 192 : 128);
   return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch;
 }
 
 // Row-sum partial slots per split: one per wave column of every column tile.
 int64_t rs_slots_of(int cfg, int64_t n) {
-  const int64_t bn = cfg == 1 ? 256 : (cfg == 2 ? 192 : 128), wgn = cfg == 1 ? 4 : 2;
+  const bool c256 = cfg == 1 || cfg == 3;
+  const int64_t bn = c256 ? 256 : (cfg == 2 ? 192 : 128), wgn = c256 ? 4 : 2;
   return (n + bn - 1) / bn * wgn;
 }
 
@@ -782,9 +802,10 @@ int64_t rs_slots_of(int cfg, int64_t n) {
 // per-round time measured on gfx950 at K = 768..3072 (a C256 round does
 // twice a C128 round's work in 1.82x its time).  An m-contiguous A (a weight
 // gradient dY^T X) reads both operands through transposing LDS reads, which
-// C256 tiles halve per flop: when its C256 tiles fill the CUs it takes them
-// (the 50304 x 768 embedding gradient: 1.72 -> 1.53 ms).  Then split K when
-// the output alone cannot fill the chip.
+// C256 tiles halve per flop: when both sides span a 256 tile it takes them,
+// in 32-k stages (the 50304 x 768 embedding gradient: 1.53 -> 1.35 ms, the
+// 768 x 3072 one 105 -> 84 us with 7 K splits).  Then split K when the
+// output alone cannot fill the chip.
 Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool a_kcontig, bool b_kcontig) {
   Plan best{0, 1, k};
   const int64_t t128 = tiles_of(0, batch, m, n), t256 = tiles_of(1, batch, m, n), t192 = tiles_of(2, batch, m, n);
@@ -794,17 +815,19 @@ Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool a_kcontig, b
   double cbest = c128;
   if (t256 >= kCUs && c256 < cbest) best.cfg = 1, cbest = c256;
   if (b_kcontig && t192 >= kCUs && c192 < cbest) best.cfg = 2, cbest = c192;
-  if (!a_kcontig && t256 >= kCUs) best.cfg = 1;
-  static const char* forced = getenv("MI355X_GEMM_TILE");  // tuning override: "128", "192" or "256"
+  // (measured exception: the 3072 x 768 fc weight gradient, m = 4n, runs
+  // faster as split-K C128: 940 against 850 TF/s)
+  if (!a_kcontig && m >= 256 && n >= 256 && (m < 4 * n || t256 >= kCUs)) best.cfg = 3;
+  static const char* forced = getenv("MI355X_GEMM_TILE");  // tuning override: "128", "192", "256" or "256.32"
   if (forced) {
-    const int f = atoi(forced);
-    best.cfg = f == 256 ? 1 : (f == 192 && b_kcontig ? 2 : 0);
+    const double f = atof(forced);
+    best.cfg = f == 256 ? 1 : (f > 256 && !a_kcontig ? 3 : (f == 192 && b_kcontig ? 2 : 0));
   }
   const int64_t tiles = tiles_of(best.cfg, batch, m, n);
   if (tiles < kCUs && k >= 2048) {
     // as many K splits as keep every block in the first round of block
     // slots: a second, partly filled round would double the time
-    const int64_t slots = best.cfg == 1 ? kCUs : 2 * kCUs;  // block slots of the chosen config
+    const int64_t slots = best.cfg == 1 || best.cfg == 3 ? kCUs : 2 * kCUs;  // block slots of the chosen config
     int64_t s = slots / tiles;
     const int64_t max_s = k / 512;
     if (s > max_s) s = max_s;
@@ -825,7 +848,7 @@ template <typename T, int CFG, bool A_K, bool B_K, bool KT, bool RS>
 int launch_kernel(const GemmArgs& g, dim3 grid, hipStream_t s) {
   typedef TileCfg<CFG> C;
   constexpr int NT = 64 * C::WGM * C::WGN;
-  constexpr size_t lds = C::STAGES * (size_t)(C::BM + C::BN) * 128;
+  constexpr size_t lds = C::STAGES * (size_t)(C::BM + C::BN) * C::BK * 2;
   static bool attr = false;
   if (lds > 65536 && !attr) {
     if (hipFuncSetAttribute((const void*)gemm_tile<T, CFG, A_K, B_K, KT, RS>,
@@ -840,7 +863,11 @@ int launch_kernel(const GemmArgs& g, dim3 grid, hipStream_t s) {
 template <typename T, int CFG, bool KT, bool RS>
 int launch_layout(const GemmArgs& g, dim3 grid, hipStream_t s) {
   const bool ak = g.a_cs == 1, bk = g.b_rs == 1;
-  if constexpr (CFG == 2) {  // 192-wide B tiles are only loaded k-contiguous
+  if constexpr (CFG == 3) {  // chosen for m-contiguous A only
+    if (ak) return fail(MI355X_EINVAL, "mi355x_gemm: 32-k C256 tiles take an m-contiguous A");
+    if (bk) return launch_kernel<T, CFG, false, true, KT, RS>(g, grid, s);
+    return launch_kernel<T, CFG, false, false, KT, RS>(g, grid, s);
+  } else if constexpr (CFG == 2) {  // 192-wide B tiles are only loaded k-contiguous
     if (!bk) return fail(MI355X_EINVAL, "mi355x_gemm: 128x192 tiles need a k-contiguous B");
     if (ak) return launch_kernel<T, CFG, true, true, KT, RS>(g, grid, s);
     return launch_kernel<T, CFG, false, true, KT, RS>(g, grid, s);
@@ -902,6 +929,7 @@ int launch_mfma(GemmArgs g, int64_t batch, const Plan& p, hipStream_t s) {
   const bool kt = g.k % 64 != 0;
   int rc;
   if (p.cfg == 1) rc = kt ? launch_tile<T, 1, true>(g, batch, p.splits, s) : launch_tile<T, 1, false>(g, batch, p.splits, s);
+  else if (p.cfg == 3) rc = kt ? launch_tile<T, 3, true>(g, batch, p.splits, s) : launch_tile<T, 3, false>(g, batch, p.splits, s);
   else if (p.cfg == 2) rc = kt ? launch_tile<T, 2, true>(g, batch, p.splits, s) : launch_tile<T, 2, false>(g, batch, p.splits, s);
   else rc = kt ? launch_tile<T, 0, true>(g, batch, p.splits, s) : launch_tile<T, 0, false>(g, batch, p.splits, s);
   if (rc || !g.part) return rc;

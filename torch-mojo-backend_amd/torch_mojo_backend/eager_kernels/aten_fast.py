@@ -753,17 +753,19 @@ def _binary(name, a, b, alpha=1, *, out=None, inplace=False, mode=None):
         opcode = OP["div_trunc"]
     elif name == "div" and mode == "floor":
         opcode = OP["div_floor"]
-    # result dtype by torch's promotion rules (scalars are "wrapped numbers")
-    ra = a if isinstance(a, torch.Tensor) else a
-    rb = b if isinstance(b, torch.Tensor) else b
-    rtype = torch.result_type(ra, rb)
+    # result dtype by torch's promotion rules (scalars are "wrapped numbers";
+    # two tensors of rank >= 1 promote by dtype alone)
+    if ta is not None and tb is not None and sha and shb:
+        rtype = torch.promote_types(da, db)
+    else:
+        rtype = torch.result_type(a, b)
     if name in _COMPARE:
         out_dtype = torch.bool
     elif name in _FLOAT_RESULT and mode is None and not rtype.is_floating_point:
         out_dtype = torch.get_default_dtype()
     else:
         out_dtype = rtype
-    shape = tuple(torch.broadcast_shapes(sha, shb))
+    shape = tuple(sha) if tuple(sha) == tuple(shb) else tuple(torch.broadcast_shapes(sha, shb))
     if inplace:
         target = ta
         if tuple(target._shape) != shape:
@@ -1159,6 +1161,26 @@ def _cat_in_place(ts, d, shape):
     return MT._view_of(first, tuple(shape), tuple(strides), first._offset, True)
 
 
+def _stack_in_place(ts):
+    """A view of the buffer when `ts` are equal-shape contiguous slices of
+    one cat-ready buffer lying one after the other (the per-tensor results
+    of `_foreach_norm`), i.e. already laid out as their stack along dim 0,
+    else None.  The mark is consumed."""
+    first = ts[0]
+    holder = first._holder
+    if not getattr(holder, _CAT_READY, False) or not first._is_contiguous:
+        return None
+    shape, step, off = first._shape, first._numel, first._offset
+    for x in ts:
+        if (x._holder is not holder or x._offset != off or x._shape != shape or x._dtype != first._dtype
+                or not x._is_contiguous):
+            return None
+        off += step
+    setattr(holder, _CAT_READY, False)
+    out_shape = (len(ts),) + tuple(shape)
+    return MT._view_of(first, out_shape, row_major_strides(out_shape), first._offset, True)
+
+
 def fast_aten_cat(tensors, dim=0):
     ts = [_require(x) for x in tensors]
     ts_nonempty = [x for x in ts if not (len(x._shape) == 1 and x._shape[0] == 0)]
@@ -1225,6 +1247,10 @@ def fast_aten_cat(tensors, dim=0):
 def fast_aten_stack(tensors, dim=0):
     ts = [_require(x) for x in tensors]
     d = _norm_dim(dim, len(ts[0]._shape) + 1)
+    if d == 0:
+        view = _stack_in_place(ts)
+        if view is not None:
+            return view
     return fast_aten_cat([fast_aten_unsqueeze(x, d) for x in ts], d)
 
 
@@ -2356,9 +2382,9 @@ def fast_aten__fused_adamw_(
         raise RuntimeError("_fused_adamw_: all tensor lists must have the same length")
     if amsgrad and len(max_exp_avg_sqs) != n:
         raise RuntimeError("_fused_adamw_: max_exp_avg_sqs must match params when amsgrad=True")
-    descs = (AdamWTensor * n)()
     f32 = torch.float32
     P, G, M, V, S = ([_require(t) for t in lst] for lst in lists)
+    fields = []  # AdamWTensor records, flattened (seven 8-byte fields each)
     for i in range(n):
         p, g, m, v, s = P[i], G[i], M[i], V[i], S[i]
         pn = p._numel
@@ -2370,19 +2396,18 @@ def fast_aten__fused_adamw_(
             raise RuntimeError(f"_fused_adamw_: {name} {i} has {t._numel} elements, param has {pn}")
         if s._dtype != f32 or s._numel != 1:
             return NOT_HANDLED
-        d = descs[i]
-        d.param, d.grad, d.exp_avg, d.exp_avg_sq = p._ptr, g._ptr, m._ptr, v._ptr
+        mx_ptr = 0
         if amsgrad:
             mx = _require(max_exp_avg_sqs[i])
             if mx._dtype != f32 or not mx._is_contiguous:
                 return NOT_HANDLED
             if mx._numel != pn:
                 raise RuntimeError(f"_fused_adamw_: max_exp_avg_sq {i} has {mx._numel} elements, param has {pn}")
-            d.max_exp_avg_sq = mx._ptr
-        else:
-            d.max_exp_avg_sq = None
-        d.step = s._ptr
-        d.numel = pn
+            mx_ptr = mx._ptr
+        fields += (p._ptr, g._ptr, m._ptr, v._ptr, mx_ptr, s._ptr, pn)
+    assert ctypes.sizeof(AdamWTensor) == 7 * 8
+    raw = (ctypes.c_uint64 * len(fields))(*fields)
+    descs = (AdamWTensor * n).from_buffer(raw)
     lr_t = _t(lr)
     lr_value = 0.0 if lr_t is not None else float(lr)
     if lr_t is not None and lr_t._dtype != torch.float32:
@@ -2397,11 +2422,23 @@ def fast_aten__fused_adamw_(
     # parameters the autocast forward casts get their 16-bit copy from this step
     low_dt = None
     lows = [None] * n
+    take = []
     for i, prm in enumerate(params):
         dt = prm.__dict__.get(_CAST_DTYPE_ATTR) if hasattr(prm, "__dict__") else None
         if dt is not None and (low_dt is None or dt == low_dt):
             low_dt = dt
-            lows[i] = _alloc(prm._shape, dt, prm._device)
+            take.append(i)
+    if take:
+        # the copies are slices of one allocation, each 256-byte aligned
+        align = 256 // low_dt.itemsize
+        offs, total = [], 0
+        for i in take:
+            offs.append(total)
+            total += -(-P[i]._numel // align) * align
+        buf = _alloc((total,), low_dt, P[take[0]]._device)
+        for i, off in zip(take, offs):
+            shp = P[i]._shape
+            lows[i] = MT._view_of(buf, shp, row_major_strides(shp), off, True)
     low_ptrs = (ctypes.c_void_p * n)(*[x._ptr if x is not None else None for x in lows]) if low_dt else None
     check(
         "mi355x_fused_adamw_ex",
@@ -2477,9 +2514,13 @@ def fast_aten__foreach_norm(self, ord=2, dtype=None):
         return NOT_HANDLED
     n = len(ts)
     out_dtype = dtype or ts[0]._dtype
-    outs = [_alloc((), out_dtype, ts[0]._device) for _ in range(n)]
     if n == 0:
-        return outs
+        return []
+    # one buffer, one 0-d view per tensor: the stack of the norms that
+    # clip_grad_norm_ takes next is then a view of it
+    buf = _alloc((n,), out_dtype, ts[0]._device)
+    _mark_cat_ready(buf)
+    outs = [MT._view_of(buf, (), (), i, True) for i in range(n)]
     numels = _i64([t._numel for t in ts])
     ws = lib().mi355x_foreach_norm_workspace_bytes(numels, n)
     hold, wptr = _workspace(ws, ts[0]._device)

@@ -124,16 +124,28 @@ def _alloc_bytes(nbytes: int, device: int) -> torch.Tensor:
         return torch.empty(size, dtype=torch.uint8, device=dev)
 
 
+_DISPATCH = None
+
+
+def _dispatch_module():
+    """The dispatch module, imported on first use (it imports this one)."""
+    global _DISPATCH
+    if _DISPATCH is None:
+        from . import dispatch
+
+        _DISPATCH = dispatch
+    return _DISPATCH
+
+
 class TorchMojoTensor(torch.Tensor):
     """Eager mojo tensor (storage-less PrivateUse1 wrapper subclass)."""
 
     @classmethod
     def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
-        if not all(issubclass(cls, t) for t in types):
-            return NotImplemented
-        from .dispatch import dispatch
-
-        return dispatch(func, args, kwargs or {})
+        for t in types:
+            if not issubclass(cls, t):
+                return NotImplemented
+        return _dispatch_module().dispatch(func, args, kwargs or {})
 
     __torch_function__ = torch._C._disabled_torch_function_impl
 
