@@ -388,7 +388,7 @@ typedef struct mi355x_adamw_tensor {
 #define MI355X_ADAMW_MAXIMIZE 2
 /* torch.optim AdamW (decoupled weight decay) over n tensors.  lr_ptr (if
  * not NULL) overrides lr; grad_scale divides grads; a nonzero *found_inf
- * skips the update.  Any n (batched 32 tensors per launch). */
+ * skips the update.  Any n (batched 160 tensors per launch). */
 int mi355x_fused_adamw(const mi355x_adamw_tensor* tensors, int n, double lr,
                        const float* lr_ptr, double beta1, double beta2,
                        double weight_decay, double eps, int flags,

@@ -4,7 +4,7 @@
 // All three use the same launch shape: up to kBatch tensors per launch,
 // described in the kernel arguments, each split into fixed-size chunks; the
 // grid is the total chunk count and a block locates its (tensor, chunk) by a
-// scan of the chunk prefix sums.  Contiguous f32 data moves as float4.
+// binary search over the chunk prefix sums.  Contiguous f32 data moves as float4.
 //
 // AdamW (torch.optim.AdamW, decoupled weight decay), per element:
 //   g = maximize ? -g : g;  g /= grad_scale (if given)
@@ -25,7 +25,10 @@ namespace mi {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kAdamBatch = 32;
+// Tensors per launch.  The batch descriptors travel as kernel arguments
+// (up to ~12 KB here; gfx950 kernels take at least 16 KB), so a GPT-2 sized
+// parameter list updates in one launch per parameter group.
+constexpr int kAdamBatch = 160;
 constexpr int64_t kAdamChunk = 16384;
 
 struct AdamBatch {
@@ -35,10 +38,16 @@ struct AdamBatch {
   int n;
 };
 
+// The tensor whose chunk range [starts[k], starts[k+1]) holds `chunk`
+// (binary search; empty tensors have empty ranges and are never returned).
 __device__ __forceinline__ int find_tensor(const int64_t* starts, int n, int64_t chunk) {
-  int k = 0;
-  while (k + 1 < n && starts[k + 1] <= chunk) ++k;
-  return k;
+  int lo = 0, hi = n - 1;  // starts[lo] <= chunk < starts[hi + 1]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (starts[mid] <= chunk) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
 }
 
 struct AdamScalars {
@@ -155,7 +164,7 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
 // ---------------------------------------------------------------------------
 // foreach norm
 // ---------------------------------------------------------------------------
-constexpr int kNormBatch = 64;
+constexpr int kNormBatch = 160;
 constexpr int64_t kNormChunk = 32768;
 
 struct NormBatch {
@@ -245,7 +254,7 @@ __global__ void __launch_bounds__(kThreads) norm_final(NormBatch b, int kind, co
 // ---------------------------------------------------------------------------
 // foreach apply
 // ---------------------------------------------------------------------------
-constexpr int kApplyBatch = 40;
+constexpr int kApplyBatch = 160;
 constexpr int64_t kApplyChunk = 16384;
 
 struct ApplyBatch {
