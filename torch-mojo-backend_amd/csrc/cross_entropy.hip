@@ -201,13 +201,18 @@ __device__ __forceinline__ uint4 shift_pair(uint4 lo, uint4 hi, int bytes) {
   return o;
 }
 
+// The backward writes every element of the row: 1024 threads, one 16-byte
+// output chunk each per iteration (gfx950, [16384, 50257] bf16: 0.687 ms
+// with 256 threads x 2 chunks, 0.604 ms like this).
+constexpr int kBwdThreads = 1024;
+
 template <typename T, typename TD>
-__global__ void __launch_bounds__(kRowThreads)
+__global__ void __launch_bounds__(kBwdThreads)
     ce_bwd_rows(TD* __restrict__ dx, int64_t ld_dx, const T* __restrict__ x, int64_t ld,
                 const float* __restrict__ lse, const int64_t* __restrict__ target,
                 const float* __restrict__ grad, int grad_per_row, const float* __restrict__ total,
                 int64_t n, int64_t c, int64_t ignore_index) {
-  constexpr int V = Chunk<T>::V, U = 2;
+  constexpr int V = Chunk<T>::V, U = 1;
   static_assert(sizeof(TD) == sizeof(T), "dx chunks follow the logits chunks");
   const int64_t row = blockIdx.x;
   const int64_t tg = target[row];
@@ -223,11 +228,11 @@ __global__ void __launch_bounds__(kRowThreads)
   uint4* o = (uint4*)(dx + row * ld_dx);
   const int nout = (int)(ld_dx / V);
   // U output chunks per thread per iteration, their loads issued first
-  for (int t0 = threadIdx.x; t0 < nout; t0 += kRowThreads * U) {
+  for (int t0 = threadIdx.x; t0 < nout; t0 += kBwdThreads * U) {
     uint4 lo[U], hi[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * kRowThreads;
+      const int t = t0 + u * kBwdThreads;
       lo[u] = hi[u] = make_uint4(0, 0, 0, 0);
       if (t * V < ci) {
         lo[u] = geo.base[t];
@@ -236,7 +241,7 @@ __global__ void __launch_bounds__(kRowThreads)
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * kRowThreads;
+      const int t = t0 + u * kBwdThreads;
       if (t >= nout) break;
       const int k0 = t * V;
       Chunk<T> ch;
@@ -312,7 +317,7 @@ extern "C" int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx, c
   const int per_row = reduction == 0;
   const float* tw = reduction == 1 ? total_weight : nullptr;
 #define CE_BWD(TX, TD)                                                                                   \
-  ce_bwd_rows<TX, TD><<<(unsigned)n, kRowThreads, 0, s>>>((TD*)dx, ld_dx, (const TX*)logits, ld, lse, \
+  ce_bwd_rows<TX, TD><<<(unsigned)n, kBwdThreads, 0, s>>>((TD*)dx, ld_dx, (const TX*)logits, ld, lse, \
                                                           target, grad_out, per_row, tw, n, c,       \
                                                           ignore_index)
   if (dtype == MI355X_BF16 && dx_dtype == MI355X_BF16) CE_BWD(bf16, bf16);

