@@ -403,14 +403,19 @@ __device__ __forceinline__ void store_tile(CT* __restrict__ C, int c_rs, const f
 }
 
 // Full wave tiles without beta: the accumulators go through a per-wave LDS
-// slab 16 rows at a time (one MFMA row of tiles, f32, rows padded by 2
+// slab 16 rows at a time (one MFMA row of tiles, f32, rows padded by 4
 // floats) and leave as row-contiguous 16-byte stores: 8 bf16/f16 or 4 f32
-// per lane instead of one element per store.  The slab holds 16 x (WN + 2)
+// per lane instead of one element per store.  The slab holds 16 x (WN + 4)
 // floats; `lane` is the wave lane.  Requires 16-byte aligned rows of C.
 template <typename CT, typename T, bool ROUND, int TM, int TN>
 __device__ __forceinline__ void store_tile_lds(CT* __restrict__ C, int c_rs, const f32x4 (&acc)[TM][TN],
                                                const float (&bias)[TN], float* slab, int lr, int lg, int lane) {
-  constexpr int WN = TN * 16, LD = WN + 2;       // slab row stride in floats
+#ifndef GEMM_SLAB_PAD
+#define GEMM_SLAB_PAD 4
+#endif
+  // slab row stride in floats: 4 * LD = 16 (mod 64) puts the four 16-lane
+  // groups of a store (rows lg*4 + e) on disjoint banks
+  constexpr int WN = TN * 16, LD = WN + GEMM_SLAB_PAD;
   constexpr int E = 16 / sizeof(CT);             // elements per 16-byte store
   constexpr int CHUNKS = 16 * WN / E;            // 16-byte chunks per 16-row slab
   static_assert(WN % E == 0 && CHUNKS % 64 == 0, "slab shape");
@@ -581,7 +586,7 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
 
   // every wave is past its last LDS read: the stages become store slabs
   __syncthreads();
-  float* const slab = (float*)lds + wave * (16 * (WN + 2));
+  float* const slab = (float*)lds + wave * (16 * (WN + GEMM_SLAB_PAD));
   const int64_t row0 = m0 + wm * WM, col0 = n0 + wn * WN;
   if (RS && rs_on && lr == 0) {
     // lane (lg, 0) holds rows 4*lg .. 4*lg+3 of each 16-row fragment
