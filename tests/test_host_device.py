@@ -618,3 +618,32 @@ def test_adamw_parameter_copies_are_aligned_slices(mojo):
     for p, c in zip(model.parameters(), copies):
         assert c[0]._ptr % 256 == 0
         assert torch.equal(c[0].cpu(), p.detach().cpu().bfloat16())
+
+
+def test_held_back_gradient_sum_becomes_the_leaf_grad_without_a_copy(mojo):
+    """A parameter used twice gets the sum of its two gradients; that sum is
+    a held-back add (large f32, same shape).  The record keeps only the
+    storages, so autograd takes the sum as .grad as is (no clone) and the
+    value matches torch."""
+    from torch_mojo_backend.mojo_device import dispatch as D
+
+    g = torch.Generator().manual_seed(6)
+    w = torch.randn(512, 256, generator=g)
+    x, z = torch.randn(8, 256, generator=g), torch.randn(8, 256, generator=g)
+    wm = w.to("mojo").requires_grad_()
+    seen = []
+    orig = D.dispatch
+
+    def spy(func, args, kwargs):
+        seen.append(str(func))
+        return orig(func, args, kwargs)
+
+    D.dispatch = spy
+    try:
+        ((x.to("mojo") @ wm.t()).sum() + (z.to("mojo") @ wm.t() * 2.0).sum()).backward()
+    finally:
+        D.dispatch = orig
+    wc = w.clone().requires_grad_()
+    ((x @ wc.t()).sum() + (z @ wc.t() * 2.0).sum()).backward()
+    assert torch.allclose(wm.grad.cpu(), wc.grad, atol=1e-5, rtol=1e-5)
+    assert "aten.copy_.default" not in seen, seen

@@ -800,10 +800,27 @@ def _binary(name, a, b, alpha=1, *, out=None, inplace=False, mode=None):
     if name == "add" and not inplace and out is None and s0 == 1.0 and _residual_add(res, ta, tb):
         # x + f(...) of a pre-norm block: held back so that the LayerNorm
         # reading the sum can compute it in the same pass (any other
-        # consumer issues it first)
-        defer(Deferred(res, (ta, tb), lambda: _map_call(opcode, res, [(ta, da), (tb, db)], s0, 0.0)))
+        # consumer issues it first).  The record keeps the storages, not
+        # the tensors: a held reference to the sum would stop autograd from
+        # taking it as a leaf's .grad without a copy.
+        r_out, r_a, r_b = _Ref(res), _Ref(ta), _Ref(tb)
+        defer(Deferred(r_out, (r_a, r_b), lambda: _map_call(opcode, r_out, [(r_a, da), (r_b, db)], s0, 0.0)))
         return res
     return _map_call(opcode, res, [(ta, da), (tb, db)], s0, 0.0)
+
+
+class _Ref:
+    """What a held-back launch needs of a mojo tensor (pointer, layout,
+    dtype, and the storage holder that keeps the memory alive), without a
+    reference to the tensor object itself."""
+
+    __slots__ = ("_holder", "_ptr", "_shape", "_strides", "_offset", "_dtype", "_numel", "_is_contiguous",
+                 "_device", "_itemsize")
+
+    def __init__(self, t: MT):
+        self._holder, self._ptr, self._shape, self._strides = t._holder, t._ptr, t._shape, t._strides
+        self._offset, self._dtype, self._numel = t._offset, t._dtype, t._numel
+        self._is_contiguous, self._device, self._itemsize = t._is_contiguous, t._device, t._itemsize
 
 
 _RESIDUAL_MIN_NUMEL = 1 << 16
