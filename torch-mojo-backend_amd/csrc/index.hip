@@ -10,14 +10,16 @@
 // ATen's CPU kernel computes as an index_add in index order):
 //   1. stable radix sort of (idx[n], n) pairs -> positions grouped by row,
 //      ascending within each row;
-//   2. one block per weight row binary-searches its segment and sums the
-//      grad rows in that order into f32, then writes the row once.
+//   2. one wave per weight row finds its segment (a wave-wide 64-ary search)
+//      and sums the grad rows in that order into f32, then writes the row
+//      once.
 // Every weight row is written exactly once (no zero pre-pass, no atomics),
 // and the per-row summation order equals the sequential CPU order, so f32
 // results match ATen's CPU result bit for bit.
 #include <hipcub/hipcub.hpp>
 
 #include "common.h"
+#include "vec.h"
 
 namespace mi {
 namespace {
@@ -76,34 +78,62 @@ __global__ void iota_i32(int32_t* v, int64_t n) {
   if (i < n) v[i] = (int32_t)i;
 }
 
-// One block per weight row (grid-stride): ordered segment sum.
+// First index in [0, n) whose sorted key is >= target (n if none), found by
+// the whole wave: each round the 64 lanes probe 64 evenly spaced keys and a
+// ballot narrows the range 64-fold, so a search of n = 16384 keys costs
+// three dependent loads instead of fourteen.  Wave-uniform result.
+__device__ __forceinline__ int64_t wave_lower_bound(const int64_t* __restrict__ keys, int64_t n,
+                                                     int64_t target, int lane) {
+  int64_t lo = 0, hi = n;  // the answer lies in [lo, hi]
+  while (hi - lo > 64) {
+    const int64_t step = (hi - lo + 63) / 64;
+    const int64_t i = lo + (int64_t)lane * step;
+    const bool ge = i >= hi || keys[i] >= target;
+    const uint64_t m = __ballot(ge);
+    const int f = m ? __ffsll((unsigned long long)m) - 1 : 64;  // first probe >= target
+    const int64_t nlo = f == 0 ? lo : lo + (int64_t)(f - 1) * step + 1;
+    const int64_t nhi = f == 64 ? hi : min(hi, lo + (int64_t)f * step);
+    lo = nlo;
+    hi = nhi;
+  }
+  const int64_t i = lo + lane;
+  const bool ge = i >= hi || keys[i] >= target;
+  const uint64_t m = __ballot(ge);
+  return m ? lo + (__ffsll((unsigned long long)m) - 1) : hi;
+}
+
+// One wave per weight row (four rows per block, grid-stride): ordered
+// segment sum.  Each lane owns a fixed set of columns and adds the row's
+// grad rows in sorted (= index) order, 16 bytes at a time when the row
+// allows it.
 template <typename T>
 __global__ void __launch_bounds__(kThreads)
     embedding_bwd_rows(T* __restrict__ gw, const T* __restrict__ go,
                        const int64_t* __restrict__ keys, const int32_t* __restrict__ pos,
-                       int64_t n, int64_t num_weights, int64_t dim, int64_t padding_idx) {
-  for (int64_t row = blockIdx.x; row < num_weights; row += gridDim.x) {
-    // lower_bound(row), upper_bound(row) in the sorted keys
-    int64_t lo = 0, hi = n;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
-      if (keys[mid] < row) lo = mid + 1; else hi = mid;
-    }
-    int64_t end = lo;
-    {
-      int64_t l2 = lo, h2 = n;
-      while (l2 < h2) {
-        const int64_t mid = (l2 + h2) >> 1;
-        if (keys[mid] <= row) l2 = mid + 1; else h2 = mid;
+                       int64_t n, int64_t num_weights, int64_t dim, int64_t padding_idx, bool vec4) {
+  const int lane = threadIdx.x & 63;
+  constexpr int RPB = kThreads / 64;
+  for (int64_t row = (int64_t)blockIdx.x * RPB + (threadIdx.x >> 6); row < num_weights;
+       row += (int64_t)gridDim.x * RPB) {
+    const int64_t lo = wave_lower_bound(keys, n, row, lane);
+    const int64_t end = row == padding_idx ? lo : wave_lower_bound(keys, n, row + 1, lane);
+    if (vec4) {
+      for (int64_t c = (int64_t)lane * 4; c < dim; c += 64 * 4) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int64_t k = lo; k < end; ++k) {
+          float v[4];
+          Vec4<T>::load(go + (int64_t)pos[k] * dim + c, v);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] += v[e];
+        }
+        Vec4<T>::store(gw + row * dim + c, acc);
       }
-      end = l2;
-    }
-    const bool skip = row == padding_idx;
-    for (int64_t c = threadIdx.x; c < dim; c += kThreads) {
-      float acc = 0.f;
-      if (!skip)
+    } else {
+      for (int64_t c = lane; c < dim; c += 64) {
+        float acc = 0.f;
         for (int64_t k = lo; k < end; ++k) acc += to_f32(go[(int64_t)pos[k] * dim + c]);
-      gw[row * dim + c] = from_f32<T>(acc);
+        gw[row * dim + c] = from_f32<T>(acc);
+      }
     }
   }
 }
@@ -182,16 +212,19 @@ extern "C" int mi355x_embedding_bwd(void* grad_weight, const void* grad_out, int
                                                       (int)n_idx, 0, 64, s);
     if (e != hipSuccess) return fail(MI355X_ELAUNCH, "mi355x_embedding_bwd: sort failed: %s", hipGetErrorString(e));
   }
-  int64_t grid = num_weights < 65536 ? num_weights : 65536;
+  const int64_t blocks = (num_weights + kThreads / 64 - 1) / (kThreads / 64);
+  const unsigned grid = (unsigned)(blocks < 65536 ? blocks : 65536);
+  const size_t es = (size_t)dtype_size(dtype);
+  const bool vec4 = dim % 4 == 0 && ((uintptr_t)grad_weight % (4 * es)) == 0 && ((uintptr_t)grad_out % (4 * es)) == 0;
   switch (dtype) {
     case MI355X_F32:
-      embedding_bwd_rows<float><<<(unsigned)grid, kThreads, 0, s>>>((float*)grad_weight, (const float*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx);
+      embedding_bwd_rows<float><<<grid, kThreads, 0, s>>>((float*)grad_weight, (const float*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx, vec4);
       break;
     case MI355X_BF16:
-      embedding_bwd_rows<bf16><<<(unsigned)grid, kThreads, 0, s>>>((bf16*)grad_weight, (const bf16*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx);
+      embedding_bwd_rows<bf16><<<grid, kThreads, 0, s>>>((bf16*)grad_weight, (const bf16*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx, vec4);
       break;
     case MI355X_F16:
-      embedding_bwd_rows<f16><<<(unsigned)grid, kThreads, 0, s>>>((f16*)grad_weight, (const f16*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx);
+      embedding_bwd_rows<f16><<<grid, kThreads, 0, s>>>((f16*)grad_weight, (const f16*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx, vec4);
       break;
     default:
       return fail(MI355X_EUNSUPPORTED, "mi355x_embedding_bwd: unsupported dtype %d", dtype);
