@@ -254,7 +254,7 @@ def test_attention_cfg1_shape_properties(kernels):
 @pytest.mark.parametrize("m,n,k,layout,batch", [(2304, 768, 16384, "TN", 1), (300, 200, 1001, "NT", 1),
                                                 (130, 96, 320, "NN", 2), (1000, 520, 4160, "TN", 1),
                                                 (768, 3072, 16384, "TT", 1), (2048, 3072, 1024, "NT", 1),
-                                                (4096, 4096, 512, "NT", 1)])
+                                                (4096, 4096, 512, "NT", 1), (4096, 3072, 1000, "NT", 1)])
 def test_gemm_ex_round_and_rowsum(kernels, m, n, k, layout, batch):
     """mi355x_gemm_ex with MI355X_GEMM_ROUND (f32 C holding bf16-rounded
     values) and the row sums of A (the linear bias gradient), with and
