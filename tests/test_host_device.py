@@ -616,7 +616,9 @@ def test_adamw_parameter_copies_are_aligned_slices(mojo):
     holders = {id(c[0]._holder) for c in copies}
     assert len(holders) == 1
     for p, c in zip(model.parameters(), copies):
-        assert c[0]._ptr % 256 == 0
+        # 256-byte aligned within the allocation (whose base the device
+        # allocator aligns; the host stand-in's may not be)
+        assert (c[0]._ptr - c[0]._holder.data_ptr()) % 256 == 0
         assert torch.equal(c[0].cpu(), p.detach().cpu().bfloat16())
 
 
