@@ -13,7 +13,6 @@ from __future__ import annotations
 import functools
 
 import torch
-from torch.utils._pytree import tree_map
 
 _EXCLUDE_AUTOCAST = torch._C.DispatchKeySet(torch._C.DispatchKey.AutocastPrivateUse1)
 
@@ -32,16 +31,28 @@ def _autocast_dtype():
     return torch.get_autocast_dtype("mojo")
 
 
-def _retype(dtype):
-    """Leaf function for tree_map: a floating mojo tensor below float64 that
-    is not already `dtype` becomes a `dtype` copy; everything else passes."""
-    def leaf(x):
-        if (isinstance(x, torch.Tensor) and x.device.type == "mojo" and x.dtype != dtype
-                and x.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+_RETYPED = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _retype(x, dtype):
+    """A floating mojo tensor below float64 that is not already `dtype`
+    becomes a `dtype` copy, also inside a list or tuple argument (a tensor
+    list); everything else passes unchanged.  (Aten arguments nest no
+    deeper, so no general tree walk is needed.)"""
+    if isinstance(x, torch.Tensor):
+        if x.dtype != dtype and x.dtype in _RETYPED and x.device.type == "mojo":
             return x.to(dtype)
         return x
+    if isinstance(x, (list, tuple)) and any(isinstance(e, torch.Tensor) for e in x):
+        return type(x)(_retype(e, dtype) for e in x)
+    return x
 
-    return leaf
+
+def _retype_call(args, kwargs, dtype):
+    args = tuple(_retype(a, dtype) for a in args)
+    if kwargs:
+        kwargs = {k: _retype(v, dtype) for k, v in kwargs.items()}
+    return args, kwargs
 
 
 def _under_policy(op, target, low_copy=False):
@@ -53,7 +64,7 @@ def _under_policy(op, target, low_copy=False):
     @functools.wraps(op)
     def kernel(*args, **kwargs):
         with torch._C._ExcludeDispatchKeyGuard(_EXCLUDE_AUTOCAST):
-            args, kwargs = tree_map(_retype(target()), (args, kwargs))
+            args, kwargs = _retype_call(args, kwargs, target())
             if not low_copy:
                 return op(*args, **kwargs)
             from ..eager_kernels import aten_fast
@@ -101,5 +112,5 @@ def _linear_autocast(input, weight, bias=None):
         dt = _autocast_dtype()
         if fused_linear_inputs(input, weight, bias, dt):
             return fused_linear(input, weight, bias, dt)
-        input, weight, bias = tree_map(_retype(dt), (input, weight, bias))
+        input, weight, bias = (_retype(t, dt) for t in (input, weight, bias))
         return torch.ops.aten.linear.default(input, weight, bias)
