@@ -423,6 +423,35 @@ __device__ __forceinline__ typename Mfma<T>::frag tr_frag(const char* tile, int 
   return f;
 }
 
+// This lane's byte offsets of tr_frag's reads at tile row 0, one per
+// head-dim block dt.  Row t0*16 + r has the swizzle of r (it uses only the
+// row's low four bits), so tr_frag(tile, dt, t0, t1) reads tile +
+// t0*16*ROWB + o[dt] and tile + t1*16*ROWB + o[dt]: with the offsets kept
+// in registers the per-step address arithmetic folds into immediates.
+template <int D>
+struct TrOffsets {
+  int o[D / 16];
+  __device__ __forceinline__ TrOffsets() {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, src = lane & 15;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) o[dt] = KvLayout<D>::off(4 * g + (src >> 2), dt * 16 + 4 * (src & 3));
+  }
+};
+
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::frag tr_frag_at(const char* tile, const TrOffsets<D>& to, int dt,
+                                                             int t0, int t1) {
+  constexpr int RB = 16 * KvLayout<D>::ROWB;
+  s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + t0 * RB + to.o[dt]));
+  s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + t1 * RB + to.o[dt]));
+  typename Mfma<T>::frag f;
+  short* fs = (short*)&f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) fs[e] = a[e], fs[4 + e] = b[e];
+  return f;
+}
+
 // K/V tile loader for the forward: each thread's chunk offsets within a
 // tile are fixed, so a tile costs one scalar row-offset product plus one
 // 64-bit add per load.  Rows past the end (only in the last tile) reload the
@@ -532,6 +561,7 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
   kl.issue(j0 * 64, p.Skv, lds);
   vl.issue(j0 * 64, p.Skv, lds + L::TILE);
   const int sw = L::swz(lr);  // fragment rows kt*16 + lr share the swizzle of lr
+  const TrOffsets<D> tro;
   const float c = p.scale_log2;
   int buf = 0;
   // One step per 64 keys: the unmasked steps first, then the ones that
@@ -619,7 +649,7 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
         for (int qt = 0; qt < QT; ++qt) lacc[qt] = Mfma<T>::mma(ones, pf[qt], lacc[qt]);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const frag vf = tr_frag<T, D>(Vt, dt, 2 * ks2, 2 * ks2 + 1);
+          const frag vf = tr_frag_at<T, D>(Vt, tro, dt, 2 * ks2, 2 * ks2 + 1);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) oacc[dt][qt] = Mfma<T>::mma(vf, pf[qt], oacc[dt][qt]);
         }
@@ -957,6 +987,7 @@ __device__ __forceinline__ void dkv_body(const AttnBwdArgs& p, GridPos gp, char*
 
   const int64_t qstart = f.causal ? (k0 / 64) * 64 : 0;
   const int sw = L::swz(lr);
+  const TrOffsets<D> tro;
   int buf = 0;
   if (qstart < f.Sq) issue(qstart, lds);
   // One step per 64 queries.  Masks are needed only where the tile crosses
@@ -1030,8 +1061,8 @@ __device__ __forceinline__ void dkv_body(const AttnBwdArgs& p, GridPos gp, char*
           }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const frag dof = tr_frag<T, D>(dOt, dt, 2 * qs, 2 * qs + 1);
-          const frag qtf = tr_frag<T, D>(Qt, dt, 2 * qs, 2 * qs + 1);
+          const frag dof = tr_frag_at<T, D>(dOt, tro, dt, 2 * qs, 2 * qs + 1);
+          const frag qtf = tr_frag_at<T, D>(Qt, tro, dt, 2 * qs, 2 * qs + 1);
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             dva[dt][t] = Mfma<T>::mma(dof, pb[t], dva[dt][t]);
@@ -1114,6 +1145,7 @@ __device__ __forceinline__ void dq_body(const AttnBwdArgs& p, GridPos gp, char* 
   int64_t kv_end = f.Skv;
   if (f.causal) kv_end = min(f.Skv, q0 + 128);
   const int sw = L::swz(lr);
+  const TrOffsets<D> tro;
   int buf = 0;
   kv_tile_issue<D>(K, ks_b, 0, f.Skv, lds);
   kv_tile_issue<D>(V, vs_b, 0, f.Skv, lds + L::TILE);
@@ -1181,7 +1213,7 @@ __device__ __forceinline__ void dq_body(const AttnBwdArgs& p, GridPos gp, char* 
           }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const frag ktf = tr_frag<T, D>(Kt, dt, 2 * ks2, 2 * ks2 + 1);
+          const frag ktf = tr_frag_at<T, D>(Kt, tro, dt, 2 * ks2, 2 * ks2 + 1);
 #pragma unroll
           for (int u = 0; u < 2; ++u) dqa[dt][u] = Mfma<T>::mma(ktf, sb[u], dqa[dt][u]);
         }
