@@ -392,7 +392,7 @@ def _adam_descs(params, grads, ms, vs, steps, vmax=None):
 
 @pytest.mark.parametrize("amsgrad,maximize,wd", [(False, False, 0.1), (True, False, 0.1), (False, True, 0.0)])
 def test_fused_adamw_matches_oracle(kernels, amsgrad, maximize, wd):
-    sizes = [768 * 768, 3, 50257, 1, 4 * 65536 + 17] + [10] * 40  # > one 32-tensor batch
+    sizes = [768 * 768, 3, 50257, 1, 4 * 65536 + 17] + [10] * 40
     ps = [randn(s) for s in sizes]
     gs = [randn(s) for s in sizes]
     ms = [randn(s) * 0.1 for s in sizes]
@@ -576,3 +576,39 @@ def test_geglu_bit_exact_vs_gelu_then_mul(kernels, approximate):
     call("mi355x_gelu_fwd", p(a), p(gate), n, approximate, CODE[torch.bfloat16], None)
     want = (host(a).float() * host(up).float()).bfloat16()
     assert torch.equal(host(y), want)
+
+
+def test_multi_tensor_kernels_across_batches_with_empty_tensors(kernels):
+    """Lists longer than one launch's 160 tensors, with empty tensors among
+    them (first, inside a batch and at a batch boundary): foreach norm,
+    foreach apply and fused AdamW locate every chunk of every tensor."""
+    g = torch.Generator().manual_seed(12)
+    sizes = [0] + [int(s) for s in torch.randint(1, 3000, (158,), generator=g)] + [0, 0, 5000] + \
+            [int(s) for s in torch.randint(0, 40, (200,), generator=g)] + [70000, 0]
+    xs = [torch.randn(s, generator=g) for s in sizes]
+    tx = [dev(x) for x in xs]
+    n = len(sizes)
+    outs = [torch.empty((), device="cuda") for _ in sizes]
+    numels = i64(*sizes)
+    ws_n = lib().mi355x_foreach_norm_workspace_bytes(numels, n)
+    ws = workspace(ws_n)
+    ptrs_out = (ctypes.c_void_p * n)(*[p(o) for o in outs])
+    ptrs_in = (ctypes.c_void_p * n)(*[p(t) for t in tx])
+    call("mi355x_foreach_norm", ptrs_out, 0, ptrs_in, 0, numels, n, 2.0, p(ws), ws_n, None)
+    for i, (o, x) in enumerate(zip(outs, xs)):
+        assert abs(host(o).item() - x.double().norm().item()) <= 1e-5 * max(1.0, x.double().norm().item()), i
+    coef = dev(torch.tensor(0.5))
+    call("mi355x_foreach_apply", 2, ptrs_in, None, None, None, numels, n, 0, 0.0, p(coef), None)
+    for i, (t, x) in enumerate(zip(tx, xs)):
+        assert torch.equal(host(t), x * 0.5), i
+    gs = [torch.randn(s, generator=g) for s in sizes]
+    ms = [torch.zeros(s) for s in sizes]
+    vs = [torch.zeros(s) for s in sizes]
+    tg, tm, tv = ([dev(x) for x in xs_] for xs_ in (gs, ms, vs))
+    steps = [dev(torch.tensor(1.0)) for _ in sizes]
+    d = _adam_descs(tx, tg, tm, tv, steps)
+    call("mi355x_fused_adamw", d, n, 1e-3, None, 0.9, 0.999, 0.01, 1e-8, 0, None, None, None)
+    for i in range(n):
+        exp = O.adamw_step((xs[i] * 0.5).numpy(), gs[i].numpy(), ms[i].numpy(), vs[i].numpy(), 1.0, 1e-3, 0.9,
+                           0.999, 0.01, 1e-8, False, False, None)
+        tol_close(np64(tx[i]), exp[0], atol=1e-6, rtol=1e-5, what=f"p{i}")

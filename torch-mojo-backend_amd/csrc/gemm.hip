@@ -366,12 +366,6 @@ struct TileCfg<2> {  // C192: 128x192, waves of 64x96, 40 KB per stage (k-contig
 // operands are both m/n-contiguous.  Their transposing fragment reads make
 // a 64-k step long; halving it and keeping two stages in flight hides the
 // loads better (gfx950, cfg 2 shapes: 7-13% over 64-k stages).
-// 256x192: two C192 tiles sharing one B tile in one 8-wave block (same
-// 64x96 wave tiles), so a CU loads 56 KB per 64-k step instead of 80 KB.
-template <>
-struct TileCfg<4> {
-  static constexpr int BM = 256, BN = 192, BK = 64, WGM = 4, WGN = 2, STAGES = 2, MIN_BLOCKS = 1;
-};
 template <>
 struct TileCfg<3> {
   static constexpr int BM = 256, BN = 256, BK = 32, WGM = 2, WGN = 4, STAGES = 3, MIN_BLOCKS = 1;
@@ -790,29 +784,28 @@ __global__ void __launch_bounds__(256) gemm_f32(GemmArgs g) {
 // planning
 // ---------------------------------------------------------------------------
 struct Plan {
-  int cfg;  // 0 = C128, 1 = C256, 2 = C192, 3 = C256 in 32-k stages, 4 = 256x192
+  int cfg;  // 0 = C128, 1 = C256, 2 = C192, 3 = C256 in 32-k stages
   int splits;
   int64_t kchunk;
 };
 
 int64_t tiles_of(int cfg, int64_t batch, int64_t m, int64_t n) {
   const bool c256 = cfg == 1 || cfg == 3;
-  const int64_t bm = (c256 || cfg == 4) ? 256 : 128, bn = c256 ? 256 : (cfg == 2 || cfg == 4 ? 192 : 128);
+  const int64_t bm = c256 ? 256 : 128, bn = c256 ? 256 : (cfg == 2 ? 192 : 128);
   return ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * batch;
 }
 
 // Row-sum partial slots per split: one per wave column of every column tile.
 int64_t rs_slots_of(int cfg, int64_t n) {
   const bool c256 = cfg == 1 || cfg == 3;
-  const int64_t bn = c256 ? 256 : (cfg == 2 || cfg == 4 ? 192 : 128), wgn = c256 ? 4 : 2;
+  const int64_t bn = c256 ? 256 : (cfg == 2 ? 192 : 128), wgn = c256 ? 4 : 2;
   return (n + bn - 1) / bn * wgn;
 }
 
 // Pick the configuration that finishes in the least time: whole rounds of
-// the CUs' block slots (two C128 or C192 blocks, or one C256 or 256x192
-// block, per CU) times the per-round time measured on gfx950 at K =
-// 768..50304 (a C256 round does twice a C128 round's work in 1.82x its
-// time, a C192 round 1.5x the work in 1.5x, a 256x192 round 3x in 1.42x).  An m-contiguous A (a weight
+// the CUs' block slots (two C128 blocks or one C256 block per CU) times the
+// per-round time measured on gfx950 at K = 768..3072 (a C256 round does
+// twice a C128 round's work in 1.82x its time).  An m-contiguous A (a weight
 // gradient dY^T X) reads both operands through transposing LDS reads, which
 // C256 tiles halve per flop: when both sides span a 256 tile it takes them,
 // in 32-k stages (the 50304 x 768 embedding gradient: 1.53 -> 1.35 ms, the
@@ -821,32 +814,25 @@ int64_t rs_slots_of(int cfg, int64_t n) {
 Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool a_kcontig, bool b_kcontig) {
   Plan best{0, 1, k};
   const int64_t t128 = tiles_of(0, batch, m, n), t256 = tiles_of(1, batch, m, n), t192 = tiles_of(2, batch, m, n);
-  const int64_t t4 = tiles_of(4, batch, m, n);
   const double c128 = (double)((t128 + 2 * kCUs - 1) / (2 * kCUs));
   const double c256 = 1.82 * (double)((t256 + kCUs - 1) / kCUs);
   const double c192 = 1.5 * (double)((t192 + 2 * kCUs - 1) / (2 * kCUs));
-  const double c4 = 1.42 * (double)((t4 + kCUs - 1) / kCUs);
   double cbest = c128;
   if (t256 >= kCUs && c256 < cbest) best.cfg = 1, cbest = c256;
   if (b_kcontig && t192 >= kCUs && c192 < cbest) best.cfg = 2, cbest = c192;
-  // 256x192 only for long K: at K <= 3072 it won alone but lost inside the
-  // training step (+0.27 ms), where the smaller blocks overlap their
-  // prologues and epilogues better
-  static const char* no4 = getenv("MI355X_GEMM_NO_256X192");  // tuning override
-  if (!no4 && k >= 8192 && b_kcontig && t4 >= kCUs && c4 < cbest) best.cfg = 4, cbest = c4;
   // (measured exception: the 3072 x 768 fc weight gradient, m = 4n, runs
   // faster as split-K C128: 940 against 850 TF/s)
   if (!a_kcontig && m >= 256 && n >= 256 && (m < 4 * n || t256 >= kCUs)) best.cfg = 3;
-  static const char* forced = getenv("MI355X_GEMM_TILE");  // tuning override: "128", "192", "193" (256x192), "256" or "256.32"
+  static const char* forced = getenv("MI355X_GEMM_TILE");  // tuning override: "128", "192", "256" or "256.32"
   if (forced) {
     const double f = atof(forced);
-    best.cfg = f == 256 ? 1 : (f > 256 && !a_kcontig ? 3 : (f == 192 && b_kcontig ? 2 : (f == 193 && b_kcontig ? 4 : 0)));
+    best.cfg = f == 256 ? 1 : (f > 256 && !a_kcontig ? 3 : (f == 192 && b_kcontig ? 2 : 0));
   }
   const int64_t tiles = tiles_of(best.cfg, batch, m, n);
   if (tiles < kCUs && k >= 2048) {
     // as many K splits as keep every block in the first round of block
     // slots: a second, partly filled round would double the time
-    const int64_t slots = best.cfg == 1 || best.cfg >= 3 ? kCUs : 2 * kCUs;  // block slots of the chosen config
+    const int64_t slots = best.cfg == 1 || best.cfg == 3 ? kCUs : 2 * kCUs;  // block slots of the chosen config
     int64_t s = slots / tiles;
     const int64_t max_s = k / 512;
     if (s > max_s) s = max_s;
@@ -886,7 +872,7 @@ int launch_layout(const GemmArgs& g, dim3 grid, hipStream_t s) {
     if (ak) return fail(MI355X_EINVAL, "mi355x_gemm: 32-k C256 tiles take an m-contiguous A");
     if (bk) return launch_kernel<T, CFG, false, true, KT, RS>(g, grid, s);
     return launch_kernel<T, CFG, false, false, KT, RS>(g, grid, s);
-  } else if constexpr (CFG == 2 || CFG == 4) {  // 192-wide B tiles are only loaded k-contiguous
+  } else if constexpr (CFG == 2) {  // 192-wide B tiles are only loaded k-contiguous
     if (!bk) return fail(MI355X_EINVAL, "mi355x_gemm: 128x192 tiles need a k-contiguous B");
     if (ak) return launch_kernel<T, CFG, true, true, KT, RS>(g, grid, s);
     return launch_kernel<T, CFG, false, true, KT, RS>(g, grid, s);
@@ -948,7 +934,6 @@ int launch_mfma(GemmArgs g, int64_t batch, const Plan& p, hipStream_t s) {
   const bool kt = g.k % 64 != 0;
   int rc;
   if (p.cfg == 1) rc = kt ? launch_tile<T, 1, true>(g, batch, p.splits, s) : launch_tile<T, 1, false>(g, batch, p.splits, s);
-  else if (p.cfg == 4) rc = kt ? launch_tile<T, 4, true>(g, batch, p.splits, s) : launch_tile<T, 4, false>(g, batch, p.splits, s);
   else if (p.cfg == 3) rc = kt ? launch_tile<T, 3, true>(g, batch, p.splits, s) : launch_tile<T, 3, false>(g, batch, p.splits, s);
   else if (p.cfg == 2) rc = kt ? launch_tile<T, 2, true>(g, batch, p.splits, s) : launch_tile<T, 2, false>(g, batch, p.splits, s);
   else rc = kt ? launch_tile<T, 0, true>(g, batch, p.splits, s) : launch_tile<T, 0, false>(g, batch, p.splits, s);
