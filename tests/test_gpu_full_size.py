@@ -102,3 +102,54 @@ def test_gemm_cfg2_linear_launches_match_oracle(kernels, K, N):
     tol_close(got.double().numpy(), O.addmm(dyc.T, X.double().numpy()), atol=5e-2, rtol=1e-2,
               what=f"dW {K}->{N}")
     tol_close(host(db).double().numpy(), dY.sum(0, dtype=torch.float64).numpy(), atol=5e-2, rtol=1e-2, what=f"db {K}->{N}")
+
+
+def test_attention_gemma_shape_window_slices_match_oracle(kernels):
+    """Gemma-3-1B-shaped attention at its real size: 4 query heads on one K/V
+    head, head_dim 256, causal sliding window 512, T = 4096, bf16; forward
+    through mi355x_attn_fwd_ex (the MFMA kernel) and backward through
+    mi355x_attn_bwd_gen, as the fused autograd Function runs them.
+
+    The f64 oracle runs on two 1024-row sub-problems that the window makes
+    exact.  The prefix (rows 0..1023): top-left causal masking is the same
+    there, so O, LSE and dQ of every row and dK/dV of keys 0..512 (all
+    their queries are below 1024) must match.  The tail (rows 3072..4095):
+    a query at local row >= 511 sees only keys inside the sub-problem, so
+    O, LSE and dQ of rows 3583..4095 must match; with the device's O and
+    LSE as the backward's inputs every P in the sub-problem is the full
+    problem's, and every query of keys 3072..4095 lies inside, so their
+    dK/dV must match too."""
+    B, H, Hk, T, D, W = 1, 4, 1, 4096, 256, 512
+    g = torch.Generator().manual_seed(4096)
+    q, do = (torch.randn(B, H, T, D, generator=g).bfloat16() for _ in range(2))
+    k, v = (torch.randn(B, Hk, T, D, generator=g).bfloat16() for _ in range(2))
+    tq, tk, tv, tdo = dev(q), dev(k), dev(v), dev(do)
+    scale = 1.0 / math.sqrt(D)
+    o = torch.empty(B, T, H, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    lse = torch.empty(B, H, T, device="cuda")
+    call("mi355x_attn_fwd_ex", p(o), bhs(o), p(lse), p(tq), bhs(tq), p(tk), bhs(tk), p(tv), bhs(tv),
+         B, H, Hk, T, T, D, scale, 1, W, CODE[torch.bfloat16], None)
+    dq = torch.empty(B, T, H, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    dk = torch.empty(B, T, Hk, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    dv = torch.empty(B, T, Hk, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    ws_n = lib().mi355x_attn_bwd_gen_workspace_bytes(B, H, T)
+    ws = workspace(ws_n)
+    call("mi355x_attn_bwd_gen", p(dq), bhs(dq), p(dk), bhs(dk), p(dv), bhs(dv), p(tdo), bhs(tdo),
+         p(tq), bhs(tq), p(tk), bhs(tk), p(tv), bhs(tv), p(o), bhs(o), p(lse),
+         B, H, Hk, T, T, D, scale, 1, W, CODE[torch.bfloat16], p(ws), ws_n, None)
+    got = {name: host(t).double().numpy() for name, t in
+           (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv))}
+    n = lambda t: t.double().numpy()  # noqa: E731
+    for s0, rows, keys in ((0, slice(0, 1024), slice(0, 513)), (3072, slice(511, 1024), slice(0, 1024))):
+        sl = slice(s0, s0 + 1024)
+        qs, ks, vs, dos = n(q[:, :, sl]), n(k[:, :, sl]), n(v[:, :, sl]), n(do[:, :, sl])
+        eo, el = O.sdpa_forward(qs, ks, vs, causal=True, window=W)
+        what = f"gemma T4096 rows {s0 + rows.start}..{s0 + rows.stop - 1}"
+        tol_close(got["o"][:, :, sl][:, :, rows], eo[:, :, rows], atol=2e-2, rtol=2e-2, what=f"O {what}")
+        tol_close(got["lse"][:, :, sl][:, :, rows], el[:, :, rows], atol=1e-2, rtol=1e-3, what=f"LSE {what}")
+        edq, edk, edv = O.sdpa_backward(dos, qs, ks, vs, got["o"][:, :, sl], got["lse"][:, :, sl],
+                                        causal=True, window=W)
+        tol_close(got["dq"][:, :, sl][:, :, rows], edq[:, :, rows], atol=3e-2, rtol=2e-2, what=f"dQ {what}")
+        kw = f"gemma T4096 keys {s0 + keys.start}..{s0 + keys.stop - 1}"
+        tol_close(got["dk"][:, :, sl][:, :, keys], edk[:, :, keys], atol=3e-2, rtol=2e-2, what=f"dK {kw}")
+        tol_close(got["dv"][:, :, sl][:, :, keys], edv[:, :, keys], atol=3e-2, rtol=2e-2, what=f"dV {kw}")
