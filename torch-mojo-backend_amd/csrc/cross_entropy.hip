@@ -201,67 +201,56 @@ __device__ __forceinline__ uint4 shift_pair(uint4 lo, uint4 hi, int bytes) {
   return o;
 }
 
-// The backward writes every element of the row: 1024 threads, one 16-byte
-// output chunk each per iteration (gfx950, [16384, 50257] bf16: 0.687 ms
-// with 256 threads x 2 chunks, 0.604 ms like this).
-constexpr int kBwdThreads = 1024;
+// The backward writes every element of the row.  It has no reduction, so
+// rows are split over blocks: block b covers 16-byte output chunks
+// (b % nb) * 256 .. +255 of row b / nb, one chunk per thread (gfx950,
+// [16384, 50257] bf16: 0.565 ms, against 0.604 ms for one 1024-thread
+// block per row looping over it and 0.59-0.66 ms for 2-8 chunks per thread).
+constexpr int kBwdThreads = 256;
 
 template <typename T, typename TD>
 __global__ void __launch_bounds__(kBwdThreads)
-    ce_bwd_rows(TD* __restrict__ dx, int64_t ld_dx, const T* __restrict__ x, int64_t ld,
-                const float* __restrict__ lse, const int64_t* __restrict__ target,
-                const float* __restrict__ grad, int grad_per_row, const float* __restrict__ total,
-                int64_t n, int64_t c, int64_t ignore_index) {
-  constexpr int V = Chunk<T>::V, U = 1;
+    ce_bwd_chunks(TD* __restrict__ dx, int64_t ld_dx, const T* __restrict__ x, int64_t ld,
+                  const float* __restrict__ lse, const int64_t* __restrict__ target,
+                  const float* __restrict__ grad, int grad_per_row, const float* __restrict__ total,
+                  int64_t n, int64_t c, int64_t ignore_index, int nb) {
+  constexpr int V = Chunk<T>::V;
   static_assert(sizeof(TD) == sizeof(T), "dx chunks follow the logits chunks");
-  const int64_t row = blockIdx.x;
+  const int64_t row = blockIdx.x / nb;
+  const int t = (int)(blockIdx.x - row * nb) * kBwdThreads + threadIdx.x;
+  const int nout = (int)(ld_dx / V);
+  if (t >= nout) return;
   const int64_t tg = target[row];
   float g = grad[grad_per_row ? row : 0];
   if (!grad_per_row && total) g /= total[0];
   const bool valid = tg != ignore_index && tg >= 0 && tg < c;
   if (!valid) g = 0.f;
   const float l = lse[row];
-  const T* r = x + row * ld;
-  const RowGeo<T> geo(r, c);
+  const RowGeo<T> geo(x + row * ld, c);
   const int bytes = geo.p * (int)sizeof(T);
   const int nch = (int)geo.nch, ci = (int)c, tgi = valid ? (int)tg : -1;
-  uint4* o = (uint4*)(dx + row * ld_dx);
-  const int nout = (int)(ld_dx / V);
-  // U output chunks per thread per iteration, their loads issued first
-  for (int t0 = threadIdx.x; t0 < nout; t0 += kBwdThreads * U) {
-    uint4 lo[U], hi[U];
+  const int k0 = t * V;
+  uint4 lo = make_uint4(0, 0, 0, 0), hi = lo;
+  if (k0 < ci) {
+    lo = geo.base[t];
+    if (bytes && t + 1 < nch) hi = geo.base[t + 1];
+  }
+  Chunk<T> ch;
+  ch.w = bytes ? shift_pair(lo, hi, bytes) : lo;
+  struct alignas(16) Out { TD v[V]; } out;
+  if (k0 + V <= ci && (tgi < k0 || tgi >= k0 + V)) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * kBwdThreads;
-      lo[u] = hi[u] = make_uint4(0, 0, 0, 0);
-      if (t * V < ci) {
-        lo[u] = geo.base[t];
-        if (bytes && t + 1 < nch) hi[u] = geo.base[t + 1];
-      }
-    }
+    for (int e = 0; e < V; ++e) out.v[e] = from_f32<TD>(g * hw_exp2((ch.get(e) - l) * kLog2e));
+  } else {  // the last chunk, padding past c, or the target's chunk
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * kBwdThreads;
-      if (t >= nout) break;
-      const int k0 = t * V;
-      Chunk<T> ch;
-      ch.w = bytes ? shift_pair(lo[u], hi[u], bytes) : lo[u];
-      struct alignas(16) Out { TD v[V]; } out;
-      if (k0 + V <= ci && (tgi < k0 || tgi >= k0 + V)) {
-#pragma unroll
-        for (int e = 0; e < V; ++e) out.v[e] = from_f32<TD>(g * hw_exp2((ch.get(e) - l) * kLog2e));
-      } else {  // the last chunk, padding past c, or the target's chunk
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const int k = k0 + e;
-          float d = 0.f;
-          if (k < ci) d = g * (hw_exp2((ch.get(e) - l) * kLog2e) - (k == tgi ? 1.f : 0.f));
-          out.v[e] = from_f32<TD>(d);
-        }
-      }
-      o[t] = *(const uint4*)&out;
+    for (int e = 0; e < V; ++e) {
+      const int k = k0 + e;
+      float d = 0.f;
+      if (k < ci) d = g * (hw_exp2((ch.get(e) - l) * kLog2e) - (k == tgi ? 1.f : 0.f));
+      out.v[e] = from_f32<TD>(d);
     }
   }
+  ((uint4*)(dx + row * ld_dx))[t] = *(const uint4*)&out;
 }
 
 }  // namespace
@@ -316,10 +305,12 @@ extern "C" int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx, c
   hipStream_t s = (hipStream_t)stream;
   const int per_row = reduction == 0;
   const float* tw = reduction == 1 ? total_weight : nullptr;
-#define CE_BWD(TX, TD)                                                                                   \
-  ce_bwd_rows<TX, TD><<<(unsigned)n, kBwdThreads, 0, s>>>((TD*)dx, ld_dx, (const TX*)logits, ld, lse, \
-                                                          target, grad_out, per_row, tw, n, c,       \
-                                                          ignore_index)
+  const int nb = (int)ceil_div(ld_dx / v, kBwdThreads);
+  MI_REQUIRE(n * nb < (1ll << 31), "mi355x_cross_entropy_bwd: too many rows");
+#define CE_BWD(TX, TD)                                                                                     \
+  ce_bwd_chunks<TX, TD><<<(unsigned)(n * nb), kBwdThreads, 0, s>>>((TD*)dx, ld_dx, (const TX*)logits, ld, \
+                                                                  lse, target, grad_out, per_row, tw, n,  \
+                                                                  c, ignore_index, nb)
   if (dtype == MI355X_BF16 && dx_dtype == MI355X_BF16) CE_BWD(bf16, bf16);
   else if (dtype == MI355X_F32 && dx_dtype == MI355X_F32) CE_BWD(float, float);
   else if (dtype == MI355X_F16 && dx_dtype == MI355X_F16) CE_BWD(f16, f16);
