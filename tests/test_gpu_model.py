@@ -202,6 +202,32 @@ def test_gemma_shaped_prefill_matches_cpu(mojo):
     assert err <= 5e-2 * want.abs().max().item() + 5e-2, err
 
 
+def test_gemma_full_width_prefill_matches_cpu(mojo):
+    """Gemma-3-1B's real layer shapes at its benchmarked length: hidden 1152,
+    4 query heads on 1 K/V head of head_dim 256, GeGLU 6912, window 512,
+    T = 4096, with six layers (five sliding-window, one global) and a 4096
+    vocabulary so the f32 CPU reference stays cheap.  Device bf16 against
+    the same bf16-rounded weights in f32 on the CPU."""
+    from torch_mojo_backend.gemma3 import Gemma3, Gemma3Config
+
+    cfg = Gemma3Config(vocab_size=4096, layers=6)
+    torch.manual_seed(0)
+    ref = Gemma3(cfg)
+    for _, prm in ref.named_parameters():
+        if prm.dim() == 1:
+            torch.nn.init.normal_(prm, std=0.1)
+    ref = ref.to(torch.bfloat16).float()
+    model = Gemma3(cfg)
+    model.load_state_dict(ref.state_dict())
+    model = model.to(torch.bfloat16).to("mojo")
+    idx = torch.randint(0, cfg.vocab_size, (1, 4096), generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        got = model(idx.to("mojo")).float().cpu()
+        want = ref(idx)
+    err = (got - want).abs().max().item()
+    assert err <= 5e-2 * want.abs().max().item() + 5e-2, (err, want.abs().max().item())
+
+
 @pytest.mark.parametrize("dtype,bits", [(torch.float32, torch.int32), (torch.bfloat16, torch.int16)])
 def test_stack_and_cat_of_many_pieces_are_bit_exact(mojo, dtype, bits):
     """stack/cat of many contiguous pieces (clip_grad_norm_ stacks one norm
