@@ -87,10 +87,11 @@ class Attention(nn.Module):
     def forward(self, x, rope, mask):
         b, t, _ = x.shape
         c = self.cfg
-        q = self.q_proj(x).view(b, t, c.heads, c.head_dim).transpose(1, 2)
-        k = self.k_proj(x).view(b, t, c.kv_heads, c.head_dim).transpose(1, 2)
+        # the per-head norms run on the projections' dense [B, T, H, D] rows,
+        # before the head transpose (the same rows, no copy)
+        q = self.q_norm(self.q_proj(x).view(b, t, c.heads, c.head_dim)).transpose(1, 2)
+        k = self.k_norm(self.k_proj(x).view(b, t, c.kv_heads, c.head_dim)).transpose(1, 2)
         v = self.v_proj(x).view(b, t, c.kv_heads, c.head_dim).transpose(1, 2)
-        q, k = self.q_norm(q), self.k_norm(k)
         cos, sin = rope
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         scale = 1.0 / math.sqrt(c.head_dim)
