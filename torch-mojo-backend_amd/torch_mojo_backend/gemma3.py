@@ -142,6 +142,21 @@ class Gemma3(nn.Module):
         for name, p in self.named_parameters():
             if p.dim() >= 2:
                 nn.init.normal_(p, mean=0.0, std=0.02)
+        # rotary tables and the sliding-window mask of the last (length,
+        # device, dtype) seen: built on the host and copied over, they cost
+        # more than a third of a prefill's host time when rebuilt per call
+        self._tables = {}
+
+    def _rope_and_mask(self, t, dev, dt):
+        key = (t, str(dev), dt)
+        hit = self._tables.get(key)
+        if hit is None:
+            c = self.cfg
+            hit = (rope_tables(t, c.head_dim, c.rope_local_base, dev, dt),
+                   rope_tables(t, c.head_dim, c.rope_global_base, dev, dt),
+                   sliding_window_causal_mask(t, c.window, dev))
+            self._tables = {key: hit}
+        return hit
 
     def forward(self, idx):
         """Logits [B, T, vocab] of one prefill over token ids idx [B, T]."""
@@ -149,9 +164,7 @@ class Gemma3(nn.Module):
         c = self.cfg
         dev, dt = idx.device, self.embed.weight.dtype
         x = self.embed(idx) * torch.tensor(c.hidden ** 0.5, dtype=dt, device=dev)
-        rope_local = rope_tables(t, c.head_dim, c.rope_local_base, dev, dt)
-        rope_global = rope_tables(t, c.head_dim, c.rope_global_base, dev, dt)
-        mask = sliding_window_causal_mask(t, c.window, dev)
+        rope_local, rope_global, mask = self._rope_and_mask(t, dev, dt)
         for blk in self.blocks:
             x = blk(x, rope_local, rope_global, mask)
         x = self.norm(x)
