@@ -22,6 +22,12 @@ def _on_mojo(*ts) -> bool:
     return all(isinstance(t, TorchMojoTensor) for t in ts)
 
 
+def _needs_grad(*ts) -> bool:
+    """Whether autograd records this call (otherwise the forward kernel is
+    called directly, without an autograd Function's per-call cost)."""
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
 class _Rope(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, cos, sin):
@@ -40,6 +46,8 @@ def rotary_embedding(x, cos, sin):
     if (_on_mojo(x, cos, sin) and x.dim() == 4 and x.shape[-1] % 8 == 0
             and tuple(cos.shape) == (x.shape[2], x.shape[3]) and tuple(sin.shape) == tuple(cos.shape)
             and x.dtype in (torch.float32, torch.bfloat16, torch.float16)):
+        if not _needs_grad(x, cos, sin):
+            return aten_fast.rope_forward(x, cos, sin)
         return _Rope.apply(x, cos, sin)
     half = x.shape[-1] // 2
     return x * cos + torch.cat([-x[..., half:], x[..., :half]], dim=-1) * sin
@@ -65,6 +73,8 @@ def geglu(gate, up, approximate="tanh"):
     """gelu(gate) * up."""
     if (_on_mojo(gate, up) and gate.shape == up.shape and gate.dtype == up.dtype
             and gate.dtype in (torch.float32, torch.bfloat16, torch.float16)):
+        if not _needs_grad(gate, up):
+            return aten_fast.geglu_forward(gate, up, approximate)
         return _GeGLU.apply(gate, up, approximate)
     return F.gelu(gate, approximate=approximate) * up
 
@@ -76,5 +86,7 @@ def rms_norm(x, weight, eps, weight_offset=0.0):
 
     shape = (x.shape[-1],)
     if _on_mojo(x, weight) and aten_fast.rms_norm_inputs(x, shape, weight):
+        if not _needs_grad(x, weight):
+            return aten_fast.rms_norm_forward(x, shape, weight, float(eps), float(weight_offset))[0]
         return _FusedRMSNorm.apply(x, shape, weight, float(eps), float(weight_offset))
     return F.rms_norm(x, shape, weight.float() + weight_offset, eps)
