@@ -62,6 +62,24 @@ def test_map_binary_broadcast_exact(kernels, op, fn):
     assert torch.equal(host(out), fn(a, b).to(out_dt))
 
 
+@pytest.mark.parametrize("op,fn", [(0, lambda a, b: torch.add(a, b, alpha=0.5)),
+                                   (1, lambda a, b: torch.sub(a, b, alpha=0.5)),
+                                   (2, torch.mul), (3, torch.div)])
+@pytest.mark.parametrize("cols", [64, 70])
+def test_map_bf16_dense_binary(kernels, op, fn, cols):
+    """bf16 (op) bf16 -> bf16 over dense [33, cols]: 64 columns take the
+    8-wide kernel, 70 the generic one; both compute in f32 and round once,
+    bit for bit as torch does on the CPU."""
+    a, b = randn(33, cols).bfloat16(), randn(33, cols).bfloat16()
+    ta, tb = dev(a), dev(b)
+    out = torch.empty(33, cols, dtype=torch.bfloat16, device="cuda")
+    ins = (ctypes.c_void_p * 3)(p(ta), p(tb), None)
+    dts = (ctypes.c_int * 3)(CODE[torch.bfloat16], CODE[torch.bfloat16], 0)
+    call("mi355x_map", op, p(out), CODE[torch.bfloat16], 2, ins, dts, i64(cols, 1, cols, 1, cols, 1),
+         i64(33, cols), 2, 0.5, 0.0, None)
+    assert torch.equal(host(out), fn(a, b))
+
+
 @pytest.mark.parametrize("op,fn", [(0, lambda a, b: a + 0.5 * b), (1, lambda a, b: a - 0.5 * b),
                                    (2, lambda a, b: a * b), (3, lambda a, b: a / b)])
 @pytest.mark.parametrize("ydt", [torch.float32, torch.bfloat16])

@@ -382,6 +382,29 @@ __global__ void __launch_bounds__(kThreads) binary_x4(int op, float* __restrict_
   }
 }
 
+// Dense binary add/sub/mul/div of two bf16 tensors into bf16 (a residual
+// stream kept in bf16): 8 elements per 16-byte access, computed in f32 as
+// map_dense does and rounded once.
+__global__ void __launch_bounds__(kThreads) binary_x8_bf16(int op, bf16* __restrict__ out, const bf16* __restrict__ x,
+                                                           const bf16* __restrict__ y, float alpha, int64_t n8) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * kThreads) {
+    const bf16x8 a = ((const bf16x8*)x)[i], b = ((const bf16x8*)y)[i];
+    bf16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float u = (float)a[e], v = (float)b[e];
+      float w;
+      if (op == MI355X_OP_ADD) w = u + alpha * v;
+      else if (op == MI355X_OP_SUB) w = u - alpha * v;
+      else if (op == MI355X_OP_MUL) w = u * v;
+      else w = u / v;
+      r[e] = (bf16)w;
+    }
+    ((bf16x8*)out)[i] = r;
+  }
+}
+
 // out = x (op) y with y one dense row of inner4 float4s broadcast over the
 // `outer` rows of x and out (a position embedding added to every sequence).
 template <typename TX, typename TY>
@@ -688,6 +711,14 @@ extern "C" int mi355x_map(int op, void* out, int out_dtype, int nin, const void*
     else if (!xb) binary_x4<float, bf16><<<grid, kThreads, 0, s>>>(op, o, (const float*)ins[0], (const bf16*)ins[1], al, n / 4);
     else if (!yb) binary_x4<bf16, float><<<grid, kThreads, 0, s>>>(op, o, (const bf16*)ins[0], (const float*)ins[1], al, n / 4);
     else binary_x4<bf16, bf16><<<grid, kThreads, 0, s>>>(op, o, (const bf16*)ins[0], (const bf16*)ins[1], al, n / 4);
+    return check_launch("mi355x_map");
+  }
+  if (g.ndim == 1 && geo_dense(g) && nin == 2 && ins[0] && ins[1] && out_dtype == MI355X_BF16 &&
+      in_dtypes[0] == MI355X_BF16 && in_dtypes[1] == MI355X_BF16 && n % 8 == 0 && aligned(out, 16) &&
+      aligned(ins[0], 16) && aligned(ins[1], 16) &&
+      (op == MI355X_OP_ADD || op == MI355X_OP_SUB || op == MI355X_OP_MUL || op == MI355X_OP_DIV)) {
+    binary_x8_bf16<<<grid_for(n / 8, 2), kThreads, 0, s>>>(op, (bf16*)out, (const bf16*)ins[0], (const bf16*)ins[1],
+                                                          (float)s0, n / 8);
     return check_launch("mi355x_map");
   }
   // y one dense row broadcast over the rows of a dense x and out
