@@ -111,7 +111,28 @@ def register_autograd_ops() -> None:
     _library.impl("scaled_dot_product_attention", _scaled_dot_product_attention_autograd)
     _library.impl("cross_entropy_loss", _cross_entropy_loss_autograd)
     _library.impl("rms_norm", _rms_norm_autograd)
+    _library.impl("linear", _linear_autograd)
     _registered = True
+
+
+def _linear_autograd(input, weight, bias=None):
+    """aten::linear on the device.  When autograd records nothing (no_grad
+    or inputs without requires_grad) and the operands share a float dtype,
+    one GEMM with the bias in its epilogue, instead of the composite's
+    transpose + matmul (+ add) chain of dispatches; otherwise the composite
+    itself (aten's CompositeImplicitAutograd kernel), so training graphs are
+    unchanged."""
+    ts = (input, weight) if bias is None else (input, weight, bias)
+    if (
+        not (torch.is_grad_enabled() and any(t.requires_grad for t in ts))
+        and all(isinstance(t, TorchMojoTensor) and hasattr(t, "_holder") for t in ts)
+        and input.dtype in (torch.float32, torch.bfloat16, torch.float16)
+        and all(t.dtype == input.dtype for t in ts)
+        and weight.dim() == 2 and input.dim() >= 1 and input.shape[-1] == weight.shape[1]
+        and (bias is None or (bias.dim() == 1 and bias.shape[0] == weight.shape[0]))
+    ):
+        return aten_fast.linear_forward(input, weight, bias)
+    return torch.ops.aten.linear.default.decompose(input, weight, bias)
 
 
 class _FusedLinear(torch.autograd.Function):
