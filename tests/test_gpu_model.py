@@ -294,3 +294,44 @@ def test_gqa_window_attention_backward_is_fused(mojo, window):
     for a, b in ((qm, qc), (km, kc), (vm, vc)):
         assert a.grad.shape == b.grad.shape
         assert torch.allclose(a.grad.double().cpu(), b.grad, atol=6e-2, rtol=3e-2), (a.grad.double().cpu() - b.grad).abs().max()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_attention_pair_return_contract(mojo, causal):
+    """The ATen flash pair called directly on mojo tensors: the forward's
+    9-tuple (out, lse f32 [B,H,Sq], None, None, Sq, Sk, rng_state, unused,
+    debug mask), its lse against the log-sum-exp of the scaled scores, and
+    the backward's (dq, dk, dv) against torch CPU autograd
+    (reference aten_fast.py:7726-7734)."""
+    g = torch.Generator().manual_seed(7 + causal)
+    B, H, S, D = 2, 3, 70, 64
+    q, k, v = (torch.randn(B, H, S, D, generator=g).bfloat16() for _ in range(3))
+    qm, km, vm = (t.to("mojo") for t in (q, k, v))
+    res = torch.ops.aten._scaled_dot_product_flash_attention(qm, km, vm, 0.0, causal)
+    assert len(res) == 9
+    out, lse, cq, ck, mq, mk, seed, offset, dbg = res
+    assert cq is None and ck is None
+    assert int(mq) == S and int(mk) == S
+    assert out.shape == (B, H, S, D) and out.dtype == torch.bfloat16
+    assert lse.shape == (B, H, S) and lse.dtype == torch.float32
+    assert seed.numel() == 2 and offset.numel() == 0
+    assert dbg.numel() == 0
+
+    qd, kd, vd = (t.double() for t in (q, k, v))
+    scores = qd @ kd.transpose(-1, -2) / math.sqrt(D)
+    if causal:
+        scores = scores.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
+    ref_lse = torch.logsumexp(scores, dim=-1)
+    ref_out = torch.softmax(scores, dim=-1) @ vd
+    assert torch.allclose(lse.double().cpu(), ref_lse, atol=2e-3, rtol=1e-3)
+    assert torch.allclose(out.double().cpu(), ref_out, atol=3e-2, rtol=3e-2)
+
+    dout = torch.randn(B, H, S, D, generator=g).bfloat16()
+    dq, dk, dv = torch.ops.aten._scaled_dot_product_flash_attention_backward(
+        dout.to("mojo"), qm, km, vm, out, lse, cq, ck, S, S, 0.0, causal, seed, offset)
+    qc, kc, vc = (t.double().requires_grad_() for t in (q, k, v))
+    ref = F.scaled_dot_product_attention(qc, kc, vc, is_causal=causal)
+    ref.backward(dout.double())
+    for a, b in ((dq, qc), (dk, kc), (dv, vc)):
+        assert a.shape == b.shape and a.dtype == torch.bfloat16
+        assert torch.allclose(a.double().cpu(), b.grad, atol=6e-2, rtol=3e-2), (a.double().cpu() - b.grad).abs().max()

@@ -320,7 +320,8 @@ __global__ void __launch_bounds__(THREADS)
 #pragma unroll
     for (int e = 0; e < V; ++e) {
       const float gv = cg[i].get(e), yv = yc.get(e);
-      o[e] = LOG ? gv - expf(yv) * sum : yv * (gv - sum);
+      // exp(y) as one hardware exp2 of y log2(e)
+      o[e] = LOG ? gv - __builtin_amdgcn_exp2f(yv * 1.4426950408889634f) * sum : yv * (gv - sum);
     }
     store_chunk(dx, g.off, j, g.p, cols, o);
   }
