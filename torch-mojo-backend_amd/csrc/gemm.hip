@@ -38,6 +38,10 @@
 
 #include "common.h"
 #include "mfma.h"
+
+#ifndef GEMM_XCD_FLAT
+#define GEMM_XCD_FLAT 1
+#endif
 #include "vec.h"
 
 extern __shared__ __attribute__((aligned(16))) char gemm_smem[];
@@ -490,12 +494,31 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
   constexpr int A_BYTES = BM * ROWB, STAGE = A_BYTES + BN * ROWB, S = C::STAGES;
   char* const lds = gemm_smem;
 
+#if GEMM_XCD_FLAT
+  // XCD-aware order over the whole grid: the hardware deals workgroups to
+  // the 8 XCDs round-robin in dispatch order (x fastest, then y), so XCD
+  // L % 8 gets every 8th block.  Each XCD is given one contiguous run of the
+  // (split, batch)-major tile list instead: its blocks share A/B panels and,
+  // with split K, one or two K ranges, so each L2 fetches about 1/8 of the
+  // operands (dealing a plane's tiles over all XCDs made every L2 fetch
+  // every split's panels).  A bijection for any grid size.
+  const uint32_t nt = gridDim.x;
+  uint32_t L = blockIdx.x + nt * blockIdx.y;
+  {
+    const uint32_t total = nt * gridDim.y, xcd = L & 7, q = total >> 3, r = total & 7;
+    L = xcd * q + min(xcd, r) + (L >> 3);
+  }
+  const uint32_t plane = L / nt, t = L - plane * nt;
+  const uint32_t tm = t / (uint32_t)g.tiles_n, tn = t - tm * (uint32_t)g.tiles_n;
+  const uint32_t split = plane / (uint32_t)g.batch, bidx = plane - split * (uint32_t)g.batch;
+#else
   // XCD-aware tile order within one (split, batch) plane.
   uint32_t t = blockIdx.x;
   const uint32_t nt = gridDim.x;
   if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);
   const uint32_t tm = t / (uint32_t)g.tiles_n, tn = t - tm * (uint32_t)g.tiles_n;
   const uint32_t split = blockIdx.y / (uint32_t)g.batch, bidx = blockIdx.y - split * (uint32_t)g.batch;
+#endif
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   int64_t kbeg = 0, kend = g.k;
   if (g.part) {
@@ -826,9 +849,12 @@ Plan plan_gemm(int64_t batch, int64_t m, int64_t n, int64_t k, bool a_kcontig, b
   double cbest = c128;
   if (t256 >= kCUs && c256 < cbest) best.cfg = 1, cbest = c256;
   if (b_kcontig && t192 >= kCUs && c192 < cbest) best.cfg = 2, cbest = c192;
-  // (measured exception: the 3072 x 768 fc weight gradient, m = 4n, runs
-  // faster as split-K C128: 940 against 850 TF/s)
-  if (!a_kcontig && m >= 256 && n >= 256 && (m < 4 * n || t256 >= kCUs)) best.cfg = 3;
+  // Weight gradients (m-contiguous A) take the 32-k C256 stages when their
+  // 256x256 tiles fill the CUs (wte: 50304 x 768); smaller ones take
+  // split-K C128, whose K ranges the XCD-ordered grid keeps in one or two
+  // L2s (config 2 shapes, TF/s: 768 x 768 646 against 501, 2304 x 768 912
+  // against 839, 768 x 3072 933 against 915).
+  if (!a_kcontig && m >= 256 && n >= 256 && t256 >= kCUs) best.cfg = 3;
   static const char* forced = getenv("MI355X_GEMM_TILE");  // tuning override: "128", "192", "256" or "256.32"
   if (forced) {
     const double f = atof(forced);
