@@ -109,6 +109,26 @@ def test_gemm_accumulate_and_batched(kernels):
     tol_close(np64(tc), exp, atol=2e-2, rtol=1e-2, what="batched beta=1")
 
 
+@pytest.mark.parametrize("m,n,k", [(300, 136, 5120), (200, 136, 6144)])
+def test_gemm_batched_split_k_grid_order(kernels, m, n, k):
+    """Batched GEMMs with a long K take split K over several batch planes:
+    the block -> (split, batch, tile) order spans the whole grid (grids of
+    180 and 144 blocks, one not a multiple of the 8 XCDs), and every tile of
+    every plane must come out once."""
+    bsz = 3
+    A = randn(bsz, m, k).bfloat16()
+    B = randn(bsz, k, n).bfloat16()
+    C0 = randn(bsz, m, n)
+    ta, tb, tc = dev(A), dev(B), dev(C0)
+    ws_n = lib().mi355x_gemm_workspace_bytes(p(ta), k, 1, m * k, p(tb), n, 1, k * n, 1, bsz, m, n, k)
+    assert ws_n > 0  # the split-K partials live in the workspace
+    ws = workspace(ws_n)
+    call("mi355x_gemm", p(tc), 0, n, m * n, p(ta), k, 1, m * k, p(tb), n, 1, k * n, 1, None, 0, 1,
+         bsz, m, n, k, p(ws), ws_n, None)
+    exp = C0.double().numpy() + np.einsum("bmk,bkn->bmn", A.double().numpy(), B.double().numpy())
+    tol_close(np64(tc), exp, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what=f"batched split-K {m}x{n}x{k}")
+
+
 @pytest.mark.parametrize("n,c_dtype", [(80, torch.float32), (78, torch.float32), (80, torch.bfloat16)])
 def test_gemm_split_k_with_bias_and_beta(kernels, n, c_dtype):
     """Small C, long K (the weight-gradient regime) takes the split-K path:
