@@ -544,7 +544,9 @@ int mi355x_attn_bwd_gen(void* dq, const int64_t* dq_bhs, void* dk, const int64_t
  * hipMalloc).  The row terms live in a fixed 32 MiB device array per GPU,
  * which limits batch * heads * sq to 4,194,272 query rows (larger shapes
  * return MI355X_EINVAL).  Every call on one GPU shares that array: calls
- * that overlap on one GPU (different streams or threads) race. */
+ * that overlap on one GPU (different streams or threads) race.  The array
+ * used is the one on the device that owns `stream` (the current device for
+ * the null stream). */
 int mi355x_attn_bwd_noalloc(void* dq, const int64_t* dq_bhs, void* dk,
                             const int64_t* dk_bhs, void* dv, const int64_t* dv_bhs,
                             const void* dout, const int64_t* do_bhs, const void* q,

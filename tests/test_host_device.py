@@ -551,6 +551,33 @@ def test_residual_add_is_fused_into_the_next_layer_norm(mojo):
     assert torch.equal(s4.cpu(), ref_s)
 
 
+def test_chained_held_back_adds_keep_their_order(mojo):
+    """h = x + a and h2 = h + b are both held back; a LayerNorm (or a cast)
+    of h must not take h's add out of the queue ahead of h2's, which reads
+    h: h2 would then be computed from h before h exists."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    g = torch.Generator().manual_seed(19)
+    x = torch.randn(128, 768, generator=g)
+    a = torch.randn(128, 768, generator=g).bfloat16()
+    b = torch.randn(128, 768, generator=g).bfloat16()
+    w, bias = torch.randn(768, generator=g), torch.randn(768, generator=g)
+    xm, am, bm, wm, biasm = (t.to("mojo") for t in (x, a, b, w, bias))
+    ref_h = x + a.float()
+    ref_h2 = ref_h + b.float()
+    for consume in (lambda h: F.layer_norm(h, (768,), wm, biasm), lambda h: h.to(torch.bfloat16)):
+        h = xm + am
+        h2 = h + bm
+        assert len(ek._pending) == 2
+        y = consume(h)
+        assert not ek._pending
+        assert torch.equal(h.cpu(), ref_h)
+        assert torch.equal(h2.cpu(), ref_h2)
+        assert y.cpu().shape == (128, 768)
+    assert torch.allclose(F.layer_norm(xm + am, (768,), wm, biasm).cpu(),
+                          F.layer_norm(ref_h, (768,), w, bias), atol=1e-5, rtol=1e-5)
+
+
 def test_held_back_sum_and_its_autocast_copy_in_one_pass(mojo):
     """cast_to of a held-back f32 sum (the residual gradient the autograd
     engine adds up, then cast for the next linear's backward) computes the

@@ -1422,18 +1422,35 @@ std::once_flag g_scratch_once[kMaxDevices];
 void* g_scratch_ptr[kMaxDevices];
 hipError_t g_scratch_err[kMaxDevices];
 
-// This device's address of `scratch` (looked up once per device, with that
-// device current); nullptr with the error recorded on failure.
-void* scratch_for_current_device() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+// The address of `scratch` on the device that owns `stream` (looked up once
+// per device, with that device current; the caller's current device is
+// restored); nullptr with the error recorded on failure.
+void* scratch_for_stream(hipStream_t stream) {
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur < 0) {
     set_error("mi355x_attn_bwd_noalloc: no current HIP device");
     return nullptr;
   }
-  std::call_once(g_scratch_once[dev], [dev] {
+  int dev = cur;
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess) {
+      set_error("mi355x_attn_bwd_noalloc: cannot query the stream's device");
+      return nullptr;
+    }
+    dev = (int)sdev;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("mi355x_attn_bwd_noalloc: device %d out of range", dev);
+    return nullptr;
+  }
+  std::call_once(g_scratch_once[dev], [dev, cur] {
     void* ptr = nullptr;
-    g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? ptr : nullptr;
+    hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
+    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    g_scratch_err[dev] = e;
+    g_scratch_ptr[dev] = e == hipSuccess ? ptr : nullptr;
   });
   if (!g_scratch_ptr[dev])
     set_error("mi355x_attn_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
@@ -1490,7 +1507,7 @@ extern "C" int mi355x_attn_bwd_noalloc(void* dq, const int64_t* dq_bhs, void* dk
                 "(at most %lld rows); use mi355x_attn_bwd with a workspace",
                 (long long)(batch * heads * sq), (long long)need, (long long)kAttnScratchBytes,
                 (long long)((kAttnScratchBytes - 256) / 8));
-  void* ws = scratch_for_current_device();
+  void* ws = scratch_for_stream((hipStream_t)stream);
   if (!ws) return MI355X_ELAUNCH;
   // every scratch word the kernels read is written first by attn_bwd_delta
   // in the same call, so nothing is cleared

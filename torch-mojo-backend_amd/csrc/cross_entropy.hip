@@ -306,7 +306,10 @@ extern "C" int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx, c
   const int per_row = reduction == 0;
   const float* tw = reduction == 1 ? total_weight : nullptr;
   const int nb = (int)ceil_div(ld_dx / v, kBwdThreads);
-  MI_REQUIRE(n * nb < (1ll << 31), "mi355x_cross_entropy_bwd: too many rows");
+  // one block per (row, chunk of kBwdThreads 16-byte pieces): the grid's
+  // work-items must stay below 2^32
+  MI_REQUIRE(n * nb * kBwdThreads < (1ll << 32), "mi355x_cross_entropy_bwd: too many rows (%lld x %d blocks of %d)",
+             (long long)n, nb, kBwdThreads);
 #define CE_BWD(TX, TD)                                                                                     \
   ce_bwd_chunks<TX, TD><<<(unsigned)(n * nb), kBwdThreads, 0, s>>>((TD*)dx, ld_dx, (const TX*)logits, ld, \
                                                                   lse, target, grad_out, per_row, tw, n,  \

@@ -301,7 +301,7 @@ class Deferred:
 
 _pending: list = []
 _pending_lock = threading.RLock()
-_flushing = False
+_state = threading.local()  # .flushing: this thread is issuing deferred launches
 
 
 def defer(record: Deferred) -> None:
@@ -311,37 +311,50 @@ def defer(record: Deferred) -> None:
         _pending.append(record)
 
 
+def _reads_storage_of(rec: Deferred, ref) -> bool:
+    return any(inp._holder is ref._holder for inp in rec.inputs)
+
+
 def take_pending(match):
     """Remove and return the first pending launch for which match(record)
-    holds (the caller then performs its work itself), else None."""
+    holds (the caller then performs its work itself), else None.
+
+    The caller issues the taken work after the launches still pending
+    (its next library call flushes them first), so a record is taken only
+    when no later pending launch reads the storage it writes; otherwise the
+    later launch would read that output before it exists, and None is
+    returned (the caller's library call then issues everything in order)."""
     if not _pending:
         return None
     with _pending_lock:
         for i, rec in enumerate(_pending):
             if match(rec):
+                if any(_reads_storage_of(later, rec.out) for later in _pending[i + 1:]):
+                    return None
                 return _pending.pop(i)
     return None
 
 
 def flush_pending() -> None:
-    """Issue every deferred launch, oldest first."""
-    global _flushing
-    if not _pending or _flushing:
+    """Issue every deferred launch, oldest first.  A launch issued from
+    here calls lib() itself, which must not re-enter the flush; other
+    threads wait on the lock until the flush has finished."""
+    if not _pending or getattr(_state, "flushing", False):
         return
     with _pending_lock:
-        _flushing = True
+        _state.flushing = True
         try:
             while _pending:
                 _pending.pop(0).launch()
         finally:
-            _flushing = False
+            _state.flushing = False
 
 
 def lib() -> ctypes.CDLL:
     """The loaded kernel library (loaded on first use).  Deferred launches
     are issued first, so every kernel sees them in stream order."""
     global _LIB
-    if _pending and not _flushing:
+    if _pending:
         flush_pending()
     if _LIB is None:
         _LIB = _load()
