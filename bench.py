@@ -16,9 +16,9 @@ after W warmup steps.  Alongside it:
   cfg4_prefill  report only: one Gemma-3-1B-shaped prefill (grouped-query
                 sliding-window/global attention at head_dim 256, RMSNorm,
                 GeGLU, RoPE; 1 x 4096 tokens, bf16), tokens/s and TFLOP/s;
-  cpu_baseline  the same training step in f32 on the host's cores with
-                stock PyTorch CPU (the reference's oracle), on a bounded
-                sample (four 1 x 1024-token steps, about 15 s on 8 cores).
+  cpu_baseline  BASELINE config 0 (GPT-2 small f32 train step on batch
+                4 x 256) on the host's cores with stock PyTorch CPU (the
+                reference's oracle): median of 3 steps after a warmup.
 """
 
 from __future__ import annotations
@@ -96,15 +96,22 @@ def bench_model(args):
         losses.append(training_step(model, opt, x, y, torch.bfloat16, grad_clip=GRAD_CLIP))
     torch.accelerator.synchronize()
     dt = time.perf_counter() - t0
-    vals = [float(l.item()) for l in losses]
-    tokens = args.batch * args.block * args.steps
-    # per-step relative deviation from the f32 CPU curve of the same run
-    # (tests/golden fixture; only at the fixture's batch and block size)
+    # Untimed: the same run continued to the 50 steps of the f32 CPU curve
+    # (tests/golden fixture; only at the fixture's batch and block size), so
+    # the per-step deviation covers the whole curve.
     dev = None
     fx_path = ROOT / "tests" / "golden" / "loss_curve_b16_t1024_f32cpu.json"
     if fx_path.exists() and args.batch == 16 and args.block == 1024:
         ref = json.loads(fx_path.read_text())["losses"]
+        for i in range(len(losses), len(ref)):
+            x, y = batches[i % 2]
+            losses.append(training_step(model, opt, x, y, torch.bfloat16, grad_clip=GRAD_CLIP))
+        vals = [float(l.item()) for l in losses]
         dev = [abs(a - b) / abs(b) for a, b in zip(vals, ref)]
+    else:
+        vals = [float(l.item()) for l in losses]
+    tokens = args.batch * args.block * args.steps
+    worst = max(range(len(dev)), key=dev.__getitem__) if dev else None
     return {
         "tokens_per_s": tokens / dt,
         "ms_per_step": 1000.0 * dt / args.steps,
@@ -113,7 +120,12 @@ def bench_model(args):
         "loss_last": vals[-1],
         "losses": [round(v, 5) for v in vals],
         "loss_rel_dev_vs_f32cpu": [round(v, 5) for v in dev] if dev else None,
-        "loss_max_rel_dev_vs_f32cpu": round(max(dev), 5) if dev else None,
+        "loss_steps_compared": len(dev) if dev else 0,
+        "loss_max_rel_dev_vs_f32cpu": round(dev[worst], 5) if dev else None,
+        "loss_max_rel_dev_step": worst,
+        # steps 0-31: where every stock-torch bf16 realisation of this run is
+        # within 1% of f32 (later steps spread to 1-4% with rounding noise)
+        "loss_max_rel_dev_steps_0_31": round(max(dev[:32]), 5) if dev else None,
     }
 
 
@@ -330,29 +342,47 @@ def bench_copy(iters):
     return {"bytes_read": 2 * n, "bytes_written": 2 * n, "ms": ms, "gbs": 4 * n / ms / 1e6}
 
 
-def cpu_baseline():
-    """f32 training step on the host cores with stock PyTorch CPU (bounded
-    sample: batch 1 x 1024 tokens, 4 timed steps after 1 warmup)."""
-    from torch_mojo_backend.gpt2 import (BETAS, GRAD_CLIP, LEARNING_RATE, WEIGHT_DECAY, GPT, GPTConfig,
-                                         make_batches, training_step)
+def _cpu_model_name() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(steps=3):
+    """BASELINE config 0 on the host cores: GPT-2 small in f32, one eager
+    forward+backward+AdamW step (lr 6e-4, betas 0.9/0.95, wd 0.1) on batch
+    4 x 256 int64 ids, with stock PyTorch CPU (the reference's oracle);
+    median of `steps` timed steps after one warmup step."""
+    from torch_mojo_backend.gpt2 import (BETAS, LEARNING_RATE, WEIGHT_DECAY, GPT, GPTConfig, make_batches,
+                                         training_step)
 
     torch.manual_seed(1337)
     model = GPT(GPTConfig())
     opt = model.configure_optimizers(WEIGHT_DECAY, LEARNING_RATE, BETAS, fused=True)
-    (x, y), = make_batches(1, 1024, 50257, 1, 5, "cpu")
-    training_step(model, opt, x, y, grad_clip=GRAD_CLIP)
-    steps = 4
-    t0 = time.perf_counter()
+    (x, y), = make_batches(4, 256, 50257, 1, 5, "cpu")
+    training_step(model, opt, x, y, grad_clip=0.0)
+    times = []
     for _ in range(steps):
-        training_step(model, opt, x, y, grad_clip=GRAD_CLIP)
-    dt = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        training_step(model, opt, x, y, grad_clip=0.0)
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
     return {
-        "value": steps * 1024 / dt,
+        "value": 4 * 256 / med,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": _cpu_model_name(),
+        "ms_per_step": 1000.0 * med,
         "kind": "port",
-        "sample": "four f32 GPT-2-small train steps (fwd+bwd+clip+fused AdamW) on batch 1 x 1024 tokens, "
-                  "stock PyTorch CPU ATen (the reference's oracle), after one warmup step",
+        "sample": f"BASELINE config 0: f32 GPT-2-small fwd+bwd+AdamW step on batch 4 x 256 tokens, stock "
+                  f"PyTorch CPU ATen (the reference's oracle), median of {steps} steps after one warmup",
     }
 
 

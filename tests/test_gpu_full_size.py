@@ -6,6 +6,11 @@ XCDs of the XCD-aware block map (each XCD owns 12 consecutive (b, h) pairs
 at this shape) and take different places in its heaviest-first tile order,
 so the one-launch dK/dV + dQ grid is pinned where it is timed.
 
+Config 3's HBM-bound kernels at the step's sizes: the fused cross-entropy
+and the stand-alone log_softmax on bf16 logits [16384, 50257], GELU on the
+fc activation [16384, 3072]; and config 4's tied lm_head GEMM (M = 4096,
+N = 262144, K = 1152).
+
 Config 2 (GEMMs at M = 16384): every (K, N) of the sweep, in the three
 launches of a linear layer as the autocast model issues them -- forward
 x W^T + b (bf16 out), dX = dY W (f32 out rounded to bf16), dW = dY^T X (f32
@@ -46,9 +51,9 @@ def test_attention_cfg1_slices_match_oracle(kernels):
         # backward from the device's own O and LSE, as the autograd pair runs it
         edq, edk, edv = O.sdpa_backward(dos, qs, ks, vs, got["o"][sl].double().numpy(),
                                         got["lse"][sl].double().numpy(), causal=True)
-        tol_close(got["dv"][sl].double().numpy(), edv, atol=3e-2, rtol=2e-2, what=f"dV {what}")
-        tol_close(got["dk"][sl].double().numpy(), edk, atol=3e-2, rtol=2e-2, what=f"dK {what}")
-        tol_close(got["dq"][sl].double().numpy(), edq, atol=3e-2, rtol=2e-2, what=f"dQ {what}")
+        tol_close(got["dv"][sl].double().numpy(), edv, atol=2e-2, rtol=2e-2, what=f"dV {what}")
+        tol_close(got["dk"][sl].double().numpy(), edk, atol=2e-2, rtol=2e-2, what=f"dK {what}")
+        tol_close(got["dq"][sl].double().numpy(), edq, atol=2e-2, rtol=2e-2, what=f"dQ {what}")
 
 
 def _gemm_ex(c, c_rs, a, ars, acs, b, brs, bcs, m, n, k, bias=None, flags=0, rowsum=None):
@@ -149,7 +154,111 @@ def test_attention_gemma_shape_window_slices_match_oracle(kernels):
         tol_close(got["lse"][:, :, sl][:, :, rows], el[:, :, rows], atol=1e-2, rtol=1e-3, what=f"LSE {what}")
         edq, edk, edv = O.sdpa_backward(dos, qs, ks, vs, got["o"][:, :, sl], got["lse"][:, :, sl],
                                         causal=True, window=W)
-        tol_close(got["dq"][:, :, sl][:, :, rows], edq[:, :, rows], atol=3e-2, rtol=2e-2, what=f"dQ {what}")
+        tol_close(got["dq"][:, :, sl][:, :, rows], edq[:, :, rows], atol=2e-2, rtol=2e-2, what=f"dQ {what}")
         kw = f"gemma T4096 keys {s0 + keys.start}..{s0 + keys.stop - 1}"
-        tol_close(got["dk"][:, :, sl][:, :, keys], edk[:, :, keys], atol=3e-2, rtol=2e-2, what=f"dK {kw}")
-        tol_close(got["dv"][:, :, sl][:, :, keys], edv[:, :, keys], atol=3e-2, rtol=2e-2, what=f"dV {kw}")
+        tol_close(got["dk"][:, :, sl][:, :, keys], edk[:, :, keys], atol=2e-2, rtol=2e-2, what=f"dK {kw}")
+        tol_close(got["dv"][:, :, sl][:, :, keys], edv[:, :, keys], atol=2e-2, rtol=2e-2, what=f"dV {kw}")
+
+
+def test_cross_entropy_cfg3_logits_match_oracle(kernels):
+    """Fused cross-entropy at config 3's real logits: bf16 [16384, 50257]
+    (rows contiguous, 50257 columns: every row starts at another 2-byte
+    phase), mean reduction, gradient rows padded to 50264 as the model
+    allocates them.  The loss and every row's log-sum-exp against f64 over
+    all rows; dlogits on sampled rows (every 64-row span, both ends)."""
+    n, c, ld_dx = 16384, 50257, 50264
+    g = torch.Generator().manual_seed(50257)
+    x = (torch.randn(n, c, generator=g) * 3).bfloat16()
+    tgt = torch.randint(0, c, (n,), generator=g)
+    tx, tt = dev(x), dev(tgt)
+    out = torch.empty((), device="cuda")
+    lse = torch.empty(n, device="cuda")
+    tw = torch.empty((), device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws_n = lib().mi355x_cross_entropy_workspace_bytes(n)
+    ws = workspace(ws_n)
+    call("mi355x_cross_entropy_fwd", p(out), p(tw), p(lse), p(tx), CODE[torch.bfloat16], c, p(tt), n, c,
+         1, -100, p(err), p(ws), ws_n, None)
+    # f64 log-sum-exp of every row, in chunks
+    else_ = torch.empty(n, dtype=torch.float64)
+    picked = torch.empty(n, dtype=torch.float64)
+    for r0 in range(0, n, 1024):
+        xc = x[r0:r0 + 1024].double()
+        else_[r0:r0 + 1024] = torch.logsumexp(xc, 1)
+        picked[r0:r0 + 1024] = xc.gather(1, tgt[r0:r0 + 1024, None])[:, 0]
+    tol_close(host(lse).double().numpy(), else_.numpy(), atol=1e-4, rtol=1e-5, what="ce lse cfg3")
+    eloss = float((else_ - picked).mean())
+    tol_close(host(out).double().numpy(), eloss, atol=1e-4, rtol=1e-5, what="ce loss cfg3")
+    assert host(tw).item() == n and host(err).item() == 0
+    del tx
+    tx = dev(x)
+    dx = torch.empty(n, ld_dx, dtype=torch.bfloat16, device="cuda")
+    gout = dev(torch.tensor(1.0))
+    call("mi355x_cross_entropy_bwd", p(dx), CODE[torch.bfloat16], ld_dx, p(tx), CODE[torch.bfloat16], c, p(lse),
+         p(tt), p(gout), 1, p(tw), n, c, -100, None)
+    rows = _rows(n, 64)
+    logp = O.log_softmax(x[rows].double().numpy())
+    dnll = O.nll_loss_backward(np.float64(1.0), (len(rows), c), tgt[rows].numpy(), None, "mean", -100, n)
+    edx = O.log_softmax_backward(dnll, logp)
+    got = host(dx[rows]).double().numpy()
+    tol_close(got[:, :c], edx, atol=1e-12, rtol=2e-2, what="ce dlogits cfg3")
+    assert (got[:, c:] == 0).all()
+
+
+def test_log_softmax_cfg3_logits_match_oracle(kernels):
+    """Stand-alone log_softmax forward and backward at the logits' size, bf16
+    [16384, 50257] (the register-resident row kernels), on sampled rows."""
+    n, c = 16384, 50257
+    g = torch.Generator().manual_seed(16384)
+    x = (torch.randn(n, c, generator=g) * 3).bfloat16()
+    tx = dev(x)
+    y = torch.empty(n, c, dtype=torch.bfloat16, device="cuda")
+    call("mi355x_softmax_fwd", p(y), CODE[torch.bfloat16], p(tx), CODE[torch.bfloat16], n, c, 1, None)
+    rows = _rows(n, 64)
+    tol_close(host(y[rows]).double().numpy(), O.log_softmax(x[rows].double().numpy()), atol=2e-2, rtol=2e-2,
+              what="log_softmax cfg3")
+    del tx
+    dy = torch.randn(n, c, generator=g).bfloat16()
+    tdy = dev(dy)
+    dx = torch.empty(n, c, dtype=torch.bfloat16, device="cuda")
+    call("mi355x_softmax_bwd", p(dx), CODE[torch.bfloat16], p(tdy), CODE[torch.bfloat16], p(y),
+         CODE[torch.bfloat16], n, c, 1, None)
+    edx = O.log_softmax_backward(dy[rows].double().numpy(), host(y[rows]).double().numpy())
+    tol_close(host(dx[rows]).double().numpy(), edx, atol=2e-2, rtol=2e-2, what="log_softmax bwd cfg3")
+
+
+@pytest.mark.parametrize("approx", [0, 1])
+def test_gelu_cfg3_fc_activation_matches_oracle(kernels, approx):
+    """GELU forward and backward on the fc activation of config 3, bf16
+    [16384, 3072], every element against the f64 oracle."""
+    g = torch.Generator().manual_seed(3072 + approx)
+    x = (torch.randn(16384, 3072, generator=g) * 2).bfloat16()
+    dy = torch.randn(16384, 3072, generator=g).bfloat16()
+    tx, tdy = dev(x), dev(dy)
+    n = x.numel()
+    mode = "tanh" if approx else "none"
+    y = torch.empty_like(tx)
+    call("mi355x_gelu_fwd", p(y), p(tx), n, approx, CODE[torch.bfloat16], None)
+    xd = x.double().numpy()
+    tol_close(host(y).double().numpy(), O.gelu(xd, mode), atol=1e-2, rtol=1e-2, what="gelu cfg3")
+    dx = torch.empty_like(tx)
+    call("mi355x_gelu_bwd", p(dx), p(tdy), p(tx), n, approx, CODE[torch.bfloat16], None)
+    tol_close(host(dx).double().numpy(), O.gelu_backward(dy.double().numpy(), xd, mode), atol=1e-2, rtol=1e-2,
+              what="gelu bwd cfg3")
+
+
+def test_gemma_tied_lm_head_gemm_matches_oracle(kernels):
+    """The Gemma-3-1B prefill's largest GEMM: the tied lm_head, logits =
+    x W^T with M = 4096, N = 262144, K = 1152 (2.5 TFLOP), bf16 in and out,
+    W read in place; f64 oracle on sampled rows crossing every row tile,
+    all 262144 columns."""
+    M, N, K = 4096, 262144, 1152
+    g = torch.Generator().manual_seed(262144)
+    X = torch.randn(M, K, generator=g).bfloat16()
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    tx, tw = dev(X), dev(W)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    _gemm_ex(y, N, tx, K, 1, tw, 1, K, M, N, K)
+    rows = _rows(M, 37)
+    want = X[rows].double().numpy() @ W.double().numpy().T
+    tol_close(host(y[rows]).double().numpy(), want, atol=2e-2, rtol=2e-2, what="gemma lm_head")

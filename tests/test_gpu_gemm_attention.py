@@ -216,9 +216,9 @@ def test_attention_fwd_bwd_matches_oracle(kernels, shape, causal):
     dq, dk, dv = _attn_bwd(tdo, tq, tk, tv, o, lse, causal)
     edq, edk, edv = O.sdpa_backward(do.double().numpy(), q.double().numpy(), k.double().numpy(),
                                     v.double().numpy(), np64(o), np64(lse), causal=causal)
-    tol_close(np64(dv), edv, atol=3e-2, rtol=2e-2, what="dV")
-    tol_close(np64(dk), edk, atol=3e-2, rtol=2e-2, what="dK")
-    tol_close(np64(dq), edq, atol=3e-2, rtol=2e-2, what="dQ")
+    tol_close(np64(dv), edv, atol=2e-2, rtol=2e-2, what="dV")
+    tol_close(np64(dk), edk, atol=2e-2, rtol=2e-2, what="dK")
+    tol_close(np64(dq), edq, atol=2e-2, rtol=2e-2, what="dQ")
 
 
 def test_attention_special_cases(kernels):
@@ -393,7 +393,7 @@ def test_attention_f32_kernels_match_oracle(kernels, dtype, shape, mode):
     tol_close(np64(o), eo, what="O", **tol)
     tol_close(np64(lse), el, atol=1e-4, rtol=1e-4, what="LSE")
     edq, edk, edv = O.sdpa_backward(n(do), n(q), n(k), n(v), np64(o), np64(lse), causal=causal, window=window)
-    gtol = dict(atol=2e-4, rtol=2e-4) if dtype == torch.float32 else dict(atol=3e-2, rtol=2e-2)
+    gtol = dict(atol=2e-4, rtol=2e-4) if dtype == torch.float32 else dict(atol=2e-2, rtol=2e-2)
     tol_close(np64(dv), edv, what="dV", **gtol)
     tol_close(np64(dk), edk, what="dK", **gtol)
     tol_close(np64(dq), edq, what="dQ", **gtol)

@@ -36,7 +36,7 @@ def test_sdpa_autograd_uses_fused_kernels(mojo):
     ref.sum().backward()
     assert torch.allclose(out.float().cpu(), ref, atol=2e-2, rtol=2e-2)
     for a, b in ((qm, qc), (km, kc), (vm, vc)):
-        assert torch.allclose(a.grad.float().cpu(), b.grad, atol=5e-2, rtol=5e-2)
+        assert torch.allclose(a.grad.float().cpu(), b.grad, atol=2e-2, rtol=2e-2), (a.grad.float().cpu() - b.grad).abs().max()
 
 
 def _small_cfg():
@@ -116,20 +116,21 @@ def test_nanogpt_loss_curve_f32_matches_cpu_fixture(mojo):
 
 
 def test_nanogpt_loss_curve_bf16_autocast_tracks_cpu_fixture(mojo):
-    """bf16 autocast on the device against the f32 CPU curve, bounded by what
-    bf16 rounding does to this run in stock PyTorch.
+    """bf16 autocast on the device against the f32 CPU
+    curve.
 
     tests/golden/loss_envelope_b16_t1024_bf16_torch.json holds stock
-    PyTorch-ROCm bf16-autocast curves of the same run (as is, and with the
-    initial weights scaled by 1 + 1e-6 N(0,1) under twelve seeds;
-    tests/golden/make_bf16_envelope.py).  On every step the device's loss
-    must lie within 1% (of the f32 loss) of that envelope joined with the
-    f32 loss: stock torch stays within 0.1% of f32 for the first ~30 steps,
-    where this is a 1% bound around the f32 curve, and spreads to about 4%
-    by step 48 as the two-batch memorisation run amplifies rounding noise
-    (one more realisation of that noise may land just outside a sampled
-    envelope, hence the 1% margin there too).  Before the run's first loss spike (steps
-    0-4) the device must also be within 0.1%."""
+    PyTorch-ROCm bf16-autocast runs of the same seed: unperturbed, and with
+    the initial weights scaled by 1 + 1e-6 N(0,1) under twelve seeds.  All
+    thirteen stay within 1% of the f32 curve up to step 31; from step 32 on
+    the two-batch memorisation run amplifies bf16 rounding noise and the
+    realisations spread to 1-3.8% (the unperturbed one happens to stay
+    within 0.93%).  Which realisation a run follows is set by last-bit
+    differences (summation order, exp rounding), so the device is held to:
+      - within 0.1% of f32 on steps 0-4 (before the first loss spike);
+      - within 1% of f32 on steps 0-31, where every stock realisation is;
+      - on steps 32-49, within 1% (of the f32 loss) of the stock
+        realisations' range joined with the f32 loss."""
     import json
     from pathlib import Path
 
@@ -137,14 +138,20 @@ def test_nanogpt_loss_curve_bf16_autocast_tracks_cpu_fixture(mojo):
     got, ref = _loss_curve(amp=True)
     assert all(math.isfinite(v) for v in got)
     rel = [abs(a - b) / abs(b) for a, b in zip(got, ref)]
-    assert max(rel[:5]) <= 1e-3, max(enumerate(rel[:5]), key=lambda t: t[1])
+    per_step = [round(r, 5) for r in rel]
+    curves = list(env["curves"].values())
+    stock_max = [max(abs(c[i] - ref[i]) / ref[i] for c in curves) for i in range(len(ref))]
+    tight = [i for i in range(len(ref)) if max(stock_max[:i + 1]) <= 1e-2]
+    assert tight == list(range(32)), tight
+    assert max(rel[:5]) <= 1e-3, per_step
+    bad = [(i, round(got[i], 4), round(ref[i], 4)) for i in tight if rel[i] > 1e-2]
+    assert not bad, f"steps more than 1% from the f32 CPU curve (step, device, f32): {bad}; per step {per_step}"
     bad = []
-    for i, (g, f, lo, hi) in enumerate(zip(got, ref, env["lo"], env["hi"])):
+    for i in range(len(tight), len(ref)):
+        g, f, lo, hi = got[i], ref[i], env["lo"][i], env["hi"][i]
         if not (min(lo, f) - 0.01 * f <= g <= max(hi, f) + 0.01 * f):
             bad.append((i, round(g, 4), round(f, 4), round(lo, 4), round(hi, 4)))
-    print("bf16 device vs f32: max rel %.4f at step %d; per-step rel: %s"
-          % (max(rel), rel.index(max(rel)), [round(r, 4) for r in rel]))
-    assert not bad, f"steps more than 1% outside the stock-torch bf16 envelope (step, dev, f32, lo, hi): {bad}"
+    assert not bad, f"steps more than 1% outside the stock-torch bf16 range (step, dev, f32, lo, hi): {bad}"
 
 
 @pytest.mark.parametrize("shape,bias,strided", [((96, 200), True, False), ((3, 70, 200), True, False),
@@ -258,10 +265,10 @@ def test_sdpa_autograd_f32_and_wide_heads_use_the_flash_pair(mojo, dtype, d):
     qc, kc, vc = (t.double().requires_grad_() for t in (q, k, v))
     ref = F.scaled_dot_product_attention(qc, kc, vc, is_causal=True)
     ref.backward(dout.double())
-    tol = 1e-4 if dtype == torch.float32 else 3e-2
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
     assert torch.allclose(out.detach().double().cpu(), ref.detach(), atol=tol, rtol=tol)
     for a, b in ((qm, qc), (km, kc), (vm, vc)):
-        assert torch.allclose(a.grad.double().cpu(), b.grad, atol=2 * tol, rtol=2 * tol)
+        assert torch.allclose(a.grad.double().cpu(), b.grad, atol=tol, rtol=tol), (a.grad.double().cpu() - b.grad).abs().max()
 
 
 @pytest.mark.parametrize("window", [0, 40])
@@ -290,10 +297,10 @@ def test_gqa_window_attention_backward_is_fused(mojo, window):
     keep = (j <= i) & ((i - j < window) if window else True)
     ref = F.scaled_dot_product_attention(qc, kc, vc, attn_mask=keep, enable_gqa=True)
     ref.backward(dout.double())
-    assert torch.allclose(out.detach().double().cpu(), ref.detach(), atol=3e-2, rtol=3e-2)
+    assert torch.allclose(out.detach().double().cpu(), ref.detach(), atol=2e-2, rtol=2e-2)
     for a, b in ((qm, qc), (km, kc), (vm, vc)):
         assert a.grad.shape == b.grad.shape
-        assert torch.allclose(a.grad.double().cpu(), b.grad, atol=6e-2, rtol=3e-2), (a.grad.double().cpu() - b.grad).abs().max()
+        assert torch.allclose(a.grad.double().cpu(), b.grad, atol=2e-2, rtol=2e-2), (a.grad.double().cpu() - b.grad).abs().max()
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -324,7 +331,7 @@ def test_flash_attention_pair_return_contract(mojo, causal):
     ref_lse = torch.logsumexp(scores, dim=-1)
     ref_out = torch.softmax(scores, dim=-1) @ vd
     assert torch.allclose(lse.double().cpu(), ref_lse, atol=2e-3, rtol=1e-3)
-    assert torch.allclose(out.double().cpu(), ref_out, atol=3e-2, rtol=3e-2)
+    assert torch.allclose(out.double().cpu(), ref_out, atol=2e-2, rtol=2e-2)
 
     dout = torch.randn(B, H, S, D, generator=g).bfloat16()
     dq, dk, dv = torch.ops.aten._scaled_dot_product_flash_attention_backward(
@@ -334,4 +341,4 @@ def test_flash_attention_pair_return_contract(mojo, causal):
     ref.backward(dout.double())
     for a, b in ((dq, qc), (dk, kc), (dv, vc)):
         assert a.shape == b.shape and a.dtype == torch.bfloat16
-        assert torch.allclose(a.double().cpu(), b.grad, atol=6e-2, rtol=3e-2), (a.double().cpu() - b.grad).abs().max()
+        assert torch.allclose(a.double().cpu(), b.grad, atol=2e-2, rtol=2e-2), (a.double().cpu() - b.grad).abs().max()
