@@ -376,25 +376,6 @@ struct KvLayout {
   }
 };
 
-// Issue the direct loads of a 64-row tile (rows row0.., clamped to nrows-1).
-template <int D, int NW = 4>
-__device__ __forceinline__ void kv_tile_issue(const char* g, int64_t rs_bytes, int64_t row0,
-                                              int64_t nrows, char* dst) {
-  typedef KvLayout<D> L;
-  const int lane = threadIdx.x & 63, wave = wave_id();
-  constexpr int INSTR = L::TILE / 1024;
-#pragma unroll
-  for (int it = 0; it < INSTR / NW; ++it) {
-    const int blk = it * NW + wave;
-    const int r = blk * L::RPI + lane / L::CH;
-    const int chunk = (lane % L::CH) ^ L::swz(r);
-    int64_t gr = row0 + r;
-    if (gr >= nrows) gr = nrows - 1;
-    __builtin_amdgcn_global_load_lds((gptr_t)(g + gr * rs_bytes + chunk * 16),
-                                     (lptr_t)(dst + blk * 1024), 16, 0, 0);
-  }
-}
-
 __host__ __device__ inline int64_t ceil_div64(int64_t a, int64_t b) { return a <= 0 ? 0 : (a + b - 1) / b; }
 
 
@@ -452,10 +433,12 @@ __device__ __forceinline__ typename Mfma<T>::frag tr_frag_at(const char* tile, c
   return f;
 }
 
-// K/V tile loader for the forward: each thread's chunk offsets within a
-// tile are fixed, so a tile costs one scalar row-offset product plus one
-// 64-bit add per load.  Rows past the end (only in the last tile) reload the
-// last row; their scores are masked.
+// Tile loader (K/V in the forward and dQ pass, Q/dO in the dK/dV pass):
+// each thread's byte offsets within a full tile are computed once, so a tile
+// costs one scalar row-offset product plus one 64-bit add per load (a 64-bit
+// vector multiply per load, as recomputing them would take, runs at a
+// quarter of the VALU rate).  Rows past the end (only in the last tile)
+// reload the last row; their scores are masked.
 template <int D, int NW>
 struct KvTileLoad {
   typedef KvLayout<D> L;
@@ -463,18 +446,19 @@ struct KvTileLoad {
   const char* g;
   int64_t rs;
   int64_t off[IT];   // r * rs + chunk * 16
-  int row[IT];       // r, the tile row this thread loads
-  int coff[IT];      // chunk * 16
+  static __device__ __forceinline__ int row_of(int it) {
+    return (it * NW + wave_id()) * L::RPI + (int)(threadIdx.x & 63) / L::CH;
+  }
+  static __device__ __forceinline__ int coff_of(int row) {
+    return (((int)(threadIdx.x & 63) % L::CH) ^ L::swz(row)) * 16;
+  }
   __device__ __forceinline__ void init(const char* base, int64_t rs_bytes) {
-    const int lane = threadIdx.x & 63, wave = wave_id();
     g = base;
     rs = rs_bytes;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-      const int blk = it * NW + wave;
-      row[it] = blk * L::RPI + lane / L::CH;
-      coff[it] = ((lane % L::CH) ^ L::swz(row[it])) * 16;
-      off[it] = row[it] * rs + coff[it];
+      const int r = row_of(it);
+      off[it] = r * rs + coff_of(r);
     }
   }
   __device__ __forceinline__ void issue(int64_t row0, int64_t nrows, char* dst) const {
@@ -486,8 +470,9 @@ struct KvTileLoad {
     } else {
 #pragma unroll
       for (int it = 0; it < IT; ++it) {
-        const int64_t gr = min(row0 + row[it], nrows - 1);
-        load(g + gr * rs + coff[it], dst + (it * NW + wave) * 1024);
+        const int r = row_of(it);
+        const int64_t gr = min(row0 + r, nrows - 1);
+        load(g + gr * rs + coff_of(r), dst + (it * NW + wave) * 1024);
       }
     }
   }
@@ -581,6 +566,14 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
     const char* Kt = lds + buf * STAGE;
     const char* Vt = Kt + L::TILE;
     buf ^= 1;
+    // a tile none of this wave's queries can see (past the causal diagonal
+    // of its last query, or before the window of its first) adds nothing:
+    // the wave keeps the block's loads and barriers and skips the math
+    if constexpr (MASK) {
+      const int64_t qf = q0 + wave * QPW;
+      if (p.causal && kb0 > qf + QPW - 1) return;
+      if (p.window > 0 && kb0 + 63 < qf - p.window + 1) return;
+    }
       f32x4 s[4][QT];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
@@ -698,8 +691,10 @@ struct AttnBwdArgs {
   void* dq; int64_t dq_b, dq_h, dq_s;
   void* dk; int64_t dk_b, dk_h, dk_s;
   void* dv; int64_t dv_b, dv_h, dv_s;
-  float* delta;  // [B, H, Sq]
-  float* lse2;   // [B, H, Sq]: LSE * log2(e), written by attn_bwd_delta
+  float* ndelta;  // [B, H, Sq]: -D, written by attn_bwd_delta
+  float* nlse2;   // [B, H, Sq]: -LSE * log2(e), written by attn_bwd_delta
+  // (stored negated: the dK/dV and dQ steps add them, which saves a negation
+  // per score)
 };
 
 // D_i = sum_d dO[i, d] * O[i, d]: D/8 lanes per row, one 16-byte load of
@@ -723,8 +718,8 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_delta(AttnBwdArgs p) {
 #pragma unroll
   for (int off = CPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if (row < total && ch == 0) {
-    p.delta[row] = acc;
-    p.lse2[row] = p.f.lse[row] * kLog2e;
+    p.ndelta[row] = -acc;
+    p.nlse2[row] = -p.f.lse[row] * kLog2e;
   }
 }
 
@@ -750,7 +745,7 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dkv(AttnBwdArgs p) {
   const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
   const T* dO = (const T*)p.dout + b * p.do_b + h * p.do_h;
   const float* LSE = f.lse + (b * f.H + h) * f.Sq;
-  const float* DEL = p.delta + (b * f.H + h) * f.Sq;
+  const float* DEL = p.ndelta + (b * f.H + h) * f.Sq;
 
   const int64_t kw = k0 + wave * 16;  // this wave's 16 keys
   const int64_t kj = kw + lr;        // key of this lane's MFMA column
@@ -772,7 +767,7 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dkv(AttnBwdArgs p) {
     if (threadIdx.x < 64) {
       const int64_t qi = qb0 + threadIdx.x;
       lse_s[threadIdx.x] = qi < f.Sq ? LSE[qi] * kLog2e : 0.f;
-      delta_s[threadIdx.x] = qi < f.Sq ? DEL[qi] : 0.f;
+      delta_s[threadIdx.x] = qi < f.Sq ? -DEL[qi] : 0.f;
     }
     __syncthreads();
     // S and dP tiles: lane = key column, rows = queries 4*lg + e of tile qt
@@ -862,7 +857,7 @@ __global__ void __launch_bounds__(kThreads) attn_bwd_dq(AttnBwdArgs p) {
     df[ks] = qok ? *(const frag*)(dO + qi * p.do_s + ks * 32 + lg * 8) : zero_frag<T>();
   }
   const float lse2 = qok ? f.lse[(b * f.H + h) * f.Sq + qi] * kLog2e : 0.f;
-  const float dlt = qok ? p.delta[(b * f.H + h) * f.Sq + qi] : 0.f;
+  const float dlt = qok ? -p.ndelta[(b * f.H + h) * f.Sq + qi] : 0.f;
   f32x4 dqa[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dqa[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -954,8 +949,8 @@ __device__ __forceinline__ void dkv_body(const AttnBwdArgs& p, GridPos gp, char*
   const T* K = (const T*)f.k + b * f.k_b + h * f.k_h;
   const T* V = (const T*)f.v + b * f.v_b + h * f.v_h;
   const char* dO = (const char*)((const T*)p.dout + b * p.do_b + h * p.do_h);
-  const float* LSE = p.lse2 + (b * f.H + h) * f.Sq;
-  const float* DEL = p.delta + (b * f.H + h) * f.Sq;
+  const float* LSE = p.nlse2 + (b * f.H + h) * f.Sq;   // -LSE * log2(e)
+  const float* DEL = p.ndelta + (b * f.H + h) * f.Sq;  // -D
   const int64_t qs_b = f.q_s * (int64_t)sizeof(T), dos_b = p.do_s * (int64_t)sizeof(T);
 
   const int64_t kw = k0 + wave * 32;
@@ -974,14 +969,17 @@ __device__ __forceinline__ void dkv_body(const AttnBwdArgs& p, GridPos gp, char*
   for (int dt = 0; dt < DT; ++dt)
     dva[dt][0] = dva[dt][1] = dka[dt][0] = dka[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  KvTileLoad<D, 4> ql, dl;
+  ql.init(Q, qs_b);
+  dl.init(dO, dos_b);
   auto issue = [&](int64_t qb0, char* st) {
-    kv_tile_issue<D>(Q, qs_b, qb0, f.Sq, st);
-    kv_tile_issue<D>(dO, dos_b, qb0, f.Sq, st + L::TILE);
+    ql.issue(qb0, f.Sq, st);
+    dl.issue(qb0, f.Sq, st + L::TILE);
     if (wave < 2) {
       int64_t qi = qb0 + lane;
       if (qi >= f.Sq) qi = f.Sq - 1;
       const float* src = (wave == 0 ? LSE : DEL) + qi;
-      __builtin_amdgcn_global_load_lds((gptr_t)src, (lptr_t)(st + 2 * L::TILE + wave * 256), 4, 0, 0);
+      dma_b32(src, lds_base_of(st + 2 * L::TILE + wave * 256));
     }
   };
 
@@ -1011,8 +1009,22 @@ __device__ __forceinline__ void dkv_body(const AttnBwdArgs& p, GridPos gp, char*
       const int k_lim = (int)min((int64_t)32, f.Skv - kw);   // key rows < k_lim exist
       const int kq = (int)max((int64_t)-128, min((int64_t)128, kw - qb0));  // key row 0 minus query row 0
       const float c = f.scale_log2;
+      // Masked steps keep query row qr of key row kr iff lo[t] <= qr <
+      // q_lim (lo = the causal diagonal), tested as one unsigned compare
+      // (qr - lo[t]) < span[t]; a dropped score's exponent is -inf, so the
+      // exp2 runs unconditionally and gives 0 (no branch per element).
+      int lo[2], span[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int kr = t * 16 + lr;
+        lo[t] = f.causal ? max(0, kq + kr) : 0;
+        span[t] = kr < k_lim ? max(0, q_lim - lo[t]) : 0;
+      }
 #pragma unroll
       for (int qs = 0; qs < 2; ++qs) {
+        // on the causal diagonal, a pair of query tiles that lies wholly
+        // before this wave's first key contributes nothing
+        if (MASK && f.causal && qs * 32 + 31 < kq) continue;
         f32x4 pt[2][2], ds[2][2];  // [query tile in pair][key tile]
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -1030,20 +1042,20 @@ __device__ __forceinline__ void dkv_body(const AttnBwdArgs& p, GridPos gp, char*
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
             // dP - D: the accumulator of dO V^T starts at -D
-            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {-d4.x, -d4.y, -d4.z, -d4.w};
+            f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
               sa = Mfma<T>::mma(qa[ks], kf[t][ks], sa);
               pa = Mfma<T>::mma(da[ks], vf[t][ks], pa);
             }
-            const int kr = t * 16 + lr;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              float pv = fast_exp2(fmaf(sa[e], c, -lv[e]));
+              float x = fmaf(sa[e], c, lv[e]);
               if constexpr (MASK) {
                 const int qr = qt * 16 + 4 * lg + e;
-                if (qr >= q_lim || kr >= k_lim || (f.causal && kq + kr > qr)) pv = 0.f;
+                x = (unsigned)(qr - lo[t]) < (unsigned)span[t] ? x : -INFINITY;
               }
+              const float pv = fast_exp2(x);
               pt[u][t][e] = pv;
               ds[u][t][e] = pv * pa[e];
             }
@@ -1135,8 +1147,8 @@ __device__ __forceinline__ void dq_body(const AttnBwdArgs& p, GridPos gp, char* 
       qf[u][ks] = ok ? *(const frag*)(Q + qi * f.q_s + ks * 32 + lg * 8) : zero_frag<T>();
       df[u][ks] = ok ? *(const frag*)(dO + qi * p.do_s + ks * 32 + lg * 8) : zero_frag<T>();
     }
-    lse2[u] = ok ? p.lse2[(b * f.H + h) * f.Sq + qi] : 0.f;
-    dlt[u] = ok ? -p.delta[(b * f.H + h) * f.Sq + qi] : 0.f;  // -D, the start of dP - D
+    lse2[u] = ok ? p.nlse2[(b * f.H + h) * f.Sq + qi] : 0.f;  // -LSE * log2(e)
+    dlt[u] = ok ? p.ndelta[(b * f.H + h) * f.Sq + qi] : 0.f;  // -D, the start of dP - D
   }
   f32x4 dqa[DT][2];
 #pragma unroll
@@ -1147,8 +1159,11 @@ __device__ __forceinline__ void dq_body(const AttnBwdArgs& p, GridPos gp, char* 
   const int sw = L::swz(lr);
   const TrOffsets<D> tro;
   int buf = 0;
-  kv_tile_issue<D>(K, ks_b, 0, f.Skv, lds);
-  kv_tile_issue<D>(V, vs_b, 0, f.Skv, lds + L::TILE);
+  KvTileLoad<D, 4> kl, vl;
+  kl.init(K, ks_b);
+  vl.init(V, vs_b);
+  kl.issue(0, f.Skv, lds);
+  vl.issue(0, f.Skv, lds + L::TILE);
   // One step per 64 keys: unmasked steps first, then the ones that cross
   // this wave's causal diagonal or the key end (or all of them when the
   // wave's queries cross the query end); same step count on every wave.
@@ -1159,8 +1174,8 @@ __device__ __forceinline__ void dq_body(const AttnBwdArgs& p, GridPos gp, char* 
     __syncthreads();
     if (kb0 + 64 < kv_end) {
       char* nx = lds + (buf ^ 1) * STAGE;
-      kv_tile_issue<D>(K, ks_b, kb0 + 64, f.Skv, nx);
-      kv_tile_issue<D>(V, vs_b, kb0 + 64, f.Skv, nx + L::TILE);
+      kl.issue(kb0 + 64, f.Skv, nx);
+      vl.issue(kb0 + 64, f.Skv, nx + L::TILE);
     }
     const char* Kt = lds + buf * STAGE;
     const char* Vt = Kt + L::TILE;
@@ -1170,8 +1185,20 @@ __device__ __forceinline__ void dq_body(const AttnBwdArgs& p, GridPos gp, char* 
       const int k_lim = (int)min((int64_t)64, f.Skv - kb0);  // key rows < k_lim exist
       const int qk = (int)max((int64_t)-128, min((int64_t)128, qw - kb0));  // query row 0 minus key row 0
       const float c = f.scale_log2;
+      // Masked steps keep key row kr of query row qr iff kr < lim[u]
+      // (the key end, the causal diagonal, nothing past the query end); a
+      // dropped score's exponent is -inf (no branch per element).
+      int lim[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int qr = u * 16 + lr;
+        lim[u] = qr < q_lim ? (f.causal ? min(k_lim, qk + qr + 1) : k_lim) : 0;
+      }
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
+        // on the causal diagonal, a pair of key tiles that lies wholly after
+        // this wave's last query contributes nothing
+        if (MASK && f.causal && ks2 * 32 > qk + 31) continue;
         f32x4 ds[2][2];  // [key tile in pair][query tile]
 #pragma unroll
         for (int v2 = 0; v2 < 2; ++v2) {
@@ -1191,15 +1218,11 @@ __device__ __forceinline__ void dq_body(const AttnBwdArgs& p, GridPos gp, char* 
               sa = Mfma<T>::mma(ka[ks], qf[u][ks], sa);
               pa = Mfma<T>::mma(va[ks], df[u][ks], pa);
             }
-            const int qr = u * 16 + lr;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              float pv = fast_exp2(fmaf(sa[e], c, -lse2[u]));
-              if constexpr (MASK) {
-                const int kr = kt * 16 + 4 * lg + e;
-                if (qr >= q_lim || kr >= k_lim || (f.causal && kr > qk + qr)) pv = 0.f;
-              }
-              ds[v2][u][e] = pv * pa[e];
+              float x = fmaf(sa[e], c, lse2[u]);
+              if constexpr (MASK) x = kt * 16 + 4 * lg + e < lim[u] ? x : -INFINITY;
+              ds[v2][u][e] = fast_exp2(x) * pa[e];
             }
           }
         }
@@ -1485,8 +1508,8 @@ extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const 
   a.dq = dq; a.dq_b = dq_bhs[0]; a.dq_h = dq_bhs[1]; a.dq_s = dq_bhs[2];
   a.dk = dk; a.dk_b = dk_bhs[0]; a.dk_h = dk_bhs[1]; a.dk_s = dk_bhs[2];
   a.dv = dv; a.dv_b = dv_bhs[0]; a.dv_h = dv_bhs[1]; a.dv_s = dv_bhs[2];
-  a.delta = (float*)workspace;
-  a.lse2 = a.delta + batch * heads * sq;
+  a.ndelta = (float*)workspace;
+  a.nlse2 = a.ndelta + batch * heads * sq;
   MI_ATTN_DISPATCH(dtype, d, bwd_launch, a, (hipStream_t)stream);
 }
 
