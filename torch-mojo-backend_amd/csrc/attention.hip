@@ -574,7 +574,26 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
       if (p.causal && kb0 > qf + QPW - 1) return;
       if (p.window > 0 && kb0 + 63 < qf - p.window + 1) return;
     }
+      // Per query tile, the keys kb0 + lo..lim are visible to this lane's query.
+      int lo[QT], lim[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        lo[qt] = 0;
+        lim[qt] = 63;
+        if constexpr (MASK) {
+          const int64_t qi = q0 + wave * QPW + qt * 16 + lr;
+          int64_t lm = p.Skv - 1 - kb0;
+          if (p.causal && qi - kb0 < lm) lm = qi - kb0;
+          lim[qt] = (int)max((int64_t)-1, min((int64_t)63, lm));
+          if (p.window > 0) lo[qt] = (int)max((int64_t)0, min((int64_t)64, qi - p.window + 1 - kb0));
+        }
+      }
+      // S^T tiles, each masked and folded into the row maxima right after
+      // its MFMAs, so that work can issue beside the next tile's MFMAs.
       f32x4 s[4][QT];
+      float mx[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) mx[qt] = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         frag kf[KS];
@@ -586,33 +605,32 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
           f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int ks = 0; ks < KS; ++ks) a = Mfma<T>::mma(kf[ks], qf[qt][ks], a);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = POS ? a[e] : a[e] * c;
+            if (MASK && (kt * 16 + lg * 4 + e > lim[qt] || kt * 16 + lg * 4 + e < lo[qt])) v = -INFINITY;
+            a[e] = v;
+            mx[qt] = fmaxf(mx[qt], v);
+          }
           s[kt][qt] = a;
         }
       }
+      // One rescale decision for the wave's query tiles (a uniform branch):
+      // the exponentials and P V products after it are one branch-free
+      // region, so the second key half's exponentials can issue beside the
+      // first half's MFMAs.
+      float mxc[QT];
+      bool need = false;
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
-        int lo = 0, lim = 63;  // keys kb0 + lo..lim are visible to this lane's query
-        if constexpr (MASK) {
-          const int64_t qi = q0 + wave * QPW + qt * 16 + lr;
-          int64_t lm = p.Skv - 1 - kb0;
-          if (p.causal && qi - kb0 < lm) lm = qi - kb0;
-          lim = (int)max((int64_t)-1, min((int64_t)63, lm));
-          if (p.window > 0) lo = (int)max((int64_t)0, min((int64_t)64, qi - p.window + 1 - kb0));
-        }
-        float mx = -INFINITY;
+        const float g = group_max(mx[qt]);
+        mxc[qt] = POS ? g * c : g;
+        need |= mxc[qt] > m[qt] + kSlack;
+      }
+      if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float v = POS ? s[kt][qt][e] : s[kt][qt][e] * c;
-            if (MASK && (kt * 16 + lg * 4 + e > lim || kt * 16 + lg * 4 + e < lo)) v = -INFINITY;
-            s[kt][qt][e] = v;
-            mx = fmaxf(mx, v);
-          }
-        mx = group_max(mx);
-        const float mxc = POS ? mx * c : mx;
-        if (__builtin_amdgcn_ballot_w64(mxc > m[qt] + kSlack)) {
-          const float m_new = fmaxf(m[qt], mxc);
+        for (int qt = 0; qt < QT; ++qt) {
+          const float m_new = fmaxf(m[qt], mxc[qt]);
           // a row with every key so far masked (m_new = -inf, nothing
           // accumulated) keeps its state: exp2(-inf - -inf) would be NaN
           const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m[qt] - m_new);
@@ -621,23 +639,22 @@ __global__ void __launch_bounds__(64 * NW, D == 64 ? ATTN_FWD_BLOCKS * NW / 4 : 
           for (int dt = 0; dt < DT; ++dt) oacc[dt][qt] *= alpha;
           m[qt] = m_new;
         }
-        const float m_use = m[qt] == -INFINITY ? 0.f : m[qt];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            s[kt][qt][e] = fast_exp2(POS ? fmaf(s[kt][qt][e], c, -m_use) : s[kt][qt][e] - m_use);
       }
+      float m_use[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) m_use[qt] = m[qt] == -INFINITY ? 0.f : m[qt];
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
         frag pf[QT];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            pf[qt][e] = (T)s[2 * ks2][qt][e];
-            pf[qt][4 + e] = (T)s[2 * ks2 + 1][qt][e];
-          }
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float x = s[2 * ks2 + h][qt][e];
+              pf[qt][4 * h + e] = (T)fast_exp2(POS ? fmaf(x, c, -m_use[qt]) : x - m_use[qt]);
+            }
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) lacc[qt] = Mfma<T>::mma(ones, pf[qt], lacc[qt]);
 #pragma unroll
