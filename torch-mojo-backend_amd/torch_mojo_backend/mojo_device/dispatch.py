@@ -20,9 +20,16 @@ DIRECT: dict = {}
 _DISABLE = torch._C._DisableTorchDispatch
 
 
+_MUTABLE: dict = {}  # OpOverload -> whether its schema writes an argument
+
+
 def dispatch(func, args, kwargs):
-    if _aten_fast.param_copies_active() and func._schema.is_mutable:
-        _aten_fast.drop_param_copies_written_by(func, args, kwargs)
+    if _aten_fast._param_low_by_holder:  # parameter copies exist (autocast training)
+        mutable = _MUTABLE.get(func)
+        if mutable is None:
+            mutable = _MUTABLE[func] = func._schema.is_mutable
+        if mutable:
+            _aten_fast.drop_param_copies_written_by(func, args, kwargs)
     impl = DIRECT.get(func)
     if impl is not None:
         return impl(*args, **kwargs)

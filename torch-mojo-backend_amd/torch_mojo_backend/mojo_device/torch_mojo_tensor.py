@@ -142,10 +142,11 @@ class TorchMojoTensor(torch.Tensor):
 
     @classmethod
     def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
-        for t in types:
-            if not issubclass(cls, t):
-                return NotImplemented
-        return _dispatch_module().dispatch(func, args, kwargs or {})
+        if len(types) != 1 or types[0] is not cls:
+            for t in types:
+                if not issubclass(cls, t):
+                    return NotImplemented
+        return (_DISPATCH or _dispatch_module()).dispatch(func, args, kwargs or {})
 
     __torch_function__ = torch._C._disabled_torch_function_impl
 
