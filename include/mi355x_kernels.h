@@ -528,7 +528,11 @@ int mi355x_attn_fwd_gen(void* o, const int64_t* o_bhs, float* lse, const void* q
                         const void* v, const int64_t* v_bhs, int64_t batch, int64_t heads,
                         int64_t kv_heads, int64_t sq, int64_t skv, int64_t d, double scale,
                         int causal, int64_t window, int dtype, mi355x_stream_t stream);
-int64_t mi355x_attn_bwd_gen_workspace_bytes(int64_t batch, int64_t heads, int64_t sq);
+/* Workspace of mi355x_attn_bwd_gen: 2 floats per query row, plus (grouped
+ * heads) 2 * batch * heads * skv * d floats of per-query-head dK/dV
+ * partials that the bf16/f16 MFMA backward sums in head order. */
+int64_t mi355x_attn_bwd_gen_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads,
+                                            int64_t sq, int64_t skv, int64_t d);
 int mi355x_attn_bwd_gen(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs,
                         void* dv, const int64_t* dv_bhs, const void* dout,
                         const int64_t* do_bhs, const void* q, const int64_t* q_bhs,

@@ -595,7 +595,7 @@ class HostStandIn:
         return self.mi355x_attn_fwd_ex(o, obhs, lse, q, qbhs, k, kbhs, v, vbhs, B, H, Hk, Sq, Skv, D, scale,
                                        causal, window, dt, stream)
 
-    def mi355x_attn_bwd_gen_workspace_bytes(self, B, H, Sq):
+    def mi355x_attn_bwd_gen_workspace_bytes(self, B, H, Hk, Sq, Skv, D):
         return 16
 
     def mi355x_attn_bwd_gen(self, dq, dqs, dk, dks, dv, dvs, do, dos, q, qs, k, ks, v, vs, o, os_, lse,

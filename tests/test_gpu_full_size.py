@@ -137,7 +137,7 @@ def test_attention_gemma_shape_window_slices_match_oracle(kernels):
     dq = torch.empty(B, T, H, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
     dk = torch.empty(B, T, Hk, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
     dv = torch.empty(B, T, Hk, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
-    ws_n = lib().mi355x_attn_bwd_gen_workspace_bytes(B, H, T)
+    ws_n = lib().mi355x_attn_bwd_gen_workspace_bytes(B, H, Hk, T, T, D)
     ws = workspace(ws_n)
     call("mi355x_attn_bwd_gen", p(dq), bhs(dq), p(dk), bhs(dk), p(dv), bhs(dv), p(tdo), bhs(tdo),
          p(tq), bhs(tq), p(tk), bhs(tk), p(tv), bhs(tv), p(o), bhs(o), p(lse),

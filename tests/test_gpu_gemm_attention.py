@@ -361,7 +361,7 @@ def _attn_gen(q, k, v, do, causal, window, scale=None):
     dq = torch.empty(B, Sq, H, D, dtype=q.dtype, device="cuda").transpose(1, 2)
     dk = torch.empty(B, Skv, Hk, D, dtype=q.dtype, device="cuda").transpose(1, 2)
     dv = torch.empty(B, Skv, Hk, D, dtype=q.dtype, device="cuda").transpose(1, 2)
-    ws_n = lib().mi355x_attn_bwd_gen_workspace_bytes(B, H, Sq)
+    ws_n = lib().mi355x_attn_bwd_gen_workspace_bytes(B, H, Hk, Sq, Skv, D)
     ws = workspace(ws_n)
     call("mi355x_attn_bwd_gen", p(dq), bhs(dq), p(dk), bhs(dk), p(dv), bhs(dv), p(do), bhs(do),
          p(q), bhs(q), p(k), bhs(k), p(v), bhs(v), p(o), bhs(o), p(lse),

@@ -710,6 +710,7 @@ struct AttnBwdArgs {
   void* dv; int64_t dv_b, dv_h, dv_s;
   float* ndelta;  // [B, H, Sq]: -D, written by attn_bwd_delta
   float* nlse2;   // [B, H, Sq]: -LSE * log2(e), written by attn_bwd_delta
+  float* kv_part; // grouped backward: per-query-head dK, dV partials (f32), or null
   // (stored negated: the dK/dV and dQ steps add them, which saves a negation
   // per score)
 };
@@ -1310,6 +1311,328 @@ __global__ void __launch_bounds__(kThreads, D == 64 ? ATTN_BWD_WAVES : 1) attn_b
 }
 
 // ---------------------------------------------------------------------------
+// backward with grouped K/V heads and sliding windows (MFMA), head_dim
+// 64/128/256
+//
+// dK/dV: a block owns 64 keys of one K/V head (a wave 16, their K and V rows
+// held in registers) and walks, for each of the group's query heads, the
+// 64-query steps that can see them (causal: query >= key; window w: query <
+// key + w), staging Q, dO and the row terms of the step through LDS; the
+// group's contributions add up in the same accumulators, so dK and dV of a
+// K/V head are the sums over its query heads without atomics.
+// dQ: a block owns 64 queries of one query head (a wave 16) and walks the
+// visible 64-key steps of its K/V head.
+// Per step and wave the visible (query, key) pairs are one interval of query
+// rows per key (dK/dV) or of key rows per query (dQ), tested with a single
+// unsigned compare; steps wholly inside every wave's visible band skip the
+// test, and pairs of 16-row tiles wholly outside it skip their MFMAs.
+// ---------------------------------------------------------------------------
+template <int D>
+constexpr int kGqaDkvLds = 2 * (2 * KvLayout<D>::TILE + 512);  // 2 stages of Q, dO, -LSE log2e[64], -D[64]
+template <int D>
+constexpr int kGqaDqLds = 2 * (2 * KvLayout<D>::TILE);  // 2 stages of K, V
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, 1) attn_bwd_gqa_dkv(AttnBwdArgs p) {
+  typedef typename Mfma<T>::frag frag;
+  typedef KvLayout<D> L;
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int STAGE = 2 * L::TILE + 512;
+  char* const lds = attn_dyn_lds;
+  const AttnArgs& f = p.f;
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lr = lane & 15, lg = lane >> 4;
+  const int64_t k0 = (int64_t)blockIdx.x * 64;
+  // with partials, block (x, hk * group + gi) takes query head gi of the
+  // group alone; without, it walks the whole group
+  const int64_t hsplit = p.kv_part ? f.group : 1;
+  const int64_t hk = blockIdx.y / hsplit, gfirst = blockIdx.y - hk * hsplit, b = blockIdx.z;
+  const int64_t kw = k0 + wave * 16, kj = kw + lr;
+  const T* K = (const T*)f.k + b * f.k_b + hk * f.k_h;
+  const T* V = (const T*)f.v + b * f.v_b + hk * f.v_h;
+  frag kf[KS], vf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    kf[ks] = kj < f.Skv ? *(const frag*)(K + kj * f.k_s + ks * 32 + lg * 8) : zero_frag<T>();
+    vf[ks] = kj < f.Skv ? *(const frag*)(V + kj * f.v_s + ks * 32 + lg * 8) : zero_frag<T>();
+  }
+  f32x4 dva[DT], dka[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dva[dt] = dka[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // queries that can see keys k0 .. k0 + 63, in 64-query steps from qstart
+  int64_t qhi = f.Sq;
+  if (f.window > 0) qhi = min(qhi, k0 + 63 + f.window);
+  const int64_t qstart = f.causal ? (k0 / 64) * 64 : 0;
+  const int64_t nqb = qhi > qstart ? (qhi - qstart + 63) / 64 : 0;
+  const int64_t nheads = p.kv_part ? 1 : f.group;
+  const int64_t total = nqb * nheads;  // steps over (query head, query block)
+  const int64_t qs_b = f.q_s * (int64_t)sizeof(T), dos_b = p.do_s * (int64_t)sizeof(T);
+  KvTileLoad<D, 4> ql, dl;
+  ql.init(nullptr, qs_b);
+  dl.init(nullptr, dos_b);
+  auto issue = [&](int64_t st, char* dst) {
+    const int64_t gi = st / nqb, qb0 = qstart + (st - gi * nqb) * 64;
+    const int64_t h = hk * f.group + gfirst + gi;
+    ql.g = (const char*)((const T*)f.q + b * f.q_b + h * f.q_h);
+    dl.g = (const char*)((const T*)p.dout + b * p.do_b + h * p.do_h);
+    ql.issue(qb0, f.Sq, dst);
+    dl.issue(qb0, f.Sq, dst + L::TILE);
+    if (wave < 2) {
+      const int64_t qi = min(qb0 + lane, f.Sq - 1);
+      const float* src = (wave == 0 ? p.nlse2 : p.ndelta) + (b * f.H + h) * f.Sq + qi;
+      dma_b32(src, lds_base_of(dst + 2 * L::TILE + wave * 256));
+    }
+  };
+  const int sw = L::swz(lr);
+  const TrOffsets<D> tro;
+  const float c = f.scale_log2;
+  auto compute = [&](const char* Qt, int64_t qb0, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const char* dOt = Qt + L::TILE;
+    const float* lse_s = (const float*)(Qt + 2 * L::TILE);
+    const float* del_s = lse_s + 64;
+    const int64_t kq = kw - qb0;  // key row 0 minus query row 0
+    // query rows lo <= qr < lo + span see this lane's key
+    int lo = 0, span = 64;
+    if constexpr (MASK) {
+      const int64_t lo64 = f.causal ? max((int64_t)0, kq + lr) : 0;
+      int64_t hi = min((int64_t)64, f.Sq - qb0);
+      if (f.window > 0) hi = min(hi, kq + lr + f.window);
+      lo = (int)min((int64_t)64, lo64);
+      span = kj < f.Skv ? (int)max((int64_t)0, hi - lo64) : 0;
+    }
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      if (MASK && f.causal && qs * 32 + 31 < kq) continue;                // every query before every key
+      if (MASK && f.window > 0 && qs * 32 >= kq + 15 + f.window) continue;  // past every key's window
+      f32x4 pt[2], ds[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int qt = 2 * qs + u;
+        const float4 l4 = *(const float4*)(lse_s + qt * 16 + 4 * lg);
+        const float4 d4 = *(const float4*)(del_s + qt * 16 + 4 * lg);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {d4.x, d4.y, d4.z, d4.w};  // dP - D
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int off = (qt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4);
+          sa = Mfma<T>::mma(*(const frag*)(Qt + off), kf[ks], sa);
+          pa = Mfma<T>::mma(*(const frag*)(dOt + off), vf[ks], pa);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = fmaf(sa[e], c, lv[e]);
+          if constexpr (MASK) x = (unsigned)(qt * 16 + 4 * lg + e - lo) < (unsigned)span ? x : -INFINITY;
+          const float pv = fast_exp2(x);
+          pt[u][e] = pv;
+          ds[u][e] = pv * pa[e];
+        }
+      }
+      frag pb, sb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pb[e] = (T)pt[0][e];
+        pb[4 + e] = (T)pt[1][e];
+        sb[e] = (T)ds[0][e];
+        sb[4 + e] = (T)ds[1][e];
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        dva[dt] = Mfma<T>::mma(tr_frag_at<T, D>(dOt, tro, dt, 2 * qs, 2 * qs + 1), pb, dva[dt]);
+        dka[dt] = Mfma<T>::mma(tr_frag_at<T, D>(Qt, tro, dt, 2 * qs, 2 * qs + 1), sb, dka[dt]);
+      }
+    }
+  };
+  int buf = 0;
+  if (total > 0) issue(0, lds);
+  for (int64_t st = 0; st < total; ++st) {
+    __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
+    __syncthreads();
+    if (st + 1 < total) issue(st + 1, lds + (buf ^ 1) * STAGE);
+    const char* Qt = lds + buf * STAGE;
+    buf ^= 1;
+    const int64_t qb0 = qstart + (st % nqb) * 64;
+    if (f.causal && kw > qb0 + 63) continue;                     // every query before every key
+    if (f.window > 0 && qb0 >= kw + 15 + f.window) continue;     // past every key's window
+    const bool inside = (!f.causal || qb0 >= kw + 15) && (f.window <= 0 || qb0 + 63 < kw + f.window) &&
+                        qb0 + 64 <= f.Sq && kw + 16 <= f.Skv;
+    if (inside) compute(Qt, qb0, BoolTag<false>{});
+    else compute(Qt, qb0, BoolTag<true>{});
+  }
+  if (kj < f.Skv && p.kv_part) {
+    // f32 partials [gi][b][hk][key][D], dK's then dV's; summed by attn_bwd_gqa_sum
+    const int64_t hkn = f.H / f.group, plane = f.group * f.B * hkn * f.Skv * D;
+    float* pk = p.kv_part + (((gfirst * f.B + b) * hkn + hk) * f.Skv + kj) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      *(float4*)(pk + dt * 16 + lg * 4) = float4{dka[dt][0], dka[dt][1], dka[dt][2], dka[dt][3]};
+      *(float4*)(pk + plane + dt * 16 + lg * 4) = float4{dva[dt][0], dva[dt][1], dva[dt][2], dva[dt][3]};
+    }
+  } else if (kj < f.Skv) {
+    T* dK = (T*)p.dk + b * p.dk_b + hk * p.dk_h + kj * p.dk_s;
+    T* dV = (T*)p.dv + b * p.dv_b + hk * p.dv_h + kj * p.dv_s;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      V4<T> k4, v4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        k4.v[e] = (T)(dka[dt][e] * f.scale);
+        v4.v[e] = (T)dva[dt][e];
+      }
+      *(V4<T>*)(dK + dt * 16 + lg * 4) = k4;
+      *(V4<T>*)(dV + dt * 16 + lg * 4) = v4;
+    }
+  }
+}
+
+// dK = scale * sum over the group's query heads of the dK partials, dV = the
+// sum of the dV partials, in head order (deterministic); four head-dim
+// elements per thread.
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads) attn_bwd_gqa_sum(AttnBwdArgs p) {
+  const AttnArgs& f = p.f;
+  const int64_t hkn = f.H / f.group, rows = f.B * hkn * f.Skv, plane = f.group * rows * D;
+  const int64_t i4 = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // over rows * D / 4
+  if (i4 >= rows * (D / 4)) return;
+  const int64_t row = i4 / (D / 4), d = (i4 - row * (D / 4)) * 4;
+  const int64_t key = row % f.Skv, bh = row / f.Skv, hk = bh % hkn, b = bh / hkn;
+  float4 sk = {0.f, 0.f, 0.f, 0.f}, sv = sk;
+  for (int64_t g = 0; g < f.group; ++g) {
+    const float4 a = *(const float4*)(p.kv_part + g * rows * D + row * D + d);
+    const float4 c = *(const float4*)(p.kv_part + plane + g * rows * D + row * D + d);
+    sk.x += a.x, sk.y += a.y, sk.z += a.z, sk.w += a.w;
+    sv.x += c.x, sv.y += c.y, sv.z += c.z, sv.w += c.w;
+  }
+  V4<T> k4, v4;
+  k4.v[0] = (T)(sk.x * f.scale), k4.v[1] = (T)(sk.y * f.scale), k4.v[2] = (T)(sk.z * f.scale), k4.v[3] = (T)(sk.w * f.scale);
+  v4.v[0] = (T)sv.x, v4.v[1] = (T)sv.y, v4.v[2] = (T)sv.z, v4.v[3] = (T)sv.w;
+  *(V4<T>*)((T*)p.dk + b * p.dk_b + hk * p.dk_h + key * p.dk_s + d) = k4;
+  *(V4<T>*)((T*)p.dv + b * p.dv_b + hk * p.dv_h + key * p.dv_s + d) = v4;
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(kThreads, 1) attn_bwd_gqa_dq(AttnBwdArgs p) {
+  typedef typename Mfma<T>::frag frag;
+  typedef KvLayout<D> L;
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int STAGE = 2 * L::TILE;
+  char* const lds = attn_dyn_lds;
+  const AttnArgs& f = p.f;
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lr = lane & 15, lg = lane >> 4;
+  // causal: the heaviest query blocks first
+  const int64_t qblock = f.causal && f.window <= 0 ? (int64_t)gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const int64_t q0 = qblock * 64;
+  const int64_t h = blockIdx.y, b = blockIdx.z, hk = h / f.group;
+  const int64_t qw = q0 + wave * 16, qi = qw + lr;
+  const bool qok = qi < f.Sq;
+  const T* Q = (const T*)f.q + b * f.q_b + h * f.q_h;
+  const T* dO = (const T*)p.dout + b * p.do_b + h * p.do_h;
+  frag qf[KS], df[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qf[ks] = qok ? *(const frag*)(Q + qi * f.q_s + ks * 32 + lg * 8) : zero_frag<T>();
+    df[ks] = qok ? *(const frag*)(dO + qi * p.do_s + ks * 32 + lg * 8) : zero_frag<T>();
+  }
+  const float nl2 = qok ? p.nlse2[(b * f.H + h) * f.Sq + qi] : 0.f;   // -LSE log2e
+  const float ndl = qok ? p.ndelta[(b * f.H + h) * f.Sq + qi] : 0.f;  // -D, the start of dP - D
+  f32x4 dqa[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dqa[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int64_t khi = f.Skv;
+  if (f.causal) khi = min(khi, q0 + 64);
+  const int64_t klo = f.window > 0 ? max((int64_t)0, q0 - f.window + 1) : 0;
+  const int64_t kstart = (klo / 64) * 64;
+  const int64_t nkb = khi > kstart ? (khi - kstart + 63) / 64 : 0;
+  KvTileLoad<D, 4> kl, vl;
+  kl.init((const char*)((const T*)f.k + b * f.k_b + hk * f.k_h), f.k_s * (int64_t)sizeof(T));
+  vl.init((const char*)((const T*)f.v + b * f.v_b + hk * f.v_h), f.v_s * (int64_t)sizeof(T));
+  const int sw = L::swz(lr);
+  const TrOffsets<D> tro;
+  const float c = f.scale_log2;
+  auto compute = [&](const char* Kt, int64_t kb0, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const char* Vt = Kt + L::TILE;
+    const int64_t qk = qw - kb0;  // query row 0 minus key row 0
+    // key rows lo <= kr < lo + span are visible to this lane's query
+    int lo = 0, span = 64;
+    if constexpr (MASK) {
+      const int64_t lo64 = f.window > 0 ? max((int64_t)0, qk + lr - f.window + 1) : 0;
+      int64_t hi = min((int64_t)64, f.Skv - kb0);
+      if (f.causal) hi = min(hi, qk + lr + 1);
+      lo = (int)min((int64_t)64, lo64);
+      span = qok ? (int)max((int64_t)0, hi - lo64) : 0;
+    }
+#pragma unroll
+    for (int ks2 = 0; ks2 < 2; ++ks2) {
+      if (MASK && f.causal && ks2 * 32 > qk + 15) continue;                      // after every query
+      if (MASK && f.window > 0 && ks2 * 32 + 31 < qk - f.window + 1) continue;  // before every window
+      f32x4 ds[2];
+#pragma unroll
+      for (int v2 = 0; v2 < 2; ++v2) {
+        const int kt = 2 * ks2 + v2;
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, pa = {ndl, ndl, ndl, ndl};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int off = (kt * 16 + lr) * L::ROWB + (((ks * 4 + lg) ^ sw) << 4);
+          sa = Mfma<T>::mma(*(const frag*)(Kt + off), qf[ks], sa);
+          pa = Mfma<T>::mma(*(const frag*)(Vt + off), df[ks], pa);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = fmaf(sa[e], c, nl2);
+          if constexpr (MASK) x = (unsigned)(kt * 16 + 4 * lg + e - lo) < (unsigned)span ? x : -INFINITY;
+          ds[v2][e] = fast_exp2(x) * pa[e];
+        }
+      }
+      frag sb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sb[e] = (T)ds[0][e];
+        sb[4 + e] = (T)ds[1][e];
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        dqa[dt] = Mfma<T>::mma(tr_frag_at<T, D>(Kt, tro, dt, 2 * ks2, 2 * ks2 + 1), sb, dqa[dt]);
+    }
+  };
+  int buf = 0;
+  if (nkb > 0) {
+    kl.issue(kstart, f.Skv, lds);
+    vl.issue(kstart, f.Skv, lds + L::TILE);
+  }
+  for (int64_t j = 0; j < nkb; ++j) {
+    const int64_t kb0 = kstart + j * 64;
+    __builtin_amdgcn_s_waitcnt(0xc07f & 0x3f70);  // vmcnt(0)
+    __syncthreads();
+    if (j + 1 < nkb) {
+      char* nx = lds + (buf ^ 1) * STAGE;
+      kl.issue(kb0 + 64, f.Skv, nx);
+      vl.issue(kb0 + 64, f.Skv, nx + L::TILE);
+    }
+    const char* Kt = lds + buf * STAGE;
+    buf ^= 1;
+    if (f.causal && kb0 > qw + 15) continue;                           // every key after every query
+    if (f.window > 0 && kb0 + 63 < qw - f.window + 1) continue;        // before every query's window
+    const bool inside = (!f.causal || kb0 + 63 <= qw) && (f.window <= 0 || kb0 > qw + 15 - f.window) &&
+                        kb0 + 64 <= f.Skv && qw + 16 <= f.Sq;
+    if (inside) compute(Kt, kb0, BoolTag<false>{});
+    else compute(Kt, kb0, BoolTag<true>{});
+  }
+  if (!qok) return;
+  T* dQ = (T*)p.dq + b * p.dq_b + h * p.dq_h + qi * p.dq_s;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    V4<T> q4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q4.v[e] = (T)(dqa[dt][e] * f.scale);
+    *(V4<T>*)(dQ + dt * 16 + lg * 4) = q4;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------
 bool strides_ok(const void* ptr, const int64_t* bhs) {
@@ -1402,7 +1725,78 @@ int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
     return FN<f16, 128>(__VA_ARGS__);                                         \
   } while (0)
 
+template <typename T, int D>
+int gqa_bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
+  const int64_t rows = a.f.B * a.f.H * a.f.Sq;
+  attn_bwd_delta<T, D><<<ceil_div(rows, kThreads / (D / 8)), kThreads, 0, s>>>(a);
+  auto kkv = attn_bwd_gqa_dkv<T, D>;
+  auto kq = attn_bwd_gqa_dq<T, D>;
+  constexpr int lkv = kGqaDkvLds<D>, lq = kGqaDqLds<D>;
+  static std::once_flag once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(once, [&] {
+    attr_err = hipFuncSetAttribute((const void*)kkv, hipFuncAttributeMaxDynamicSharedMemorySize, lkv);
+    if (attr_err == hipSuccess)
+      attr_err = hipFuncSetAttribute((const void*)kq, hipFuncAttributeMaxDynamicSharedMemorySize, lq);
+  });
+  if (attr_err != hipSuccess)
+    return fail(MI355X_ELAUNCH, "mi355x_attn_bwd_gen: cannot raise the LDS limit: %s", hipGetErrorString(attr_err));
+  // grouped heads: one dK/dV block per (key block, query head), partials summed after
+  const unsigned gy = (unsigned)(a.kv_part ? a.f.H : a.f.H / a.f.group);
+  kkv<<<dim3(ceil_div(a.f.Skv, 64), gy, (unsigned)a.f.B), kThreads, lkv, s>>>(a);
+  kq<<<dim3(ceil_div(a.f.Sq, 64), (unsigned)a.f.H, (unsigned)a.f.B), kThreads, lq, s>>>(a);
+  if (a.kv_part) {
+    const int64_t n4 = a.f.B * (a.f.H / a.f.group) * a.f.Skv * (D / 4);
+    attn_bwd_gqa_sum<T, D><<<ceil_div(n4, kThreads), kThreads, 0, s>>>(a);
+  }
+  return check_launch("mi355x_attn_bwd_gen");
+}
+
 }  // namespace
+
+// MFMA backward for grouped K/V heads and/or a sliding window, called by
+// mi355x_attn_bwd_gen (attention_generic.hip) for bf16/f16 at head_dim
+// 64/128/256 with 16-byte aligned operands; returns -1 (nothing launched)
+// for inputs it does not take.  The workspace holds 2 floats per query row
+// and, with grouped heads, the per-query-head dK/dV partials
+// (mi355x_attn_bwd_gen_workspace_bytes).
+int attn_bwd_grouped_mfma(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs, void* dv,
+                          const int64_t* dv_bhs, const void* dout, const int64_t* do_bhs, const void* q,
+                          const int64_t* q_bhs, const void* k, const int64_t* k_bhs, const void* v,
+                          const int64_t* v_bhs, const void* o, const int64_t* o_bhs, const float* lse,
+                          int64_t batch, int64_t heads, int64_t kv_heads, int64_t sq, int64_t skv, int64_t d,
+                          double scale, int causal, int64_t window, int dtype, void* workspace,
+                          hipStream_t stream) {
+  if ((dtype != MI355X_BF16 && dtype != MI355X_F16) || (d != 64 && d != 128 && d != 256)) return -1;
+  if (kv_heads < 1 || heads % kv_heads != 0 || heads / kv_heads > 65535 || batch >= 65536) return -1;
+  if (window > 0 && !causal) return -1;
+  if (!(strides_ok(q, q_bhs) && strides_ok(k, k_bhs) && strides_ok(v, v_bhs) && strides_ok(dout, do_bhs) &&
+        strides_ok(o, o_bhs)))
+    return -1;
+  for (const int64_t* st : {dq_bhs, dk_bhs, dv_bhs})
+    if (st[0] % 4 || st[1] % 4 || st[2] % 4) return -1;
+  if (((uintptr_t)dq | (uintptr_t)dk | (uintptr_t)dv) % 8) return -1;
+  AttnBwdArgs a;
+  a.f = AttnArgs{(void*)o, o_bhs[0], o_bhs[1], o_bhs[2], (float*)lse, q, q_bhs[0], q_bhs[1], q_bhs[2],
+                 k, k_bhs[0], k_bhs[1], k_bhs[2], v, v_bhs[0], v_bhs[1], v_bhs[2],
+                 batch, heads, sq, skv, (float)(scale * 1.4426950408889634), (float)scale, causal,
+                 heads / kv_heads, window};
+  a.dout = dout; a.do_b = do_bhs[0]; a.do_h = do_bhs[1]; a.do_s = do_bhs[2];
+  a.dq = dq; a.dq_b = dq_bhs[0]; a.dq_h = dq_bhs[1]; a.dq_s = dq_bhs[2];
+  a.dk = dk; a.dk_b = dk_bhs[0]; a.dk_h = dk_bhs[1]; a.dk_s = dk_bhs[2];
+  a.dv = dv; a.dv_b = dv_bhs[0]; a.dv_h = dv_bhs[1]; a.dv_s = dv_bhs[2];
+  a.ndelta = (float*)workspace;
+  a.nlse2 = a.ndelta + batch * heads * sq;
+  // partials after the row terms, 256-byte aligned (grouped heads only)
+  a.kv_part = heads > kv_heads
+                  ? (float*)(((uintptr_t)(a.nlse2 + batch * heads * sq) + 255) & ~(uintptr_t)255)
+                  : nullptr;
+  const bool bf = dtype == MI355X_BF16;
+  if (d == 64) return bf ? gqa_bwd_launch<bf16, 64>(a, stream) : gqa_bwd_launch<f16, 64>(a, stream);
+  if (d == 128) return bf ? gqa_bwd_launch<bf16, 128>(a, stream) : gqa_bwd_launch<f16, 128>(a, stream);
+  return bf ? gqa_bwd_launch<bf16, 256>(a, stream) : gqa_bwd_launch<f16, 256>(a, stream);
+}
+
 }  // namespace mi
 
 using namespace mi;
@@ -1527,6 +1921,7 @@ extern "C" int mi355x_attn_bwd(void* dq, const int64_t* dq_bhs, void* dk, const 
   a.dv = dv; a.dv_b = dv_bhs[0]; a.dv_h = dv_bhs[1]; a.dv_s = dv_bhs[2];
   a.ndelta = (float*)workspace;
   a.nlse2 = a.ndelta + batch * heads * sq;
+  a.kv_part = nullptr;
   MI_ATTN_DISPATCH(dtype, d, bwd_launch, a, (hipStream_t)stream);
 }
 

@@ -391,8 +391,26 @@ extern "C" int mi355x_attn_fwd_gen(void* o, const int64_t* o_bhs, float* lse, co
   MI_GEN_DISPATCH(dtype, d, gen_fwd_launch, a, (hipStream_t)stream);
 }
 
-extern "C" int64_t mi355x_attn_bwd_gen_workspace_bytes(int64_t batch, int64_t heads, int64_t sq) {
-  return batch * heads * sq * (int64_t)sizeof(float) + 256;
+namespace mi {
+// attention.hip: the MFMA backward for grouped/windowed bf16/f16 attention
+// (-1 when it does not take the inputs)
+int attn_bwd_grouped_mfma(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs, void* dv,
+                          const int64_t* dv_bhs, const void* dout, const int64_t* do_bhs, const void* q,
+                          const int64_t* q_bhs, const void* k, const int64_t* k_bhs, const void* v,
+                          const int64_t* v_bhs, const void* o, const int64_t* o_bhs, const float* lse,
+                          int64_t batch, int64_t heads, int64_t kv_heads, int64_t sq, int64_t skv, int64_t d,
+                          double scale, int causal, int64_t window, int dtype, void* workspace,
+                          hipStream_t stream);
+}  // namespace mi
+
+// Two floats per query row (the MFMA path keeps -D and -LSE log2(e), the f32
+// path D) and, with grouped heads, the MFMA path's per-query-head dK and dV
+// partials in f32.
+extern "C" int64_t mi355x_attn_bwd_gen_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t sq,
+                                                       int64_t skv, int64_t d) {
+  int64_t bytes = 2 * batch * heads * sq * (int64_t)sizeof(float) + 256;
+  if (kv_heads >= 1 && heads > kv_heads) bytes += 2 * batch * heads * skv * d * (int64_t)sizeof(float) + 256;
+  return bytes;
 }
 
 extern "C" int mi355x_attn_bwd_gen(void* dq, const int64_t* dq_bhs, void* dk, const int64_t* dk_bhs, void* dv,
@@ -405,10 +423,14 @@ extern "C" int mi355x_attn_bwd_gen(void* dq, const int64_t* dq_bhs, void* dk, co
   int rc = gen_check(batch, heads, kv_heads, sq, skv, d, dtype, causal, window, "mi355x_attn_bwd_gen");
   if (rc) return rc;
   MI_REQUIRE(dq && dk && dv && dout && q && k && v && o && lse, "mi355x_attn_bwd_gen: null pointer");
-  const int64_t need = mi355x_attn_bwd_gen_workspace_bytes(batch, heads, sq);
+  const int64_t need = mi355x_attn_bwd_gen_workspace_bytes(batch, heads, kv_heads, sq, skv, d);
   if (!workspace || ws_bytes < need)
     return fail(MI355X_EWORKSPACE, "mi355x_attn_bwd_gen: workspace %lld < %lld", (long long)ws_bytes,
                 (long long)need);
+  const int mrc = attn_bwd_grouped_mfma(dq, dq_bhs, dk, dk_bhs, dv, dv_bhs, dout, do_bhs, q, q_bhs, k, k_bhs, v,
+                                        v_bhs, o, o_bhs, lse, batch, heads, kv_heads, sq, skv, d, scale, causal,
+                                        window, dtype, workspace, (hipStream_t)stream);
+  if (mrc >= 0) return mrc;  // bf16/f16 at head_dim 64/128/256: MFMA kernels
   GenArgs a = gen_args(q, q_bhs, k, k_bhs, v, v_bhs, batch, heads, kv_heads, sq, skv, d, scale, causal, window);
   a.o = (void*)o; a.o_b = o_bhs[0]; a.o_h = o_bhs[1]; a.o_s = o_bhs[2];
   a.lse = (float*)lse;

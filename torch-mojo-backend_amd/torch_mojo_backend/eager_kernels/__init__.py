@@ -21,7 +21,7 @@ from pathlib import Path
 
 LIB_NAME = "libmi355x_kernels.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 c_int = ctypes.c_int
 c_i64 = ctypes.c_int64
@@ -208,7 +208,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_double, c_int, c_i64, c_int, c_vp,
         ],
     ),
-    "mi355x_attn_bwd_gen_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
+    "mi355x_attn_bwd_gen_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "mi355x_attn_bwd_gen": (
         c_int,
         [

@@ -2170,7 +2170,7 @@ def attention_backward(grad_out, q: MT, k: MT, v: MT, out: MT, lse: MT, causal, 
     else:
         q, k, v = _unit_head_stride(q), _unit_head_stride(k), _unit_head_stride(v)
         out, dout = _unit_head_stride(out), _unit_head_stride(grad_out)
-        ws = lib().mi355x_attn_bwd_gen_workspace_bytes(b, h, sq)
+        ws = lib().mi355x_attn_bwd_gen_workspace_bytes(b, h, hk, sq, skv, d)
         hold, wptr = _workspace(ws, q._device)
         check(
             "mi355x_attn_bwd_gen",
