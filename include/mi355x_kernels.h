@@ -254,6 +254,17 @@ int mi355x_embedding_bwd(void* grad_weight, const void* grad_out, int dtype,
 int mi355x_rms_norm_fwd(void* y, float* rstd, const void* x, const void* weight, int weight_dtype,
                         double weight_offset, int64_t rows, int64_t cols, double eps, int dtype,
                         mi355x_stream_t stream);
+/* RMSNorm backward (the gradient of mi355x_rms_norm_fwd, its rstd saved):
+ * with s = weight + weight_offset, dx = rstd * (dy s - x rstd^2 mean(dy s x))
+ * and dweight = sum over rows of dy x rstd (optional, summed in a fixed
+ * order through the mi355x_layer_norm_bwd_workspace_bytes workspace).
+ * weight is the input dtype; rows contiguous, cols a multiple of 4 up to
+ * 2048 (others return MI355X_EUNSUPPORTED).  No reference counterpart (see
+ * mi355x_rms_norm_fwd): it replaces the decomposition of the rms_norm
+ * backward into device elementwise and reduction ops. */
+int mi355x_rms_norm_bwd(void* dx, void* dweight, const void* dy, const void* x, const float* rstd,
+                        const void* weight, double weight_offset, int64_t rows, int64_t cols, int dtype,
+                        void* workspace, int64_t ws_bytes, mi355x_stream_t stream);
 /* Rotary position embedding, half-split ("rotate_half") form, over
  * [batch, heads, seq, d] views (unit d stride, *_bht = the batch/head/seq
  * element strides, multiples of 4): y[i] = x[i] cos[t][i] - x[i+d/2] sin[t][i],

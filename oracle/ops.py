@@ -244,6 +244,19 @@ def rms_norm(x, weight=None, eps=1e-6):
     return y, rstd[..., 0]
 
 
+def rms_norm_backward(dy, x, weight=None, eps=1e-6, weight_offset=0.0):
+    """(dx, dweight) of rms_norm with scale (weight + weight_offset): the
+    chain rule through y = x r s, r = (mean(x^2) + eps)^-1/2."""
+    dy, x = _f64(dy), _f64(x)
+    n = x.shape[-1]
+    r = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+    s = (_f64(weight) + weight_offset) if weight is not None else np.ones(n)
+    gs = dy * s
+    dx = r * gs - x * r**3 * (gs * x).sum(-1, keepdims=True) / n
+    dw = (dy * x * r).reshape(-1, n).sum(0) if weight is not None else None
+    return dx, dw
+
+
 # ---------------------------------------------------------------------------
 # GEMM — fast_aten_mm / addmm / bmm (aten_fast.py:8713-8935)
 # ---------------------------------------------------------------------------

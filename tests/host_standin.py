@@ -548,6 +548,20 @@ class HostStandIn:
             dense(_val(rstd), torch.float32, (rows,)).copy_(r.float())
         return 0
 
+    def mi355x_rms_norm_bwd(self, dx, dw, dy, x, rstd, w, woff, rows, cols, dt, ws, wsb, stream):
+        if cols % 4 or cols > 2048:
+            return 3
+        X = dense(_val(x), DT[dt], (rows, cols)).double()
+        G = dense(_val(dy), DT[dt], (rows, cols)).double()
+        r = dense(_val(rstd), torch.float32, (rows,)).double()[:, None]
+        s = (dense(_val(w), DT[dt], (cols,)).double() + woff) if w else torch.ones(cols, dtype=torch.float64)
+        gw = G * s
+        DX = r * gw - X * r ** 3 * (gw * X).mean(-1, keepdim=True)
+        dense(_val(dx), DT[dt], (rows, cols)).copy_(DX.to(DT[dt]))
+        if dw:
+            dense(_val(dw), DT[dt], (cols,)).copy_((G * X * r).sum(0).to(DT[dt]))
+        return 0
+
     def mi355x_rope(self, y, ybht, x, xbht, cos, sin, B, H, T, D, inverse, dt, stream):
         X = view(_val(x), DT[dt], (B, H, T, D), (xbht[0], xbht[1], xbht[2], 1)).float()
         C = dense(_val(cos), DT[dt], (T, D)).float()

@@ -559,6 +559,32 @@ def test_rms_norm_fwd_matches_oracle(kernels, cols, dtype, wdt):
     tol_close(np64(rstd), er, atol=1e-6, rtol=1e-5, what="rstd")
 
 
+@pytest.mark.parametrize("rows,cols", [(37, 1152), (37, 256), (37, 100), (4096, 1152)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rms_norm_bwd_matches_oracle(kernels, rows, cols, dtype):
+    """The fused rms_norm backward (Gemma's 1 + w scale) against the f64
+    oracle, from the forward's own rstd; (4096, 1152) is the Gemma-3-1B
+    residual norm of a 4096-token sequence."""
+    x = (randn(rows, cols) * 2.0).to(dtype)
+    w = (0.1 * randn(cols)).to(dtype)
+    dy = randn(rows, cols).to(dtype)
+    tx, tw, tdy = dev(x), dev(w), dev(dy)
+    y = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    rstd = torch.empty(rows, device="cuda")
+    call("mi355x_rms_norm_fwd", p(y), p(rstd), p(tx), p(tw), CODE[dtype], 1.0, rows, cols, 1e-6, CODE[dtype], None)
+    dx = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    dw = torch.empty(cols, dtype=dtype, device="cuda")
+    ws_n = lib().mi355x_layer_norm_bwd_workspace_bytes(rows, cols)
+    ws = workspace(ws_n)
+    call("mi355x_rms_norm_bwd", p(dx), p(dw), p(tdy), p(tx), p(rstd), p(tw), 1.0, rows, cols, CODE[dtype],
+         p(ws), ws_n, None)
+    edx, edw = O.rms_norm_backward(dy.double().numpy(), x.double().numpy(), w.double().numpy(), eps=1e-6,
+                                   weight_offset=1.0)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    tol_close(np64(dx), edx, atol=tol, rtol=tol, what="dx")
+    tol_close(np64(dw), edw, atol=tol * math.sqrt(rows), rtol=tol, what="dw")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_rope_forward_and_inverse(kernels, dtype):
     """Rotary embedding on a [B,H,T,D] view with BTHD storage: against the

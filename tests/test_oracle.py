@@ -247,6 +247,19 @@ def test_rms_norm_matches_torch_and_invariants():
     close(rstd, 1.0 / np.sqrt(ms + 1e-6), rtol=1e-14, atol=0)
 
 
+def test_rms_norm_backward_finite_differences_and_invariants():
+    """dx and dweight of rms_norm (scale weight + offset) against central
+    finite differences of the oracle forward; with eps = 0 the forward is
+    invariant to scaling x, so dx is orthogonal to x in every row."""
+    rng = np.random.default_rng(11)
+    x, w, dy = rng.normal(size=(4, 12)) * 2.0, rng.normal(size=12) * 0.3, rng.normal(size=(4, 12))
+    dx, dw = ops.rms_norm_backward(dy, x, w, eps=1e-6, weight_offset=1.0)
+    close(dx, fd_grad(lambda t: ops.rms_norm(t, w + 1.0, eps=1e-6)[0], x, dy), rtol=1e-6, atol=1e-8)
+    close(dw, fd_grad(lambda t: ops.rms_norm(x, t + 1.0, eps=1e-6)[0], w, dy), rtol=1e-6, atol=1e-8)
+    dx0, _ = ops.rms_norm_backward(dy, x, w, eps=0.0)
+    close((dx0 * x).sum(-1), np.zeros(4), rtol=0, atol=1e-12)
+
+
 def test_sdpa_backward_finite_differences():
     rng = np.random.default_rng(6)
     shp = (1, 1, 4, 3)

@@ -265,12 +265,15 @@ __device__ __forceinline__ void ln_load_row(const T* __restrict__ x, const T* __
   }
 }
 
-template <typename T, int NV, int W>
+// RMS: the rms_norm backward (no mean: mean may be null; the scale is
+// gamma + goff): dx = r (g w - x r m2), m2 = mean over the row of g w x r,
+// dw partials = sum of g x r over the block's rows.
+template <typename T, int NV, int W, bool RMS = false>
 __global__ void __launch_bounds__(64 * W)
     ln_bwd_wave(T* __restrict__ dx, float* __restrict__ part_g, float* __restrict__ part_b,
                 const T* __restrict__ dy, const T* __restrict__ x, const float* __restrict__ mean,
                 const float* __restrict__ rstd, const T* __restrict__ gamma, int64_t rows, int cols,
-                int64_t rows_per_block) {
+                int64_t rows_per_block, float goff = 0.f) {
   __shared__ float lds[2][W][NV * 256];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const bool want_params = part_g != nullptr;
@@ -287,7 +290,7 @@ __global__ void __launch_bounds__(64 * W)
     if (gamma) {
       Vec4<T>::load(gamma + coff[j], gm[j]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) gm[j][e] = cv[j] ? gm[j][e] : 0.f;
+      for (int e = 0; e < 4; ++e) gm[j][e] = cv[j] ? gm[j][e] + goff : 0.f;
     }
   }
   const float inv_n = 1.f / (float)cols;
@@ -303,14 +306,14 @@ __global__ void __launch_bounds__(64 * W)
   {
     const int64_t first = min(row, last);
     ln_load_row<T, NV>(x, dy, first * cols, coff, cv, xa, da);
-    mu = mean[first];
+    mu = RMS ? 0.f : mean[first];
     rs = rstd[first];
   }
   for (; row < r1; row += W) {
     const int64_t nxt = min(row + W, last);
     float xn[NV][4], dn[NV][4];
     ln_load_row<T, NV>(x, dy, nxt * cols, coff, cv, xn, dn);
-    const float mu_n = mean[nxt], rs_n = rstd[nxt];
+    const float mu_n = RMS ? 0.f : mean[nxt], rs_n = rstd[nxt];
     float xh[NV][4], gy[NV][4];
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
@@ -325,7 +328,7 @@ __global__ void __launch_bounds__(64 * W)
         pb[j][e] += da[j][e];
       }
     if (dx) {
-      const float m1 = wave_sum(s1) * inv_n;
+      const float m1 = RMS ? 0.f : wave_sum(s1) * inv_n;
       const float m2 = wave_sum(s2) * inv_n;
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
@@ -599,10 +602,73 @@ int bwd_impl(T* dx, T* dgamma, T* dbeta, const T* dy, const T* x, const float* m
   return check_launch("mi355x_layer_norm_bwd");
 }
 
+// rms_norm backward: the LayerNorm wave kernel without the mean terms, the
+// weight gradient summed from the same block partials.
+template <typename T>
+int rms_bwd_impl(T* dx, T* dw, const T* dy, const T* x, const float* rstd, const T* w, float w_off, int64_t rows,
+                 int64_t cols, float* ws, hipStream_t s) {
+  const size_t al = 4 * sizeof(T);
+  const int nv = (aligned(dx, al) && aligned(dy, al) && aligned(x, al) && aligned(w, al)) ? wave_nv(cols) : 0;
+  if (!nv)
+    return fail(MI355X_EUNSUPPORTED, "mi355x_rms_norm_bwd: needs 4-element aligned rows of at most 2048 (got %lld)",
+                (long long)cols);
+  const int nb = bwd_blocks(rows);
+  const int64_t rpb = bwd_rows_per_block(rows);
+  float* pg = dw ? ws : nullptr;
+  float* pb = dw ? ws + (int64_t)nb * cols : nullptr;
+  switch (nv) {
+#define RMS_BWD_CASE(V)                                                                                      \
+  case V:                                                                                                    \
+    ln_bwd_wave<T, V, 4, true><<<nb, 256, 0, s>>>(dx, pg, pb, dy, x, nullptr, rstd, w, rows, (int)cols, rpb,  \
+                                                  w_off);                                                    \
+    break;
+    RMS_BWD_CASE(1)
+    RMS_BWD_CASE(2)
+    RMS_BWD_CASE(3)
+    RMS_BWD_CASE(4)
+    RMS_BWD_CASE(8)
+#undef RMS_BWD_CASE
+  }
+  if (dw) ln_bwd_params_sum<T><<<ceil_div(cols, kSumCols), kSumCols * kSumGroups, 0, s>>>(dw, nullptr, pg, pb, nb, cols);
+  return check_launch("mi355x_rms_norm_bwd");
+}
+
 }  // namespace
 }  // namespace mi
 
 using namespace mi;
+
+extern "C" int mi355x_rms_norm_bwd(void* dx, void* dweight, const void* dy, const void* x, const float* rstd,
+                                   const void* weight, double weight_offset, int64_t rows, int64_t cols, int dtype,
+                                   void* workspace, int64_t ws_bytes, mi355x_stream_t stream) {
+  MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_rms_norm_bwd: bad shape [%lld, %lld]", (long long)rows, (long long)cols);
+  MI_REQUIRE(dx && dy && x && rstd, "mi355x_rms_norm_bwd: null pointer");
+  MI_REQUIRE(weight || !dweight, "mi355x_rms_norm_bwd: a weight gradient needs the weight");
+  hipStream_t s = (hipStream_t)stream;
+  if (rows == 0) {
+    if (!dweight) return MI355X_OK;
+    const int64_t shape[1] = {cols}, strides[1] = {1};
+    return mi355x_fill(dweight, dtype, strides, shape, 1, 0.0, stream);
+  }
+  if (dweight) {
+    const int64_t need = mi355x_layer_norm_bwd_workspace_bytes(rows, cols);
+    if (!workspace || ws_bytes < need)
+      return fail(MI355X_EWORKSPACE, "mi355x_rms_norm_bwd: workspace %lld < %lld bytes", (long long)ws_bytes,
+                  (long long)need);
+  }
+  switch (dtype) {
+    case MI355X_F32:
+      return rms_bwd_impl<float>((float*)dx, (float*)dweight, (const float*)dy, (const float*)x, rstd,
+                                 (const float*)weight, (float)weight_offset, rows, cols, (float*)workspace, s);
+    case MI355X_BF16:
+      return rms_bwd_impl<bf16>((bf16*)dx, (bf16*)dweight, (const bf16*)dy, (const bf16*)x, rstd,
+                                (const bf16*)weight, (float)weight_offset, rows, cols, (float*)workspace, s);
+    case MI355X_F16:
+      return rms_bwd_impl<f16>((f16*)dx, (f16*)dweight, (const f16*)dy, (const f16*)x, rstd, (const f16*)weight,
+                               (float)weight_offset, rows, cols, (float*)workspace, s);
+  }
+  return fail(MI355X_EUNSUPPORTED, "mi355x_rms_norm_bwd: unsupported dtype %d", dtype);
+}
 
 extern "C" int mi355x_layer_norm_fwd_ex(void* y, void* y_low, int low_dtype, float* mean, float* rstd,
                                         const void* x, const void* gamma, const void* beta, int64_t rows,

@@ -2346,6 +2346,38 @@ def rms_norm_forward(x: MT, normalized_shape, weight, eps, weight_offset=0.0):
     return y, rstd
 
 
+_EUNSUPPORTED = 3  # MI355X_EUNSUPPORTED
+
+
+def rms_norm_backward(grad, x, normalized_shape, weight, rstd, weight_offset, need_x, need_w):
+    """(dx, dweight) of rms_norm_forward in one kernel (mi355x_rms_norm_bwd),
+    or NOT_HANDLED for inputs it does not take (a weight of another dtype
+    than x, rows that are not 4-element multiples of at most 2048)."""
+    n = math.prod(normalized_shape) if normalized_shape else 1
+    g, xt = _require(grad), _require(x)
+    w = _require(weight) if weight is not None else None
+    if w is not None and w._dtype != xt._dtype:
+        return NOT_HANDLED
+    if n % 4 or n > 2048 or g._dtype != xt._dtype or tuple(g._shape) != tuple(xt._shape):
+        return NOT_HANDLED
+    gc, xc = _contig(g), _contig(xt)
+    wc = _contig(w) if w is not None else None
+    rows = xc._numel // n
+    dx = _alloc(xt._shape, xt._dtype, xt._device)
+    dw = _alloc(w._shape, w._dtype, w._device) if (w is not None and need_w) else None
+    hold, wptr, ws = None, None, 0
+    if dw is not None:
+        ws = lib().mi355x_layer_norm_bwd_workspace_bytes(rows, n)
+        hold, wptr = _workspace(ws, xt._device)
+    rc = lib().mi355x_rms_norm_bwd(dx._ptr, dw._ptr if dw is not None else None, gc._ptr, xc._ptr, _require(rstd)._ptr,
+                                   wc._ptr if wc is not None else None, float(weight_offset), rows, n,
+                                   _code(xt._dtype), wptr, ws, _STREAM)
+    if rc == _EUNSUPPORTED:
+        return NOT_HANDLED
+    check("mi355x_rms_norm_bwd", rc)
+    return (dx if need_x else None), dw
+
+
 def rope_forward(x: MT, cos: MT, sin: MT, inverse=False) -> MT:
     """Rotary embedding of x [B, H, T, D] with dense [T, D] tables; the output
     is allocated [B, T, H, D]-dense (as the attention kernels' inputs are) and

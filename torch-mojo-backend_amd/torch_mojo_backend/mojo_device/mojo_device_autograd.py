@@ -225,7 +225,8 @@ class _FusedRMSNorm(torch.autograd.Function):
     """rms_norm (the Gemma-3-shaped workload's norm) with scale w (+ an
     optional constant offset): the forward is one gfx950 kernel that also
     keeps the row rstd; the backward uses it, dx = r*(g*w) - x * r^3/n *
-    sum(g*w*x) and dw = sum_rows(g*x*r), from device ops in f32."""
+    sum(g*w*x) and dw = sum_rows(g*x*r), in one kernel (mi355x_rms_norm_bwd;
+    device ops in f32 for inputs it does not take)."""
 
     @staticmethod
     def forward(ctx, x, normalized_shape, weight, eps, weight_offset=0.0):
@@ -239,6 +240,13 @@ class _FusedRMSNorm(torch.autograd.Function):
     def backward(ctx, grad):
         x, weight, rstd = ctx.saved_tensors
         nd = ctx.n
+        need_w = weight is not None and ctx.needs_input_grad[2]
+        with torch._C._AutoDispatchBelowAutograd():
+            res = aten_fast.rms_norm_backward(grad, x, tuple(x.shape[x.dim() - nd:]), weight, rstd, ctx.offset,
+                                              ctx.needs_input_grad[0], need_w)
+        if res is not aten_fast.NOT_HANDLED:
+            return res[0], None, res[1], None, None
+        # other inputs: device elementwise and reduction ops
         dims = tuple(range(x.dim() - nd, x.dim()))
         n = 1
         for d in dims:
