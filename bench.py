@@ -24,6 +24,7 @@ after W warmup steps.  Alongside it:
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -331,6 +332,58 @@ def bench_gemma(iters):
     }
 
 
+def bench_gemma_attention(iters):
+    """Config 4's attention layers at their real shape (1 x 4096 tokens, 4
+    query heads on 1 K/V head, head_dim 256, bf16): the forward
+    (mi355x_attn_fwd_ex) and the grouped backward (mi355x_attn_bwd_gen) of a
+    local layer (sliding window 512) and of a global (causal) layer, through
+    the C ABI.  Algorithmic work: 4 * D flop per visible (query, key) pair
+    and head forward, 2.5x that backward."""
+    from torch_mojo_backend.eager_kernels import lib
+
+    B, H, HK, T, D = 1, 4, 1, 4096, 256
+    g = torch.Generator().manual_seed(4)
+    q, do = (torch.randn(B, T, H, D, generator=g).bfloat16().cuda().transpose(1, 2) for _ in range(2))
+    k, v = (torch.randn(B, T, HK, D, generator=g).bfloat16().cuda().transpose(1, 2) for _ in range(2))
+    o = torch.empty(B, T, H, D, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    dq = torch.empty_like(o)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    lse = torch.empty(B, H, T, device="cuda")
+    ws_n = lib().mi355x_attn_bwd_gen_workspace_bytes(B, H, HK, T, T, D)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda")
+    scale = 1.0 / math.sqrt(D)
+    L = lib()
+
+    def bhs(t):
+        return (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+
+    sb = {n: bhs(t) for n, t in (("q", q), ("k", k), ("v", v), ("o", o), ("do", do), ("dq", dq), ("dk", dk),
+                                 ("dv", dv))}
+    out = {}
+    for name, window in (("local_window512", 512), ("global_causal", 0)):
+        def fwd():
+            rc = L.mi355x_attn_fwd_ex(o.data_ptr(), sb["o"], lse.data_ptr(), q.data_ptr(), sb["q"], k.data_ptr(),
+                                      sb["k"], v.data_ptr(), sb["v"], B, H, HK, T, T, D, scale, 1, window, 1, None)
+            assert rc == 0
+
+        def bwd():
+            rc = L.mi355x_attn_bwd_gen(dq.data_ptr(), sb["dq"], dk.data_ptr(), sb["dk"], dv.data_ptr(), sb["dv"],
+                                       do.data_ptr(), sb["do"], q.data_ptr(), sb["q"], k.data_ptr(), sb["k"],
+                                       v.data_ptr(), sb["v"], o.data_ptr(), sb["o"], lse.data_ptr(), B, H, HK, T, T,
+                                       D, scale, 1, window, 1, ws.data_ptr(), ws_n, None)
+            assert rc == 0
+
+        fwd()
+        f_ms = time_gpu(fwd, iters)
+        b_ms = time_gpu(bwd, iters)
+        pairs = sum(min(i + 1, window) if window else i + 1 for i in range(T))
+        flop = 4.0 * B * H * D * pairs
+        out[name] = {"fwd_ms": f_ms, "bwd_ms": b_ms, "fwd_tflops": flop / (f_ms * 1e-3) / 1e12,
+                     "bwd_tflops": 2.5 * flop / (b_ms * 1e-3) / 1e12,
+                     "fwd_bwd_tflops": 3.5 * flop / ((f_ms + b_ms) * 1e-3) / 1e12}
+    return out
+
+
 def bench_copy(iters):
     """Calibration for HBM-counter reads: a plain 1 GiB device copy (1 GiB
     read + 1 GiB written per launch) through the library's copy kernel."""
@@ -421,6 +474,7 @@ def main():
         res["copy"] = bench_copy(args.iters)
     if args.only in ("all", "gemma"):
         res["cfg4_prefill"] = bench_gemma(args.iters)
+        res["cfg4_attention"] = bench_gemma_attention(args.iters)
     traffic = None
     tfile = ROOT / "profiles" / "attention_traffic.json"
     if tfile.exists():

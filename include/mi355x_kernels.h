@@ -283,6 +283,12 @@ int mi355x_rope(void* y, const int64_t* y_bht, const void* x, const int64_t* x_b
  * the elementwise mul). */
 int mi355x_geglu_fwd(void* y, const void* gate, const void* up, int64_t n, int approximate, int dtype,
                      mi355x_stream_t stream);
+/* GeGLU backward in one pass, bit-exact with the ATen chain it replaces:
+ * d_up = grad * round(gelu(gate)), d_gate = gelu_backward(round(grad * up),
+ * gate), every product rounded to dtype.  No reference counterpart (as
+ * mi355x_geglu_fwd). */
+int mi355x_geglu_bwd(void* dgate, void* dup, const void* grad, const void* gate, const void* up, int64_t n,
+                     int approximate, int dtype, mi355x_stream_t stream);
 /* y = (x - mean)*rstd*gamma + beta over rows of `cols` contiguous elements.
  * gamma/beta may be NULL.  mean/rstd: f32 [rows]. */
 int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,

@@ -582,6 +582,15 @@ class HostStandIn:
         dense(_val(y), DT[dt], (n,)).copy_((a.float() * u.float()).to(DT[dt]))
         return 0
 
+    def mi355x_geglu_bwd(self, dg, du, grad, gate, up, n, approximate, dt, stream):
+        mode = "tanh" if approximate else "none"
+        gr, g, u = (dense(_val(t), DT[dt], (n,)).float() for t in (grad, gate, up))
+        a = torch.nn.functional.gelu(g, approximate=mode).to(DT[dt]).float()
+        dense(_val(du), DT[dt], (n,)).copy_((gr * a).to(DT[dt]))
+        gu = (gr * u).to(DT[dt]).float()
+        dense(_val(dg), DT[dt], (n,)).copy_(torch.ops.aten.gelu_backward(gu, g, approximate=mode).to(DT[dt]))
+        return 0
+
     def mi355x_attn_fwd_ex(self, o, obhs, lse, q, qbhs, k, kbhs, v, vbhs, B, H, Hk, Sq, Skv, D, scale, causal,
                            window, dt, stream):
         def t(p, st, h, s):

@@ -622,6 +622,26 @@ def test_geglu_bit_exact_vs_gelu_then_mul(kernels, approximate):
     assert torch.equal(host(y), want)
 
 
+@pytest.mark.parametrize("approximate", [0, 1])
+@pytest.mark.parametrize("n", [4096 + 5, 4096 * 6912])
+def test_geglu_bwd_bit_exact_vs_its_aten_chain(kernels, approximate, n):
+    """The fused GeGLU backward against the kernels of the chain it replaces
+    (d_up = grad * gelu(gate), d_gate = gelu_backward(grad * up, gate), each
+    product rounded to bf16): bit-exact; n = 4096 x 6912 is a Gemma-3-1B MLP
+    activation of a 4096-token sequence."""
+    grad, gate, up = (dev((randn(n) * 2).bfloat16()) for _ in range(3))
+    dg, du = torch.empty_like(gate), torch.empty_like(gate)
+    call("mi355x_geglu_bwd", p(dg), p(du), p(grad), p(gate), p(up), n, approximate, CODE[torch.bfloat16], None)
+    a = torch.empty_like(gate)
+    call("mi355x_gelu_fwd", p(a), p(gate), n, approximate, CODE[torch.bfloat16], None)
+    want_du = (host(a).float() * host(grad).float()).bfloat16()
+    gu = dev((host(grad).float() * host(up).float()).bfloat16())
+    want_dg = torch.empty_like(gate)
+    call("mi355x_gelu_bwd", p(want_dg), p(gu), p(gate), n, approximate, CODE[torch.bfloat16], None)
+    assert torch.equal(host(du), want_du)
+    assert torch.equal(host(dg), host(want_dg))
+
+
 def test_multi_tensor_kernels_across_batches_with_empty_tensors(kernels):
     """Lists longer than one launch's 160 tensors, with empty tensors among
     them (first, inside a batch and at a batch boundary): foreach norm,

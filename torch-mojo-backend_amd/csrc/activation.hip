@@ -122,6 +122,42 @@ __global__ void __launch_bounds__(kThreads) geglu_fwd_kernel(T* __restrict__ y, 
     y[i] = from_f32<T>(to_f32(from_f32<T>(gelu_f(to_f32(gate[i]), approx))) * to_f32(up[i]));
 }
 
+// GeGLU backward, bit-exact with its ATen chain: d_up = grad * a with
+// a = gelu(gate) rounded to T, d_gate = gelu_backward(grad * up rounded to
+// T, gate); one pass reads grad, gate and up and writes both gradients.
+template <typename T>
+__global__ void __launch_bounds__(kThreads) geglu_bwd_kernel(T* __restrict__ dgate, T* __restrict__ dup,
+                                                             const T* __restrict__ grad, const T* __restrict__ gate,
+                                                             const T* __restrict__ up, int64_t n, int approx) {
+  auto one = [approx](float gr, float g, float u, float& dg, float& du) {
+    const float a = to_f32(from_f32<T>(gelu_f(g, approx)));
+    du = gr * a;
+    dg = gelu_grad_f(to_f32(from_f32<T>(gr * u)), g, approx);
+  };
+  const int64_t n8 = (aligned16(dgate) && aligned16(dup) && aligned16(grad) && aligned16(gate) && aligned16(up))
+                         ? n / 8 : 0;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n8; i += stride) {
+    const Pack8<T> gr = ((const Pack8<T>*)grad)[i], g = ((const Pack8<T>*)gate)[i], u = ((const Pack8<T>*)up)[i];
+    Pack8<T> rg, ru;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float dg, du;
+      one(to_f32(gr.v[e]), to_f32(g.v[e]), to_f32(u.v[e]), dg, du);
+      rg.v[e] = from_f32<T>(dg);
+      ru.v[e] = from_f32<T>(du);
+    }
+    ((Pack8<T>*)dgate)[i] = rg;
+    ((Pack8<T>*)dup)[i] = ru;
+  }
+  for (int64_t i = n8 * 8 + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    float dg, du;
+    one(to_f32(grad[i]), to_f32(gate[i]), to_f32(up[i]), dg, du);
+    dgate[i] = from_f32<T>(dg);
+    dup[i] = from_f32<T>(du);
+  }
+}
+
 unsigned grid_for(int64_t n) {
   int64_t b = (n / 8 + kThreads - 1) / kThreads;
   if (b < 1) b = 1;
@@ -176,4 +212,28 @@ extern "C" int mi355x_geglu_fwd(void* y, const void* gate, const void* up, int64
     default: return fail(MI355X_EUNSUPPORTED, "mi355x_geglu_fwd: unsupported dtype %d", dtype);
   }
   return check_launch("mi355x_geglu_fwd");
+}
+
+extern "C" int mi355x_geglu_bwd(void* dgate, void* dup, const void* grad, const void* gate, const void* up, int64_t n,
+                                int approximate, int dtype, mi355x_stream_t stream) {
+  MI_REQUIRE(n >= 0, "mi355x_geglu_bwd: bad size");
+  if (n == 0) return MI355X_OK;
+  MI_REQUIRE(dgate && dup && grad && gate && up, "mi355x_geglu_bwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MI355X_F32:
+      geglu_bwd_kernel<float><<<grid_for(n), kThreads, 0, s>>>((float*)dgate, (float*)dup, (const float*)grad,
+                                                               (const float*)gate, (const float*)up, n, approximate);
+      break;
+    case MI355X_BF16:
+      geglu_bwd_kernel<bf16><<<grid_for(n), kThreads, 0, s>>>((bf16*)dgate, (bf16*)dup, (const bf16*)grad,
+                                                              (const bf16*)gate, (const bf16*)up, n, approximate);
+      break;
+    case MI355X_F16:
+      geglu_bwd_kernel<f16><<<grid_for(n), kThreads, 0, s>>>((f16*)dgate, (f16*)dup, (const f16*)grad,
+                                                             (const f16*)gate, (const f16*)up, n, approximate);
+      break;
+    default: return fail(MI355X_EUNSUPPORTED, "mi355x_geglu_bwd: unsupported dtype %d", dtype);
+  }
+  return check_launch("mi355x_geglu_bwd");
 }

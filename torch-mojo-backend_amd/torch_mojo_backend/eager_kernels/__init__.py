@@ -188,6 +188,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "mi355x_rope": (c_int, [c_vp, P_i64, c_vp, P_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_vp]),
     "mi355x_geglu_fwd": (c_int, [c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_vp]),
+    "mi355x_geglu_bwd": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_int, c_int, c_vp]),
     "mi355x_attn_fwd_ex": (
         c_int,
         [

@@ -2408,6 +2408,19 @@ def geglu_forward(gate: MT, up: MT, approximate: str) -> MT:
     return out
 
 
+def geglu_backward(grad: MT, gate: MT, up: MT, approximate: str):
+    """(d_gate, d_up) of geglu_forward in one pass (mi355x_geglu_bwd)."""
+    gr, g, u = _contig(_require(grad)), _contig(gate), _contig(up)
+    dg = _alloc(g._shape, g._dtype, g._device)
+    du = _alloc(g._shape, g._dtype, g._device)
+    check(
+        "mi355x_geglu_bwd",
+        lib().mi355x_geglu_bwd(dg._ptr, du._ptr, gr._ptr, g._ptr, u._ptr, g._numel, 1 if approximate == "tanh" else 0,
+                               _code(g._dtype), _STREAM),
+    )
+    return dg, du
+
+
 # ---------------------------------------------------------------------------
 # optimizer: fused AdamW and foreach (aten_fast.py:515-1162)
 # ---------------------------------------------------------------------------

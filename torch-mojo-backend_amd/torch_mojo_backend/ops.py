@@ -63,6 +63,10 @@ class _GeGLU(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad):
         gate, up = ctx.saved_tensors
+        if _on_mojo(grad) and grad.shape == gate.shape and grad.dtype == gate.dtype:
+            with torch._C._AutoDispatchBelowAutograd():
+                d_gate, d_up = aten_fast.geglu_backward(grad, gate, up, ctx.approximate)
+            return d_gate, d_up, None
         act = F.gelu(gate, approximate=ctx.approximate)
         d_up = grad * act
         d_gate = torch.ops.aten.gelu_backward(grad * up, gate, approximate=ctx.approximate)
