@@ -413,7 +413,7 @@ __global__ void __launch_bounds__(kThreads)
 
 // dgamma/dbeta = sum of the block partials [nparts, cols] in a fixed order,
 // so the result is deterministic.  A block owns 16 columns; its 16 row groups
-// (ty) each sum partials ty, ty+16, ... with every load issued before the
+// (ty) each sum partials ty, ty+16, ... with 16 loads issued before their
 // adds, then group sums are combined in LDS in group order.  With at most a
 // few hundred partials this is one latency-bound pass over an L2-resident
 // workspace.
@@ -428,16 +428,19 @@ __global__ void __launch_bounds__(kSumCols * kSumGroups)
   const int64_t c = (int64_t)blockIdx.x * kSumCols + tx;
   float g = 0.f, b = 0.f;
   if (c < cols) {
+    // 16 partials of each kind in flight per thread (one round trip for the
+    // usual 256 partials), added in partial order
+    constexpr int U = 16;
     int q = ty;
-    for (; q + 3 * kSumGroups < nparts; q += 4 * kSumGroups) {
-      float vg[4], vb[4];
+    for (; q + (U - 1) * kSumGroups < nparts; q += U * kSumGroups) {
+      float vg[U], vb[U];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < U; ++u) {
         vg[u] = part_g[(int64_t)(q + u * kSumGroups) * cols + c];
         vb[u] = part_b[(int64_t)(q + u * kSumGroups) * cols + c];
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) g += vg[u], b += vb[u];
+      for (int u = 0; u < U; ++u) g += vg[u], b += vb[u];
     }
     for (; q < nparts; q += kSumGroups) g += part_g[(int64_t)q * cols + c], b += part_b[(int64_t)q * cols + c];
   }
