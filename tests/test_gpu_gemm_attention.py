@@ -374,10 +374,11 @@ def _attn_gen(q, k, v, do, causal, window, scale=None):
                                    (1, 4, 1, 64, 64, 200), (2, 2, 2, 50, 50, 256), (1, 1, 1, 1, 1, 8)])
 @pytest.mark.parametrize("mode", ["full", "causal", "window"])
 def test_attention_f32_kernels_match_oracle(kernels, dtype, shape, mode):
-    """mi355x_attn_fwd_gen / mi355x_attn_bwd_gen (f32 math) against the f64
-    oracle: f32 and bf16 inputs, head_dims the MFMA path does not take
-    (40, 96, 200, 256), Sq != Skv, grouped K/V heads (dK/dV summed over each
-    group) and a causal sliding window."""
+    """mi355x_attn_fwd_gen / mi355x_attn_bwd_gen against the f64 oracle: f32
+    and bf16 inputs, head_dims the tuned MFMA kernels do not take (40, 96,
+    200, 256), Sq != Skv, grouped K/V heads (dK/dV summed over each group)
+    and a causal sliding window.  The bf16 backward at head_dim 64 and 256
+    runs the grouped MFMA kernels, the rest the f32 kernels."""
     B, H, Hk, Sq, Skv, D = shape
     causal = mode != "full"
     window = 17 if mode == "window" else 0
@@ -397,3 +398,29 @@ def test_attention_f32_kernels_match_oracle(kernels, dtype, shape, mode):
     tol_close(np64(dv), edv, what="dV", **gtol)
     tol_close(np64(dk), edk, what="dK", **gtol)
     tol_close(np64(dq), edq, what="dQ", **gtol)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2, 4, 2, 130, 130, 64), (1, 6, 2, 200, 200, 128), (1, 4, 1, 96, 160, 256),
+                                   (1, 8, 1, 300, 300, 64)])
+@pytest.mark.parametrize("mode", ["full", "causal", "window"])
+def test_grouped_mfma_backward_matches_oracle(kernels, dtype, shape, mode):
+    """The grouped/windowed MFMA backward (attn_bwd_gqa_*: per-query-head
+    dK/dV partials summed in head order, dQ per query head) at head_dim 64,
+    128 and 256 with ragged 64-row tiles, Sq != Skv (top-left causal) and
+    windows that end inside a tile, against the f64 oracle at atol = rtol =
+    2e-2."""
+    B, H, Hk, Sq, Skv, D = shape
+    causal = mode != "full"
+    window = 37 if mode == "window" else 0
+    if window and Sq != Skv:
+        pytest.skip("windows are defined for Sq == Skv")
+    g = torch.Generator().manual_seed(sum(shape) + len(mode))
+    q, do = (torch.randn(B, H, Sq, D, generator=g).to(dtype) for _ in range(2))
+    k, v = (torch.randn(B, Hk, Skv, D, generator=g).to(dtype) for _ in range(2))
+    o, lse, dq, dk, dv = _attn_gen(dev(q), dev(k), dev(v), dev(do), causal, window)
+    n = lambda t: t.double().numpy()  # noqa: E731
+    edq, edk, edv = O.sdpa_backward(n(do), n(q), n(k), n(v), np64(o), np64(lse), causal=causal, window=window)
+    tol_close(np64(dv), edv, atol=2e-2, rtol=2e-2, what="dV")
+    tol_close(np64(dk), edk, atol=2e-2, rtol=2e-2, what="dK")
+    tol_close(np64(dq), edq, atol=2e-2, rtol=2e-2, what="dQ")
