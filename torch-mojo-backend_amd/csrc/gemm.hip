@@ -242,6 +242,14 @@ struct TileLoad {
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) dma_b128(src[it] + koff, lds0 + it * WAVES * 1024);
   }
+  template <bool KT>
+  __device__ __forceinline__ void issue_range(int64_t k0_bytes, char* dst, int64_t kend_bytes, int lo, int hi) const {
+    const int64_t koff = (KT && k0_bytes + chunk * 16 >= kend_bytes) ? k0_bytes - chunk * 16 : k0_bytes;
+    const unsigned lds0 = lds_base_of(dst) + wave_id() * 1024;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it)
+      if (it >= lo && it < hi) dma_b128(src[it] + koff, lds0 + it * WAVES * 1024);
+  }
 };
 
 // m/n-contiguous operand tile: BK k-rows of ROWS elements, 16-byte chunks
@@ -290,6 +298,17 @@ struct TileLoadT {
       dma_b128(base + k * ld + col_off[it], lds0 + it * WAVES * 1024);
     }
   }
+  template <bool KT>
+  __device__ __forceinline__ void issue_range(int64_t k0, char* dst, int64_t kend, int lo, int hi) const {
+    const unsigned lds0 = lds_base_of(dst) + wave_id() * 1024;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      if (it < lo || it >= hi) continue;
+      int64_t k = k0 + kr[it];
+      if (KT && k >= kend) k = kend - 1;
+      dma_b128(base + k * ld + col_off[it], lds0 + it * WAVES * 1024);
+    }
+  }
 };
 
 template <int ROWS, int NT, bool K_CONTIG, int BK>
@@ -302,6 +321,11 @@ struct OperandLoad<ROWS, NT, true, BK> {
   __device__ __forceinline__ void issue(int64_t k0, char* dst, int64_t kend) const {
     t.template issue<KT>(k0 * 2, dst, kend * 2);
   }
+  template <bool KT>
+  __device__ __forceinline__ void issue_range(int64_t k0, char* dst, int64_t kend, int lo, int hi) const {
+    t.template issue_range<KT>(k0 * 2, dst, kend * 2, lo, hi);
+  }
+  static constexpr int ITERS = TileLoad<ROWS, NT, BK>::ITERS;
 };
 template <int ROWS, int NT, int BK>
 struct OperandLoad<ROWS, NT, false, BK> {
@@ -311,6 +335,11 @@ struct OperandLoad<ROWS, NT, false, BK> {
   __device__ __forceinline__ void issue(int64_t k0, char* dst, int64_t kend) const {
     t.template issue<KT>(k0, dst, kend);
   }
+  template <bool KT>
+  __device__ __forceinline__ void issue_range(int64_t k0, char* dst, int64_t kend, int lo, int hi) const {
+    t.template issue_range<KT>(k0, dst, kend, lo, hi);
+  }
+  static constexpr int ITERS = TileLoadT<ROWS, NT, BK>::ITERS;
 };
 
 
@@ -580,7 +609,13 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
     // is past it); its loads are issued after this step's first B fragment
     // reads, so the first MFMAs do not wait behind the load issue (training
     // step 22.22 -> 22.03 ms, three runs each on one box; issuing them after
-    // the reads only for k-contiguous A gave nothing)
+    // the reads only for k-contiguous A gave nothing).  The 256x256 tiles
+    // (eight MFMA rows per wave) spread the load instructions over the MFMA
+    // rows of the first 32-k substep instead, so the load issue no longer
+    // stalls the wave in one burst: the forward fc and lm_head launches run
+    // 3.4-5.8% faster in the training step (kernel trace, two boxes); the
+    // same spread lost 2-6% on the 128x128 and 128x192 tiles and the 32-k
+    // 256x256 weight-gradient tiles, which keep the single burst.
     const bool more = k0 + (S - 1) * BK < kend;
     char* const nxt = lds + (cur == 0 ? S - 1 : cur - 1) * STAGE;
     const char* at = lds + cur * STAGE;
@@ -600,12 +635,19 @@ __global__ void __launch_bounds__(64 * TileCfg<CFG>::WGM * TileCfg<CFG>::WGN, Ti
         if constexpr (B_K) bfr[j] = *(const frag*)(bt + (wn * WN + j * 16 + lr) * ROWB + coff);
         if (tail) mask_k(bfr[j], kfrag, kend);
       }
-      if (ks == 0 && more) {
+      if (CFG != 1 && ks == 0 && more) {
         la.template issue<KT>(k0 + (S - 1) * BK, nxt, kend);
         lb.template issue<KT>(k0 + (S - 1) * BK, nxt + A_BYTES, kend);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
+        if (CFG == 1 && ks == 0 && more) {
+          // load instructions q in [lo, hi) of this stage's list (A's, then B's)
+          constexpr int NA = decltype(la)::ITERS, NQ = NA + decltype(lb)::ITERS;
+          const int lo = i * NQ / TM, hi = (i + 1) * NQ / TM;
+          la.template issue_range<KT>(k0 + (S - 1) * BK, nxt, kend, lo, hi);
+          lb.template issue_range<KT>(k0 + (S - 1) * BK, nxt + A_BYTES, kend, lo - NA, hi - NA);
+        }
         frag af;
         if constexpr (A_K) af = *(const frag*)(at + (wm * WM + i * 16 + lr) * ROWB + coff);
         else af = afr[i];
