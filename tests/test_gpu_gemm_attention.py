@@ -95,6 +95,23 @@ def test_gemm_k_tail_on_padded_rows_in_place(kernels, layout):
     tol_close(np64(c), exp, atol=2e-2 * math.sqrt(k / 64), rtol=1e-2, what=f"tail {layout}")
 
 
+@pytest.mark.parametrize("layout", ["NT", "NN", "TN", "TT"])
+def test_gemm_256_tiles_with_k_tail(kernels, layout):
+    """M = N = 4096 fill 256 of the 256x256 tiles, so the planner takes them
+    (their next-stage loads are spread over the MFMA rows); K = 200 ends
+    inside a 64-k stage.  bf16 out, f64 oracle on sampled rows."""
+    m, n, k = 4096, 4096, 200
+    A = randn(m, k).bfloat16()
+    B = (randn(k, n) * 0.1).bfloat16()
+    ta, a_rs, a_cs = (dev(A), k, 1) if layout[0] == "N" else (dev(A.t().contiguous()), 1, m)
+    tb, b_rs, b_cs = (dev(B), n, 1) if layout[1] == "N" else (dev(B.t().contiguous()), 1, k)
+    c = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    _gemm(c, ta, tb, m, n, k, a_rs, a_cs, b_rs, b_cs, torch.bfloat16)
+    rows = sorted(set(list(range(0, m, 97)) + [255, 256, 511, m - 1]))
+    exp = A[rows].double().numpy() @ B.double().numpy()
+    tol_close(np64(c)[rows], exp, atol=2e-2, rtol=2e-2, what=f"256 tiles {layout}")
+
+
 def test_gemm_accumulate_and_batched(kernels):
     bsz, m, n, k = 3, 100, 72, 96
     A = randn(bsz, m, k).bfloat16()

@@ -87,6 +87,17 @@ __device__ __forceinline__ float wave_max(float v) {
 // max that propagates NaN (torch.max / torch.maximum semantics; fmaxf
 // returns the other operand when one is NaN)
 __device__ __forceinline__ float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
+// Maximum of V values, NaN if any is NaN: pairs of NaN-propagating maxima,
+// which gfx950 issues as one three-input v_maximum3_f32 per two values.
+template <int V>
+__device__ __forceinline__ float max_nan(const float (&v)[V]) {
+  float m = v[0];
+  int e = 1;
+#pragma unroll
+  for (; e + 1 < V; e += 2) m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, v[e]), v[e + 1]);
+  if (e < V) m = __builtin_elementwise_maximum(m, v[e]);
+  return m;
+}
 __device__ __forceinline__ float wave_max_nan(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = nan_max(v, __shfl_xor(v, off, 64));

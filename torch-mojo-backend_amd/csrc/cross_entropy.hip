@@ -103,11 +103,11 @@ __global__ void __launch_bounds__(kRowThreads)
 #pragma unroll
         for (int e = 0; e < V; ++e) v[e] = (k0 + e >= 0 && k0 + e < ci) ? ch[u].get(e) : -INFINITY;
       }
-      float cm = v[0];
-#pragma unroll
-      for (int e = 0; e < V; ++e) {
-        nan |= v[e] != v[e];
-        cm = fmaxf(cm, v[e]);
+      // one NaN test per chunk: the chunk maximum propagates NaN
+      const float cm = max_nan(v);
+      if (cm != cm) {
+        nan = true;
+        continue;
       }
       if (cm == -INFINITY) continue;
       if (cm > m) {

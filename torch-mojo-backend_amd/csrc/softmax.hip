@@ -248,19 +248,22 @@ __global__ void __launch_bounds__(THREADS)
     const bool interior = k0 >= 0 && k0 + V <= cols;
 #pragma unroll
     for (int e = 0; e < V; ++e) v[e] = (interior || (k0 + e >= 0 && k0 + e < cols)) ? c[i].get(e) : -INFINITY;
-    float cm = v[0];
-#pragma unroll
-    for (int e = 0; e < V; ++e) {
-      nan |= v[e] != v[e];
-      cm = fmaxf(cm, v[e]);
+    // one NaN test per chunk: the chunk maximum propagates NaN
+    const float cm = max_nan(v);
+    if (cm != cm) {
+      nan = true;
+      continue;
     }
     if (cm == -INFINITY) continue;
     if (cm > m) {
       s = (m == -INFINITY) ? 0.f : s * exp2f((m - cm) * kL2e);
       m = cm;
     }
+    // terms of the sum (>= 1, from the maximum) need no subnormal results;
+    // v - m, not an FMA against m log2(e), whose rounding (relative to m)
+    // would cost f32 rows about 1e-6 of accuracy
 #pragma unroll
-    for (int e = 0; e < V; ++e) s += exp2f((v[e] - m) * kL2e);
+    for (int e = 0; e < V; ++e) s += __builtin_amdgcn_exp2f((v[e] - m) * kL2e);
   }
   block_ms<THREADS>(m, s, nan, rm, rs, rn);
   if (nan) m = NAN;
@@ -353,6 +356,8 @@ int fwd(void* y, const void* x, int64_t rows, int64_t cols, int log, hipStream_t
   if constexpr (std::is_same<TI, TO>::value) {
     const RowShape rs = cols > 1024 && aligned16(x) && aligned16(y) ? row_shape<TI>(cols) : RowShape{0, 0};
     if (rs.threads) {
+      // 512 x 16 chunks per row at 50257 bf16 columns: 1024 x 8 ran at 47%
+      // of HBM bandwidth, 256 x 32 at 53%, 512 x 16 at 66%
       auto k = rs.threads == 1024 ? softmax_fwd_rowreg<TI, 16, 1024>
                                   : (rs.nch == 8 ? softmax_fwd_rowreg<TI, 8, 512> : softmax_fwd_rowreg<TI, 16, 512>);
       k<<<(unsigned)rows, rs.threads, 0, s>>>((TO*)y, (const TI*)x, cols, log);
