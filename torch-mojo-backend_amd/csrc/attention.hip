@@ -721,13 +721,15 @@ template <typename T, int D>
 __global__ void __launch_bounds__(kThreads) attn_bwd_delta(AttnBwdArgs p) {
   constexpr int CPR = D / 8;              // lanes per row
   constexpr int RPB = kThreads / CPR;     // rows per block
-  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / CPR;  // over B*H*Sq
+  // rows over B*H*Sq, fewer than 2^31 (checked at launch): 32-bit index
+  // arithmetic (64-bit division is a long instruction sequence)
+  const uint32_t row = blockIdx.x * (uint32_t)RPB + threadIdx.x / CPR;
   const int ch = threadIdx.x % CPR;
-  const int64_t total = p.f.B * p.f.H * p.f.Sq;
+  const uint32_t total = (uint32_t)(p.f.B * p.f.H * p.f.Sq), sq = (uint32_t)p.f.Sq, nh = (uint32_t)p.f.H;
   float acc = 0.f;
   if (row < total) {
-    const int64_t i = row % p.f.Sq, bh = row / p.f.Sq;
-    const int64_t h = bh % p.f.H, b = bh / p.f.H;
+    const uint32_t bh = row / sq, i = row - bh * sq;
+    const uint32_t b = bh / nh, h = bh - b * nh;
     const V8<T> o = *(const V8<T>*)((const T*)p.f.o + b * p.f.o_b + h * p.f.o_h + i * p.f.o_s + ch * 8);
     const V8<T> d = *(const V8<T>*)((const T*)p.dout + b * p.do_b + h * p.do_h + i * p.do_s + ch * 8);
 #pragma unroll
@@ -1702,6 +1704,7 @@ int fwd_launch(const AttnArgs& a, hipStream_t s) {
 template <typename T, int D>
 int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
   const int64_t rows = a.f.B * a.f.H * a.f.Sq;
+  MI_REQUIRE(rows < (1ll << 31), "mi355x_attn_bwd: batch x heads x query rows must be below 2^31");
   attn_bwd_delta<T, D><<<ceil_div(rows, kThreads / (D / 8)), kThreads, 0, s>>>(a);
   if constexpr (D == 64 || D == 128) {
     const uint32_t nkx = (uint32_t)ceil_div(a.f.Skv, 128), nqx = (uint32_t)ceil_div(a.f.Sq, 128);
@@ -1745,6 +1748,7 @@ int bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
 template <typename T, int D>
 int gqa_bwd_launch(const AttnBwdArgs& a, hipStream_t s) {
   const int64_t rows = a.f.B * a.f.H * a.f.Sq;
+  MI_REQUIRE(rows < (1ll << 31), "mi355x_attn_bwd: batch x heads x query rows must be below 2^31");
   attn_bwd_delta<T, D><<<ceil_div(rows, kThreads / (D / 8)), kThreads, 0, s>>>(a);
   auto kkv = attn_bwd_gqa_dkv<T, D>;
   auto kq = attn_bwd_gqa_dq<T, D>;
