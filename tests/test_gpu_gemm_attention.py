@@ -214,10 +214,14 @@ def _attn_bwd(do, q, k, v, o, lse, causal, scale=None):
 
 
 # (2, 4, 256, 256, 64), (1, 8, 300, 300, 64) and (4, 2, 130, 130, 128) have B*H*ceil(S/128) % 8 == 0,
-# which runs dK/dV and dQ as one launch; the others run them as two.
+# which runs dK/dV and dQ as one launch; the others run them as two.  With
+# B*H*ceil(S/128) % 32 == 0 ((1, 8, 512, 512, 64), (2, 4, 512, 512, 128))
+# the one launch deals the two block kinds in groups of four slots per XCD
+# (alternating per shader engine) instead of alternating slot by slot.
 @pytest.mark.parametrize("shape", [(2, 3, 128, 128, 64), (1, 2, 100, 160, 64), (2, 2, 160, 100, 64),
                                    (1, 2, 192, 192, 32), (1, 2, 130, 130, 128), (1, 1, 1, 1, 64),
-                                   (2, 4, 256, 256, 64), (1, 8, 300, 300, 64), (4, 2, 130, 130, 128)])
+                                   (2, 4, 256, 256, 64), (1, 8, 300, 300, 64), (4, 2, 130, 130, 128),
+                                   (1, 8, 512, 512, 64), (2, 4, 512, 512, 128)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_attention_fwd_bwd_matches_oracle(kernels, shape, causal):
     B, H, Sq, Skv, D = shape
