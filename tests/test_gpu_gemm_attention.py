@@ -112,6 +112,23 @@ def test_gemm_256_tiles_with_k_tail(kernels, layout):
     tol_close(np64(c)[rows], exp, atol=2e-2, rtol=2e-2, what=f"256 tiles {layout}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_weight_gradient_tiles_split_k(kernels, dtype):
+    """An m-contiguous A (a weight gradient dY^T X) with 256 or more 256x256
+    tiles and a long K takes the 32-k 256x256 tiles in two K splits summed
+    by a second kernel (the embedding-gradient launch): f32 out, f64 oracle
+    on sampled rows."""
+    m, n, k = 4096, 4352, 8192  # 16 x 17 = 272 tiles, 2.1 rounds of 256 CUs
+    A = (randn(k, m) * 0.5).to(dtype)  # stored [k][m]: m-contiguous
+    B = (randn(k, n) * 0.5).to(dtype)  # stored [k][n]: n-contiguous
+    ta, tb = dev(A), dev(B)
+    c = torch.empty(m, n, dtype=torch.float32, device="cuda")
+    _gemm(c, ta, tb, m, n, k, 1, m, n, 1, dtype)
+    rows = sorted(set(list(range(0, m, 211)) + [255, 256, m - 1]))
+    exp = A[:, rows].double().numpy().T @ B.double().numpy()
+    tol_close(np64(c)[rows], exp, atol=2e-2 * math.sqrt(k / 64), rtol=2e-2, what=f"dW split {dtype}")
+
+
 def test_gemm_accumulate_and_batched(kernels):
     bsz, m, n, k = 3, 100, 72, 96
     A = randn(bsz, m, k).bfloat16()
