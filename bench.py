@@ -452,7 +452,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}): this build has no "
-              "multi-GPU path; the data-parallel design is described in DESIGN.md", file=sys.stderr)
+              "multi-GPU path (one process per GPU with data-parallel gradient all-reduce is the "
+              "intended design; it is not built)", file=sys.stderr)
         sys.exit(2)
 
     from torch_mojo_backend import register_mojo_devices
