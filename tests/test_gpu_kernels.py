@@ -283,6 +283,11 @@ def test_softmax_fwd_bwd(kernels, rows, cols, dtype, log):
     x[2, 0] = float("-inf")
     if rows > 3:
         x[3, cols // 2] = float("nan")  # a NaN poisons its row only
+    if rows > 4 and cols > 16:
+        # a NaN whose 16-byte chunk is otherwise -inf (the chunk maximum is
+        # the only NaN test) still poisons the row
+        x[4, :16] = float("-inf")
+        x[4, 5] = float("nan")
     xq = x.to(dtype)
     tx = dev(xq)
     y = torch.empty(rows, cols, dtype=dtype, device="cuda")
@@ -370,11 +375,13 @@ def test_fused_cross_entropy_matches_log_softmax_nll_chain(kernels, reduction, d
 def test_fused_cross_entropy_nan_and_infinite_logits(kernels):
     """A NaN logit makes its row's loss NaN and leaves the other rows alone;
     -inf logits (masked classes) are legal and get zero gradient."""
-    n, c = 4, 3001
+    n, c = 5, 3001
     x = randn(n, c).bfloat16()
     x[1, 17] = float("nan")
     x[2, :1000] = float("-inf")
-    tgt = torch.tensor([5, 6, 2000, 7])
+    x[4, :16] = float("-inf")  # a NaN in an otherwise -inf 16-byte chunk
+    x[4, 5] = float("nan")
+    tgt = torch.tensor([5, 6, 2000, 7, 100])
     tx, tt = dev(x), dev(tgt)
     out, lse, tw = torch.empty(n, device="cuda"), torch.empty(n, device="cuda"), torch.empty((), device="cuda")
     ws_n = lib().mi355x_cross_entropy_workspace_bytes(n)
@@ -382,7 +389,7 @@ def test_fused_cross_entropy_nan_and_infinite_logits(kernels):
     call("mi355x_cross_entropy_fwd", p(out), p(tw), p(lse), p(tx), CODE[torch.bfloat16], c, p(tt), n, c,
          0, -100, None, p(ws), ws_n, None)
     got = host(out)
-    assert math.isnan(got[1].item())
+    assert math.isnan(got[1].item()) and math.isnan(got[4].item())
     exp = torch.nn.functional.cross_entropy(x.float(), tgt, reduction="none")
     for i in (0, 2, 3):
         assert abs(got[i].item() - exp[i].item()) < 1e-4
