@@ -300,6 +300,8 @@ int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const void* x,
  * kernel.  Under autocast the f32 layer_norm output is cast to the matmul
  * dtype right away (fp32 policy for layer_norm, lower precision for linear:
  * mojo_device_autocast.py:537-567); the copy saves that cast's read of y.
+ * y may be NULL when y_low is given: only the copy and the statistics are
+ * written, and mi355x_layer_norm_apply produces y later if it is read.
  * No counterpart in the reference, whose cast is a separate _to_copy. */
 int mi355x_layer_norm_fwd_ex(void* y, void* y_low, int low_dtype, float* mean,
                              float* rstd, const void* x, const void* gamma,
@@ -317,6 +319,16 @@ int mi355x_layer_norm_fwd_add(void* y, void* y_low, int low_dtype, float* mean, 
                               void* x_out, const void* a, const void* r, int r_dtype,
                               const void* gamma, const void* beta, int64_t rows, int64_t cols,
                               double eps, int dtype, mi355x_stream_t stream);
+/* y = (x - mean)*rstd*gamma + beta from x and the statistics a forward
+ * saved (mean/rstd f32 [rows]; gamma/beta may be NULL), bit-identical to the
+ * y that forward (mi355x_layer_norm_fwd_ex or _fwd_add, whose x is x_out)
+ * would have written.  No counterpart in the reference: it serves the
+ * autocast forward that writes only the 16-bit copy and defers the f32
+ * output until something reads it (the next linear takes the copy, so in
+ * a training step nothing does). */
+int mi355x_layer_norm_apply(void* y, const void* x, const float* mean, const float* rstd,
+                            const void* gamma, const void* beta, int64_t rows, int64_t cols,
+                            int dtype, mi355x_stream_t stream);
 /* Any of dx/dgamma/dbeta may be NULL (output_mask, aten_fast.py:5475). */
 int64_t mi355x_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t cols);
 int mi355x_layer_norm_bwd(void* dx, void* dgamma, void* dbeta,

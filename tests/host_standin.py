@@ -246,7 +246,7 @@ class HostStandIn:
     def mi355x_layer_norm_fwd_ex(self, y, y_low, low_dt, mean, rstd, x, g, b, rows, cols, eps, dt, stream):
         self.mi355x_layer_norm_fwd(y, mean, rstd, x, g, b, rows, cols, eps, dt, stream)
         if y_low:
-            dense(_val(y_low), DT[low_dt], (rows, cols)).copy_(dense(_val(y), DT[dt], (rows, cols)))
+            dense(_val(y_low), DT[low_dt], (rows, cols)).copy_(self.last_ln_y)
         return 0
 
     def mi355x_add_cast(self, out, low, low_dt, a, r, r_dt, n, stream):
@@ -266,6 +266,18 @@ class HostStandIn:
         dense(_val(x_out), DT[dt], (rows, cols)).copy_(A.float() + R)
         return self.mi355x_layer_norm_fwd_ex(y, y_low, low_dt, mean, rstd, x_out, g, b, rows, cols, eps, dt, stream)
 
+    def mi355x_layer_norm_apply(self, y, x, mean, rstd, g, b, rows, cols, dt, stream):
+        X = dense(_val(x), DT[dt], (rows, cols)).float()
+        mu = dense(_val(mean), torch.float32, (rows, 1))
+        r = dense(_val(rstd), torch.float32, (rows, 1))
+        Y = (X - mu) * r
+        if g:
+            Y = Y * dense(_val(g), DT[dt], (cols,)).float()
+        if b:
+            Y = Y + dense(_val(b), DT[dt], (cols,)).float()
+        dense(_val(y), DT[dt], (rows, cols)).copy_(Y)
+        return 0
+
     def mi355x_layer_norm_fwd(self, y, mean, rstd, x, g, b, rows, cols, eps, dt, stream):
         X = dense(_val(x), DT[dt], (rows, cols)).float()
         mu = X.mean(1, keepdim=True)
@@ -276,7 +288,9 @@ class HostStandIn:
             Y = Y * dense(_val(g), DT[dt], (cols,)).float()
         if b:
             Y = Y + dense(_val(b), DT[dt], (cols,)).float()
-        dense(_val(y), DT[dt], (rows, cols)).copy_(Y)
+        self.last_ln_y = Y.to(DT[dt])
+        if y:
+            dense(_val(y), DT[dt], (rows, cols)).copy_(Y)
         if mean:
             dense(_val(mean), torch.float32, (rows,)).copy_(mu[:, 0])
         if rstd:

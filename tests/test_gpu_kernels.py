@@ -249,6 +249,60 @@ def test_layer_norm_fwd_bwd(kernels, dtype, rows, cols):
     tol_close(np64(db), edb, atol=atol * scale, rtol=atol, what="ln dbeta")
 
 
+@pytest.mark.parametrize("dtype,rows,cols", [(torch.float32, 16384, 768), (torch.float32, 33, 1000),
+                                             (torch.float32, 7, 4099), (torch.float32, 100, 2048),
+                                             (torch.bfloat16, 300, 768), (torch.float32, 5, 770)])
+@pytest.mark.parametrize("affine", [True, False])
+def test_layer_norm_output_deferred_to_apply_is_bit_identical(kernels, dtype, rows, cols, affine):
+    """The autocast forward writes only the 16-bit copy and the statistics
+    (y = null); mi355x_layer_norm_apply later computes y from x and those
+    statistics.  That y must be the forward's own y bit for bit, on the wave
+    path (cols a multiple of 4), on the any-width block path (4099, 770 with
+    an odd row pitch) and, for the fused residual add, from its x_out."""
+    x = randn(rows, cols) * 3 + 1
+    g, b = randn(cols), randn(cols)
+    xq, gq, bq = (t.to(dtype) for t in (x, g, b))
+    tx, tg, tb = dev(xq), dev(gq), dev(bq)
+    pg, pb = (p(tg), p(tb)) if affine else (None, None)
+    low_dt = torch.bfloat16 if dtype == torch.float32 else dtype
+
+    def stats():
+        return torch.empty(rows, device="cuda"), torch.empty(rows, device="cuda")
+
+    y = torch.empty(rows, cols, dtype=dtype, device="cuda")
+    mean, rstd = stats()
+    low = torch.empty(rows, cols, dtype=low_dt, device="cuda") if dtype == torch.float32 else None
+    call("mi355x_layer_norm_fwd_ex", p(y), p(low) if low is not None else None, CODE[low_dt], p(mean), p(rstd),
+         p(tx), pg, pb, rows, cols, 1e-5, CODE[dtype], None)
+    y2 = torch.full_like(y, float("nan"))
+    mean2, rstd2 = stats()
+    if low is not None:
+        low2 = torch.empty_like(low)
+        call("mi355x_layer_norm_fwd_ex", None, p(low2), CODE[low_dt], p(mean2), p(rstd2), p(tx), pg, pb,
+             rows, cols, 1e-5, CODE[dtype], None)
+        assert torch.equal(host(low2), host(low))
+        assert torch.equal(host(mean2), host(mean)) and torch.equal(host(rstd2), host(rstd))
+    else:
+        mean2, rstd2 = mean, rstd
+    call("mi355x_layer_norm_apply", p(y2), p(tx), p(mean2), p(rstd2), pg, pb, rows, cols, CODE[dtype], None)
+    assert torch.equal(host(y2), host(y))
+    if dtype == torch.float32 and cols % 4 == 0 and cols <= 2048:
+        r = dev(randn(rows, cols).bfloat16())
+        ya, xo = torch.empty_like(y), torch.empty_like(y)
+        lowa = torch.empty_like(low)
+        ma, ra = stats()
+        call("mi355x_layer_norm_fwd_add", p(ya), p(lowa), CODE[low_dt], p(ma), p(ra), p(xo), p(tx), p(r),
+             CODE[torch.bfloat16], pg, pb, rows, cols, 1e-5, CODE[dtype], None)
+        yb, xo2 = torch.full_like(y, float("nan")), torch.empty_like(y)
+        lowb = torch.empty_like(low)
+        mb, rb = stats()
+        call("mi355x_layer_norm_fwd_add", None, p(lowb), CODE[low_dt], p(mb), p(rb), p(xo2), p(tx), p(r),
+             CODE[torch.bfloat16], pg, pb, rows, cols, 1e-5, CODE[dtype], None)
+        assert torch.equal(host(xo2), host(xo)) and torch.equal(host(lowb), host(lowa))
+        call("mi355x_layer_norm_apply", p(yb), p(xo2), p(mb), p(rb), pg, pb, rows, cols, CODE[dtype], None)
+        assert torch.equal(host(yb), host(ya))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("approx", [0, 1])
 def test_gelu(kernels, dtype, approx):

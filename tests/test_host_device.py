@@ -256,6 +256,64 @@ def test_layer_norm_low_copy_feeds_autocast_linear(mojo):
     assert torch.allclose(z2.float().cpu(), 2 * yr, atol=3e-2)
 
 
+def test_autocast_layer_norm_output_is_computed_on_first_use(mojo):
+    """Under autocast the layer norm writes its bf16 copy and statistics; its
+    f32 output is produced (mi355x_layer_norm_apply, from the saved x, mean
+    and rstd) only when something touches it, never when the linear takes the
+    copy and the output dies.  Writes into its inputs (x, the weight) or into
+    the output itself wait for it."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(64, 768, generator=g)
+    w, b = torch.randn(768, generator=g), torch.randn(768, generator=g)
+    lw = torch.randn(32, 768, generator=g)
+    xm, wm, bm, lwm = (t.to("mojo") for t in (x, w, b, lw))
+    ref = F.layer_norm(x, (768,), w, b)
+    inner, counting, calls = _counting_library()
+    ek.set_library_for_tests(counting)
+
+    def ln(t=xm):
+        with torch.autocast("mojo", dtype=torch.bfloat16):
+            return F.layer_norm(t, (768,), wm, bm)
+
+    try:
+        # only the copy is used: the f32 output is never computed
+        with torch.autocast("mojo", dtype=torch.bfloat16):
+            y = F.layer_norm(xm, (768,), wm, bm)
+            assert ek._lazy
+            z = F.linear(y, lwm)
+        del y
+        assert not ek._lazy and calls["mi355x_layer_norm_apply"] == 0
+        zr = ref.bfloat16().float() @ lw.bfloat16().float().t()
+        assert torch.allclose(z.float().cpu(), zr, atol=3e-2, rtol=2e-2)
+        # a host read, a kernel, a view
+        assert torch.allclose(ln().cpu(), ref, atol=1e-5, rtol=1e-5)
+        assert torch.allclose((ln() * 2).cpu(), 2 * ref, atol=2e-5, rtol=1e-5)
+        assert torch.allclose(ln()[5].cpu(), ref[5], atol=1e-5, rtol=1e-5)
+        assert calls["mi355x_layer_norm_apply"] == 3 and not ek._lazy
+        # writes into x, the weight and the output itself wait for it
+        x2 = xm.clone()
+        y = ln(x2)
+        x2.mul_(0)
+        assert torch.allclose(y.cpu(), ref, atol=1e-5, rtol=1e-5)
+        y = ln()
+        wm.add_(1.0)
+        assert torch.allclose(y.cpu(), ref, atol=1e-5, rtol=1e-5)
+        wm.sub_(1.0)
+        y = ln()
+        y.add_(1.0)
+        assert torch.allclose(y.cpu(), ref + 1, atol=2e-5, rtol=1e-5)
+        # the output of a fused residual add + norm: x is the add's result
+        d = torch.randn(64, 768, generator=g).bfloat16()
+        s = xm + d.to("mojo")
+        y = ln(s)
+        assert torch.allclose(y.cpu(), F.layer_norm(x + d.float(), (768,), w, b), atol=1e-5, rtol=1e-5)
+    finally:
+        ek.set_library_for_tests(inner)
+    assert not ek._lazy
+
+
 def test_adamw_parameter_copies_feed_next_autocast_forward(mojo):
     """The fused AdamW step writes the bf16 copy of every parameter the
     autocast forward casts; the next forward uses it with no cast kernel.  A

@@ -24,8 +24,17 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxBwdBlocks = 1024;
 
-// y_low (optional, element type TL): a second copy of y rounded to a 16-bit
-// type, the operand an autocast matmul consumes next.
+// y = (x - mean) * rstd * gamma + beta (gamma 1 and beta 0 when absent):
+// every forward kernel and ln_apply evaluate it through this one function,
+// so y recomputed later from x and the saved statistics has the same bits.
+__device__ __forceinline__ float ln_out(float x, float mu, float r, float g, float b) {
+  return (x - mu) * r * g + b;
+}
+
+// y (optional when y_low is given) and y_low (optional, element type TL): a
+// second copy of y rounded to a 16-bit type, the operand an autocast matmul
+// consumes next.  A caller that needs only the 16-bit copy passes y = null
+// and can produce y later with mi355x_layer_norm_apply.
 template <typename T, typename TL, int NV>
 __global__ void __launch_bounds__(kThreads)
     ln_fwd_wave(T* __restrict__ y, TL* __restrict__ y_low, float* __restrict__ mean_out,
@@ -63,7 +72,6 @@ __global__ void __launch_bounds__(kThreads)
   }
   const float var = wave_sum(q) * inv_n;
   const float r = 1.f / sqrtf(var + eps);
-  T* yr = y + row * cols;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (j * 64 + lane) * 4;
@@ -73,8 +81,8 @@ __global__ void __launch_bounds__(kThreads)
       if (beta) Vec4<T>::load(beta + c, b);
       float o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - mu) * r * g[e] + b[e];
-      Vec4<T>::store(yr + c, o);
+      for (int e = 0; e < 4; ++e) o[e] = ln_out(v[j][e], mu, r, g[e], b[e]);
+      if (y) Vec4<T>::store(y + row * cols + c, o);
       if (y_low) Vec4<TL>::store(y_low + row * cols + c, o);
     }
   }
@@ -140,8 +148,8 @@ __global__ void __launch_bounds__(kThreads)
       if (beta) Vec4<T>::load(beta + c, b);
       float o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - mu) * rs * g[e] + b[e];
-      Vec4<T>::store(y + base + c, o);
+      for (int e = 0; e < 4; ++e) o[e] = ln_out(v[j][e], mu, rs, g[e], b[e]);
+      if (y) Vec4<T>::store(y + base + c, o);
       if (y_low) Vec4<TL>::store(y_low + base + c, o);
     }
   }
@@ -170,17 +178,45 @@ __global__ void __launch_bounds__(kThreads)
   }
   const float var = block_sum(q, red) / (float)cols;
   const float r = 1.f / sqrtf(var + eps);
-  T* yr = y + row * cols;
   for (int64_t c = threadIdx.x; c < cols; c += kThreads) {
-    float o = (to_f32(xr[c]) - mu) * r;
-    if (gamma) o *= to_f32(gamma[c]);
-    if (beta) o += to_f32(beta[c]);
-    yr[c] = from_f32<T>(o);
+    const float o = ln_out(to_f32(xr[c]), mu, r, gamma ? to_f32(gamma[c]) : 1.f, beta ? to_f32(beta[c]) : 0.f);
+    if (y) y[row * cols + c] = from_f32<T>(o);
     if (y_low) y_low[row * cols + c] = from_f32<TL>(o);
   }
   if (threadIdx.x == 0) {
     if (mean_out) mean_out[row] = mu;
     if (rstd_out) rstd_out[row] = r;
+  }
+}
+
+// y from x and the statistics a forward saved (mean, rstd per row): the
+// output of a forward that wrote only its 16-bit copy, produced when it is
+// first read.  Four elements per thread when the rows allow 16-byte access.
+template <typename T, bool V4>
+__global__ void __launch_bounds__(kThreads)
+    ln_apply(T* __restrict__ y, const T* __restrict__ x, const float* __restrict__ mean,
+             const float* __restrict__ rstd, const T* __restrict__ gamma, const T* __restrict__ beta,
+             int64_t rows, int64_t cols) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  if constexpr (V4) {
+    const int64_t n4 = rows * cols / 4;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4; i += stride) {
+      const int64_t row = i * 4 / cols, c = i * 4 - row * cols;
+      float v[4], g[4] = {1.f, 1.f, 1.f, 1.f}, b[4] = {0.f, 0.f, 0.f, 0.f}, o[4];
+      Vec4<T>::load(x + i * 4, v);
+      if (gamma) Vec4<T>::load(gamma + c, g);
+      if (beta) Vec4<T>::load(beta + c, b);
+      const float mu = mean[row], r = rstd[row];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = ln_out(v[e], mu, r, g[e], b[e]);
+      Vec4<T>::store(y + i * 4, o);
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < rows * cols; i += stride) {
+      const int64_t row = i / cols, c = i - row * cols;
+      y[i] = from_f32<T>(ln_out(to_f32(x[i]), mean[row], rstd[row], gamma ? to_f32(gamma[c]) : 1.f,
+                                beta ? to_f32(beta[c]) : 0.f));
+    }
   }
 }
 
@@ -679,7 +715,7 @@ extern "C" int mi355x_layer_norm_fwd_ex(void* y, void* y_low, int low_dtype, flo
   MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_layer_norm_fwd: bad shape [%lld, %lld]",
              (long long)rows, (long long)cols);
   if (rows == 0) return MI355X_OK;
-  MI_REQUIRE(y && x, "mi355x_layer_norm_fwd: null pointer");
+  MI_REQUIRE(x && (y || y_low), "mi355x_layer_norm_fwd: null pointer");
   MI_REQUIRE(!y_low || (dtype == MI355X_F32 && (low_dtype == MI355X_BF16 || low_dtype == MI355X_F16)),
              "mi355x_layer_norm_fwd: the low-precision copy needs f32 input and a bf16/f16 copy");
   hipStream_t s = (hipStream_t)stream;
@@ -707,7 +743,7 @@ extern "C" int mi355x_layer_norm_fwd_add(void* y, void* y_low, int low_dtype, fl
   MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_layer_norm_fwd_add: bad shape [%lld, %lld]", (long long)rows,
              (long long)cols);
   if (rows == 0) return MI355X_OK;
-  MI_REQUIRE(y && x_out && a && r, "mi355x_layer_norm_fwd_add: null pointer");
+  MI_REQUIRE((y || y_low) && x_out && a && r, "mi355x_layer_norm_fwd_add: null pointer");
   MI_REQUIRE(dtype == MI355X_F32, "mi355x_layer_norm_fwd_add: f32 rows only (got dtype %d)", dtype);
   MI_REQUIRE(r_dtype == MI355X_F32 || r_dtype == MI355X_BF16 || r_dtype == MI355X_F16,
              "mi355x_layer_norm_fwd_add: unsupported residual dtype %d", r_dtype);
@@ -736,6 +772,36 @@ extern "C" int mi355x_layer_norm_fwd(void* y, float* mean, float* rstd, const vo
                                      const void* gamma, const void* beta, int64_t rows,
                                      int64_t cols, double eps, int dtype, mi355x_stream_t stream) {
   return mi355x_layer_norm_fwd_ex(y, nullptr, 0, mean, rstd, x, gamma, beta, rows, cols, eps, dtype, stream);
+}
+
+extern "C" int mi355x_layer_norm_apply(void* y, const void* x, const float* mean, const float* rstd,
+                                       const void* gamma, const void* beta, int64_t rows, int64_t cols,
+                                       int dtype, mi355x_stream_t stream) {
+  MI_REQUIRE(rows >= 0 && cols > 0, "mi355x_layer_norm_apply: bad shape [%lld, %lld]", (long long)rows,
+             (long long)cols);
+  if (rows == 0) return MI355X_OK;
+  MI_REQUIRE(y && x && mean && rstd, "mi355x_layer_norm_apply: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&](auto tag) {
+    using T = decltype(tag);
+    const size_t al = 4 * sizeof(T);
+    const bool v4 = cols % 4 == 0 && aligned(x, al) && aligned(y, al) && aligned(gamma, al) && aligned(beta, al);
+    const int64_t n = v4 ? rows * cols / 4 : rows * cols;
+    const unsigned grid = (unsigned)(n / kThreads + 1 < 65536 ? n / kThreads + 1 : 65536);
+    if (v4)
+      ln_apply<T, true><<<grid, kThreads, 0, s>>>((T*)y, (const T*)x, mean, rstd, (const T*)gamma,
+                                                   (const T*)beta, rows, cols);
+    else
+      ln_apply<T, false><<<grid, kThreads, 0, s>>>((T*)y, (const T*)x, mean, rstd, (const T*)gamma,
+                                                    (const T*)beta, rows, cols);
+  };
+  switch (dtype) {
+    case MI355X_F32: go(float{}); break;
+    case MI355X_BF16: go(bf16{}); break;
+    case MI355X_F16: go(f16{}); break;
+    default: return fail(MI355X_EUNSUPPORTED, "mi355x_layer_norm_apply: unsupported dtype %d", dtype);
+  }
+  return check_launch("mi355x_layer_norm_apply");
 }
 
 extern "C" int64_t mi355x_layer_norm_bwd_workspace_bytes(int64_t rows, int64_t cols) {

@@ -36,7 +36,7 @@ int check_launch(const char* what) {
 
 extern "C" {
 
-int mi355x_abi_version(void) { return 5; }
+int mi355x_abi_version(void) { return 6; }
 
 const char* mi355x_last_error(void) { return mi::g_error; }
 

@@ -21,7 +21,7 @@ from pathlib import Path
 
 LIB_NAME = "libmi355x_kernels.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 c_int = ctypes.c_int
 c_i64 = ctypes.c_int64
@@ -96,6 +96,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],
     ),
+    "mi355x_layer_norm_apply": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_int, c_vp]),
     "mi355x_layer_norm_bwd_workspace_bytes": (c_i64, [c_i64, c_i64]),
     "mi355x_layer_norm_bwd": (
         c_int,
@@ -353,6 +354,98 @@ def flush_pending() -> None:
                 _pending.pop(0).launch()
         finally:
             _state.flushing = False
+
+
+class Lazy:
+    """An output whose kernel has not run yet: `holder` (held weakly) is the
+    storage the kernel fills, `inputs` the tensors it reads, `launch()` runs
+    it.  The layer norm under autocast registers its f32 output this way
+    (the next linear takes the 16-bit copy instead)."""
+
+    __slots__ = ("holder", "inputs", "launch")
+
+    def __init__(self, holder, inputs, launch):
+        self.holder, self.inputs, self.launch = holder, inputs, launch
+
+
+_lazy: dict = {}  # id(storage holder) -> Lazy, while the holder lives
+
+
+def lazy(out, inputs, launch) -> None:
+    """Register `out` (a fresh tensor) as filled by `launch` when first
+    touched: `materialize_touched` runs it before any op that reads or writes
+    out's storage, or that writes the storage of one of `inputs`; if out's
+    storage dies first, the launch never runs.  The record holds the storage
+    only weakly, so it cannot outlive it (the allocator may then reuse the
+    memory), and its key is removed when the storage goes."""
+    import weakref
+
+    key = id(out._holder)
+
+    def gone(_ref, key=key):
+        with _pending_lock:
+            rec = _lazy.get(key)
+            if rec is not None and rec.holder is _ref:
+                del _lazy[key]
+
+    with _pending_lock:
+        _lazy[key] = Lazy(weakref.ref(out._holder, gone), tuple(inputs), launch)
+
+
+def lazy_live() -> bool:
+    return bool(_lazy)
+
+
+def _holders_of(args, kwargs) -> set:
+    found = set()
+
+    def add(v):
+        h = getattr(v, "_holder", None)
+        if h is not None:
+            found.add(id(h))
+
+    for v in args:
+        if isinstance(v, (list, tuple)):
+            for e in v:
+                add(e)
+        else:
+            add(v)
+    if kwargs:
+        for v in kwargs.values():
+            if isinstance(v, (list, tuple)):
+                for e in v:
+                    add(e)
+            else:
+                add(v)
+    return found
+
+
+def materialize_touched(args, kwargs, writes: bool) -> None:
+    """Run the lazy launches that an op with these arguments depends on: those
+    whose output storage it touches, and, when the op writes (`writes`), those
+    reading a storage it touches (they must run before it changes)."""
+    if not _lazy:
+        return
+    hs = _holders_of(args, kwargs)
+    if not hs:
+        return
+    with _pending_lock:
+        due = []
+        for key, rec in list(_lazy.items()):
+            if rec.holder() is None:
+                continue
+            if key in hs or (writes and any(id(t._holder) in hs for t in rec.inputs)):
+                due.append(key)
+        for key in due:
+            rec = _lazy.pop(key, None)
+            if rec is not None and rec.holder() is not None:
+                rec.launch()
+
+
+def materialize(t) -> None:
+    """Run the lazy launch that fills t's storage, if one is pending."""
+    if _lazy:
+        materialize_touched((t,), None, False)
 
 
 def lib() -> ctypes.CDLL:

@@ -19,10 +19,11 @@ from __future__ import annotations
 import ctypes
 import math
 import numbers
+import os
 
 import torch
 
-from . import AdamWTensor, Deferred, check, defer, flush_pending, lib, take_pending
+from . import AdamWTensor, Deferred, check, defer, flush_pending, lazy, lib, take_pending
 from ..mojo_device.torch_mojo_tensor import (
     DTYPE_CODE,
     TorchMojoTensor,
@@ -1437,6 +1438,8 @@ def ws_ptr_or_none(p):
 # gradient as direct kernel calls, without per-view dispatches)
 # ---------------------------------------------------------------------------
 _LOW_ATTR = "_mojo_low_copy"
+# MI355X_LAZY_LN_OUT=0 writes the f32 layer-norm output eagerly (A/B measurement)
+_LAZY_LN_OUT = os.environ.get("MI355X_LAZY_LN_OUT", "1") != "0"
 
 
 def _take_low_copy(t: MT, dtype):
@@ -1728,6 +1731,10 @@ def fast_aten_native_layer_norm(input, normalized_shape, weight, bias, eps):
     # kernel also writes y in that dtype, which the cast then takes.
     low_dt = _autocast_low_dtype() if a._dtype == torch.float32 else None
     low = _alloc(a._shape, low_dt, a._device) if (low_dt is not None and rows and cols) else None
+    # With the 16-bit copy written, the f32 y is left to a lazy launch: in an
+    # autocast step only the copy is read (the next linear takes it).
+    defer_y = low is not None and _LAZY_LN_OUT
+    y_ptr = None if defer_y else out._ptr
     # the input is a held-back residual add: compute it in the norm's pass
     rec = take_pending(lambda r: r.out._holder is x._holder and r.out._ptr == x._ptr
                        and tuple(r.out._shape) == tuple(x._shape)) if rows and cols else None
@@ -1735,7 +1742,7 @@ def fast_aten_native_layer_norm(input, normalized_shape, weight, bias, eps):
     if rec is not None:
         ra, rr = rec.inputs
         rc = lib().mi355x_layer_norm_fwd_add(
-            out._ptr, low._ptr if low is not None else None, _code(low_dt) if low is not None else 0,
+            y_ptr, low._ptr if low is not None else None, _code(low_dt) if low is not None else 0,
             mean._ptr, rstd._ptr, x._ptr, ra._ptr, rr._ptr, _code(rr._dtype), g._ptr if g is not None else None,
             b._ptr if b is not None else None, rows, cols, float(eps), _code(a._dtype), _STREAM,
         )
@@ -1746,13 +1753,20 @@ def fast_aten_native_layer_norm(input, normalized_shape, weight, bias, eps):
         check(
             "mi355x_layer_norm_fwd_ex",
             lib().mi355x_layer_norm_fwd_ex(
-                out._ptr, low._ptr if low is not None else None, _code(low_dt) if low is not None else 0,
+                y_ptr, low._ptr if low is not None else None, _code(low_dt) if low is not None else 0,
                 mean._ptr, rstd._ptr, x._ptr, g._ptr if g is not None else None,
                 b._ptr if b is not None else None, rows, cols, float(eps), _code(a._dtype), _STREAM,
             ),
         )
     if low is not None:
         setattr(out, _LOW_ATTR, (low, out._version))
+    if defer_y:
+        def fill(y=out._ptr, x=x, mean=mean, rstd=rstd, g=g, b=b, code=_code(a._dtype)):
+            check("mi355x_layer_norm_apply", lib().mi355x_layer_norm_apply(
+                y, x._ptr, mean._ptr, rstd._ptr, g._ptr if g is not None else None,
+                b._ptr if b is not None else None, rows, cols, code, _STREAM))
+
+        lazy(out, [t for t in (x, mean, rstd, g, b) if t is not None], fill)
     if a._dtype != torch.float32:
         # ATen returns the statistics in the input dtype (aten_fast.py:5228-5245)
         mean = materialize_contiguous(mean, a._dtype)

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import torch
 
+from .. import eager_kernels as _ek
 from ..eager_kernels import aten_fast as _aten_fast
 
 # OpOverload -> python implementation (filled by register_mojo_devices)
@@ -23,13 +24,18 @@ _DISABLE = torch._C._DisableTorchDispatch
 _MUTABLE: dict = {}  # OpOverload -> whether its schema writes an argument
 
 
+def _is_mutable(func) -> bool:
+    mutable = _MUTABLE.get(func)
+    if mutable is None:
+        mutable = _MUTABLE[func] = func._schema.is_mutable
+    return mutable
+
+
 def dispatch(func, args, kwargs):
-    if _aten_fast._param_low_by_holder:  # parameter copies exist (autocast training)
-        mutable = _MUTABLE.get(func)
-        if mutable is None:
-            mutable = _MUTABLE[func] = func._schema.is_mutable
-        if mutable:
-            _aten_fast.drop_param_copies_written_by(func, args, kwargs)
+    if _ek._lazy:  # outputs whose kernel waits for a first use (autocast layer norm)
+        _ek.materialize_touched(args, kwargs, _is_mutable(func))
+    if _aten_fast._param_low_by_holder and _is_mutable(func):  # parameter copies exist (autocast training)
+        _aten_fast.drop_param_copies_written_by(func, args, kwargs)
     impl = DIRECT.get(func)
     if impl is not None:
         return impl(*args, **kwargs)

@@ -234,8 +234,9 @@ class TorchMojoTensor(torch.Tensor):
         """D2H copy into a new CPU tensor (waits for pending device work).
         A bounds error that a kernel flagged since the last host read is
         raised here."""
-        from ..eager_kernels import aten_fast, flush_pending
+        from ..eager_kernels import aten_fast, flush_pending, materialize
 
+        materialize(self)  # an output whose kernel waits for its first use
         flush_pending()  # launches held back for fusion write what is read here
         aten_fast.raise_pending_device_errors()
         src = self._contig()
