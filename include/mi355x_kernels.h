@@ -427,12 +427,16 @@ int mi355x_fused_adamw(const mi355x_adamw_tensor* tensors, int n, double lr,
  * param_low itself NULL) to 16-bit copies (low_dtype bf16/f16) that the
  * kernel fills with each updated parameter, for the autocast forward that
  * follows (mojo_device_autocast.py:537-567 casts every f32 weight to the
- * matmul dtype).  No counterpart in the reference. */
+ * matmul dtype); and grad_mul (NULL, or a device f32 scalar) multiplying
+ * every gradient as it is read (before maximize and grad_scale), which
+ * applies a pending in-place gradient scale (clip_grad_norm_'s
+ * _foreach_mul_) without a pass over the gradients: the same product the
+ * separate multiply stores.  No counterpart in the reference. */
 int mi355x_fused_adamw_ex(const mi355x_adamw_tensor* tensors, void* const* param_low,
                           int low_dtype, int n, double lr, const float* lr_ptr,
                           double beta1, double beta2, double weight_decay, double eps,
                           int flags, const float* grad_scale, const float* found_inf,
-                          mi355x_stream_t stream);
+                          const float* grad_mul, mi355x_stream_t stream);
 
 /* Per-tensor p-norm (ord 2 or 1, or inf when ord_inf) of n f32/bf16 tensors
  * into outs[i] (a device scalar of out_dtype). */

@@ -426,10 +426,14 @@ class HostStandIn:
         return 0
 
     # ---- optimizer ----
-    def mi355x_fused_adamw_ex(self, descs, lows, low_dt, n, lr, lr_ptr, b1, b2, wd, eps, flags, gs, fi, stream):
+    def mi355x_fused_adamw_ex(self, descs, lows, low_dt, n, lr, lr_ptr, b1, b2, wd, eps, flags, gs, fi, gm, stream):
         if fi and dense(_val(fi), torch.float32, ()).item() != 0:
             return 0
-        self.mi355x_fused_adamw(descs, n, lr, lr_ptr, b1, b2, wd, eps, flags, gs, fi, stream)
+        self.grad_mul = gm
+        try:
+            self.mi355x_fused_adamw(descs, n, lr, lr_ptr, b1, b2, wd, eps, flags, gs, fi, stream)
+        finally:
+            self.grad_mul = None
         if lows:
             arr = ctypes.cast(lows, ctypes.POINTER(ctypes.c_void_p))
             for i in range(n):
@@ -448,6 +452,9 @@ class HostStandIn:
             m = d.numel
             p = dense(d.param, torch.float32, (m,))
             g = dense(d.grad, torch.float32, (m,)).clone()
+            gm = getattr(self, "grad_mul", None)
+            if gm:
+                g = g * dense(_val(gm), torch.float32, ()).item()
             if gs:
                 g = g / dense(_val(gs), torch.float32, ()).item()
             if flags & 2:

@@ -519,7 +519,7 @@ def test_fused_adamw_matches_oracle(kernels, amsgrad, maximize, wd):
                 for i, s_ in enumerate(sizes)]
         lp = (ctypes.c_void_p * len(sizes))(*[p(x) if x is not None else None for x in lows])
         call("mi355x_fused_adamw_ex", d, lp, CODE[torch.bfloat16], len(sizes), 6e-4, None, 0.9, 0.95, wd, 1e-8,
-             flags, None, None, None)
+             flags, None, None, None, None)
         for i, x in enumerate(lows):
             if x is not None:
                 assert torch.equal(host(x), host(tp[i]).bfloat16()), i
@@ -529,6 +529,34 @@ def test_fused_adamw_matches_oracle(kernels, amsgrad, maximize, wd):
         tol_close(np64(tp[i]), exp[0], atol=1e-6, rtol=1e-5, what=f"p{i}")
         tol_close(np64(tm[i]), exp[1], atol=1e-6, rtol=1e-5, what=f"m{i}")
         tol_close(np64(tv[i]), exp[2], atol=1e-7, rtol=1e-5, what=f"v{i}")
+
+
+@pytest.mark.parametrize("maximize", [False, True])
+def test_fused_adamw_grad_mul_is_the_scale_pass_fused(kernels, maximize):
+    """grad_mul (a pending clip_grad_norm_ scale) gives the bits of the
+    separate in-place multiply (mi355x_foreach_apply, as _foreach_mul_ runs
+    it) followed by the step, and leaves the gradients as they were."""
+    sizes = [768 * 768 + 3, 50257, 5, 4 * 65536 + 17]
+    ps = [randn(s) for s in sizes]
+    gs = [randn(s) for s in sizes]
+    ms = [randn(s) * 0.1 for s in sizes]
+    vs = [randn(s).abs() * 0.01 for s in sizes]
+    coef = dev(torch.tensor(0.3712))
+    runs = []
+    for fused in (False, True):
+        tp, tg, tm, tv = ([dev(x) for x in xs] for xs in (ps, gs, ms, vs))
+        steps = [dev(torch.tensor(3.0)) for _ in sizes]
+        if not fused:
+            call("mi355x_foreach_apply", 2, (ctypes.c_void_p * len(sizes))(*[p(t) for t in tg]), None, None, None,
+                 i64(*sizes), len(sizes), CODE[torch.float32], 0.0, p(coef), None)
+        d = _adam_descs(tp, tg, tm, tv, steps)
+        call("mi355x_fused_adamw_ex", d, None, 0, len(sizes), 6e-4, None, 0.9, 0.95, 0.1, 1e-8,
+             2 if maximize else 0, None, None, p(coef) if fused else None, None)
+        runs.append((tp, tm, tv, tg))
+    for i in range(len(sizes)):
+        for a, b in zip(runs[0][:3], runs[1][:3]):
+            assert torch.equal(host(a[i]), host(b[i])), i
+        assert torch.equal(host(runs[1][3][i]), gs[i]), i
 
 
 def test_fused_adamw_found_inf_skips_and_wd0_keeps_inf(kernels):

@@ -314,6 +314,67 @@ def test_autocast_layer_norm_output_is_computed_on_first_use(mojo):
     assert not ek._lazy
 
 
+def test_clip_scale_is_applied_inside_the_fused_adamw_step(mojo):
+    """clip_grad_norm_'s _foreach_mul_ of the gradients is held back and the
+    fused AdamW step applies it as it reads them (grad_mul): no separate
+    multiply runs, the update equals stock PyTorch's, and the gradients still
+    read as scaled afterwards (the multiply then runs once)."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    torch.manual_seed(3)
+    ref = torch.nn.Sequential(torch.nn.Linear(16, 32), torch.nn.GELU(), torch.nn.Linear(32, 4))
+    dev = torch.nn.Sequential(torch.nn.Linear(16, 32), torch.nn.GELU(), torch.nn.Linear(32, 4))
+    dev.load_state_dict(ref.state_dict())
+    dev.to("mojo")
+    opts = [torch.optim.AdamW(m.parameters(), lr=1e-2, fused=(m is dev)) for m in (ref, dev)]
+    x = torch.randn(8, 16)
+    inner = ek.lib()
+    muls = []
+
+    class MulCounting:  # counts foreach multiplies (opcode 2; the step count's add is opcode 0)
+        def __getattr__(self, name):
+            fn = getattr(inner, name)
+            if name != "mi355x_foreach_apply":
+                return fn
+
+            def wrapped(op, *a):
+                if op == 2:
+                    muls.append(1)
+                return fn(op, *a)
+
+            return wrapped
+
+    calls = {}
+    ek.set_library_for_tests(MulCounting())
+    try:
+        for m, opt, xx in ((ref, opts[0], x), (dev, opts[1], x.to("mojo"))):
+            (m(xx) ** 2).sum().backward()
+            n = torch.nn.utils.clip_grad_norm_(m.parameters(), 0.1)
+            assert float(n.cpu()) > 0.1  # the clip scales
+            opt.step()
+        calls["mi355x_foreach_apply"] = len(muls)
+        assert calls["mi355x_foreach_apply"] == 0 and ek._lazy
+        for a, b in zip(ref.parameters(), dev.parameters()):
+            assert torch.allclose(b.detach().cpu(), a.detach(), atol=1e-6, rtol=1e-5)
+        for a, b in zip(ref.parameters(), dev.parameters()):
+            assert torch.allclose(b.grad.cpu(), a.grad, atol=1e-7, rtol=1e-5)
+        calls["mi355x_foreach_apply"] = len(muls)
+        assert calls["mi355x_foreach_apply"] == 1 and not ek._lazy
+        # a second step: the grads die at zero_grad, the multiply never runs
+        for m, opt, xx in ((ref, opts[0], x), (dev, opts[1], x.to("mojo"))):
+            opt.zero_grad()
+            (m(xx) ** 2).sum().backward()
+            torch.nn.utils.clip_grad_norm_(m.parameters(), 0.1)
+            opt.step()
+            opt.zero_grad()
+        calls["mi355x_foreach_apply"] = len(muls)
+        assert calls["mi355x_foreach_apply"] == 1 and not ek._lazy
+        for a, b in zip(ref.parameters(), dev.parameters()):
+            assert torch.allclose(b.detach().cpu(), a.detach(), atol=1e-6, rtol=1e-5)
+    finally:
+        ek.set_library_for_tests(inner)
+
+
 def test_adamw_parameter_copies_feed_next_autocast_forward(mojo):
     """The fused AdamW step writes the bf16 copy of every parameter the
     autocast forward casts; the next forward uses it with no cast kernel.  A

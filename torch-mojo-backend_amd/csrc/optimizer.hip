@@ -7,7 +7,7 @@
 // binary search over the chunk prefix sums.  Contiguous f32 data moves as float4.
 //
 // AdamW (torch.optim.AdamW, decoupled weight decay), per element:
-//   g = maximize ? -g : g;  g /= grad_scale (if given)
+//   g *= grad_mul (if given);  g = maximize ? -g : g;  g /= grad_scale (if given)
 //   p -= lr*wd*p                         (skipped when wd == 0)
 //   m = b1*m + (1-b1)*g;  v = b2*v + (1-b2)*g*g
 //   vmax = max(vmax, v)                  (amsgrad)
@@ -59,6 +59,7 @@ struct AdamScalars {
   const float* lr_ptr;
   const float* grad_scale;
   const float* found_inf;
+  const float* grad_mul;
 };
 
 template <typename TL>
@@ -102,6 +103,8 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
   const bool decay = s.wd != 0.f;
   const bool maximize = s.flags & MI355X_ADAMW_MAXIMIZE;
   const float inv_scale = s.grad_scale ? 1.f / *s.grad_scale : 1.f;
+  const bool has_mul = s.grad_mul != nullptr;
+  const float gmul = has_mul ? *s.grad_mul : 1.f;
   const bool vec = ((((uintptr_t)t.param | (uintptr_t)t.grad | (uintptr_t)t.exp_avg |
                       (uintptr_t)t.exp_avg_sq) & 15) == 0) && (((uintptr_t)low & 7) == 0) &&
                    t.max_exp_avg_sq == nullptr && (begin % 4 == 0);
@@ -115,7 +118,8 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
       float pp[4] = {p.x, p.y, p.z, p.w}, mm[4] = {m.x, m.y, m.z, m.w}, vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float gj = (maximize ? -gg[j] : gg[j]) * inv_scale;
+        const float g0 = has_mul ? gg[j] * gmul : gg[j];
+        float gj = (maximize ? -g0 : g0) * inv_scale;
         adam_elem(pp[j], gj, mm[j], vv[j], nullptr, lr, s.b1, s.b2, s.wd, s.eps, step_size, bc2_sqrt, decay);
       }
       p = make_float4(pp[0], pp[1], pp[2], pp[3]);
@@ -159,6 +163,7 @@ __global__ void __launch_bounds__(kThreads) adamw_kernel(AdamBatch b, AdamScalar
   for (int64_t e = i + threadIdx.x; e < end; e += kThreads) {
     float p = t.param[e], m = t.exp_avg[e], v = t.exp_avg_sq[e];
     float g = t.grad[e];
+    if (has_mul) g *= gmul;
     g = (maximize ? -g : g) * inv_scale;
     adam_elem(p, g, m, v, t.max_exp_avg_sq ? t.max_exp_avg_sq + e : nullptr, lr, s.b1, s.b2, s.wd,
               s.eps, step_size, bc2_sqrt, decay);
@@ -337,13 +342,13 @@ using namespace mi;
 extern "C" int mi355x_fused_adamw_ex(const mi355x_adamw_tensor* tensors, void* const* param_low, int low_dtype,
                                      int n, double lr, const float* lr_ptr, double beta1, double beta2,
                                      double weight_decay, double eps, int flags, const float* grad_scale,
-                                     const float* found_inf, mi355x_stream_t stream) {
+                                     const float* found_inf, const float* grad_mul, mi355x_stream_t stream) {
   MI_REQUIRE(n >= 0 && (n == 0 || tensors), "mi355x_fused_adamw: bad tensor list");
   MI_REQUIRE(!param_low || low_dtype == MI355X_BF16 || low_dtype == MI355X_F16,
              "mi355x_fused_adamw: the parameter copies must be bf16 or f16");
   hipStream_t s = (hipStream_t)stream;
   AdamScalars sc{(float)lr, (float)beta1, (float)beta2, (float)weight_decay, (float)eps, flags,
-                 lr_ptr, grad_scale, found_inf};
+                 lr_ptr, grad_scale, found_inf, grad_mul};
   for (int base = 0; base < n; base += kAdamBatch) {
     AdamBatch b{};
     b.n = 0;
@@ -378,7 +383,7 @@ extern "C" int mi355x_fused_adamw(const mi355x_adamw_tensor* tensors, int n, dou
                                   const float* grad_scale, const float* found_inf,
                                   mi355x_stream_t stream) {
   return mi355x_fused_adamw_ex(tensors, nullptr, 0, n, lr, lr_ptr, beta1, beta2, weight_decay, eps, flags,
-                               grad_scale, found_inf, stream);
+                               grad_scale, found_inf, nullptr, stream);
 }
 
 extern "C" int64_t mi355x_foreach_norm_workspace_bytes(const int64_t* numels, int n) {

@@ -138,7 +138,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [
             ctypes.POINTER(AdamWTensor), c_vp, c_int, c_int, c_double, c_vp, c_double, c_double,
-            c_double, c_double, c_int, c_vp, c_vp, c_vp,
+            c_double, c_double, c_int, c_vp, c_vp, c_vp, c_vp,
         ],
     ),
     "mi355x_foreach_norm_workspace_bytes": (c_i64, [P_i64, c_int]),
@@ -357,39 +357,88 @@ def flush_pending() -> None:
 
 
 class Lazy:
-    """An output whose kernel has not run yet: `holder` (held weakly) is the
-    storage the kernel fills, `inputs` the tensors it reads, `launch()` runs
-    it.  The layer norm under autocast registers its f32 output this way
-    (the next linear takes the 16-bit copy instead)."""
+    """Work on some storages that has not run yet: `launch()` runs it, `inputs`
+    are the tensors it reads, `refs` maps the id of each storage holder it
+    writes to a weak reference (the record never keeps a storage alive).
+    Two kinds: an output the kernel has not filled (the layer norm's f32
+    output under autocast), and an in-place scale not yet applied (the
+    gradient-clipping `_foreach_mul_`), whose `scale` is the scalar tensor
+    and which a fused optimizer step can apply on the fly."""
 
-    __slots__ = ("holder", "inputs", "launch")
+    __slots__ = ("refs", "inputs", "launch", "scale")
 
-    def __init__(self, holder, inputs, launch):
-        self.holder, self.inputs, self.launch = holder, inputs, launch
+    def __init__(self, inputs, launch, scale=None):
+        self.refs, self.inputs, self.launch, self.scale = {}, tuple(inputs), launch, scale
 
 
 _lazy: dict = {}  # id(storage holder) -> Lazy, while the holder lives
+_lazy_records: dict = {}  # id(Lazy) -> Lazy, the records with a live holder
+
+
+def _register(rec: Lazy, tensors) -> None:
+    import weakref
+
+    def gone(ref, rec=rec):
+        with _pending_lock:
+            for key, r in list(rec.refs.items()):
+                if r is ref:
+                    del rec.refs[key]
+                    if _lazy.get(key) is rec:
+                        del _lazy[key]
+            if not rec.refs:
+                _lazy_records.pop(id(rec), None)
+
+    with _pending_lock:
+        for t in tensors:
+            key = id(t._holder)
+            old = _lazy.get(key)
+            if old is not None and old is not rec:
+                _run(old)  # an earlier record on the same storage goes first
+            rec.refs[key] = weakref.ref(t._holder, gone)
+            _lazy[key] = rec
+        _lazy_records[id(rec)] = rec
+
+
+def _run(rec: Lazy) -> None:
+    for key in rec.refs:
+        if _lazy.get(key) is rec:
+            del _lazy[key]
+    _lazy_records.pop(id(rec), None)
+    if any(r() is not None for r in rec.refs.values()):
+        rec.launch()
 
 
 def lazy(out, inputs, launch) -> None:
     """Register `out` (a fresh tensor) as filled by `launch` when first
     touched: `materialize_touched` runs it before any op that reads or writes
     out's storage, or that writes the storage of one of `inputs`; if out's
-    storage dies first, the launch never runs.  The record holds the storage
-    only weakly, so it cannot outlive it (the allocator may then reuse the
-    memory), and its key is removed when the storage goes."""
-    import weakref
+    storage dies first, the launch never runs (the allocator may reuse the
+    memory then, so the record holds the storage only weakly)."""
+    _register(Lazy(inputs, launch), (out,))
 
-    key = id(out._holder)
 
-    def gone(_ref, key=key):
-        with _pending_lock:
-            rec = _lazy.get(key)
-            if rec is not None and rec.holder is _ref:
-                del _lazy[key]
+def lazy_scale(tensors, scale, launch) -> None:
+    """Register the in-place multiplication of every tensor in `tensors` by
+    the device scalar `scale` as pending: it runs (all of it, by `launch`)
+    before any op touches one of those storages or writes `scale`, except a
+    fused optimizer step that applies it itself (`pending_scale`)."""
+    _register(Lazy((scale,), launch, scale), tensors)
 
+
+def pending_scale(tensors):
+    """The scalar of the one pending scale covering every tensor in
+    `tensors`, else None (after running any pending work on them, so the
+    caller then reads plain values)."""
+    if not _lazy:
+        return None
     with _pending_lock:
-        _lazy[key] = Lazy(weakref.ref(out._holder, gone), tuple(inputs), launch)
+        recs = {id(_lazy.get(id(t._holder))): _lazy.get(id(t._holder)) for t in tensors}
+        if len(recs) == 1:
+            rec = next(iter(recs.values()))
+            if rec is not None and rec.scale is not None:
+                return rec.scale
+    materialize_touched(tuple(tensors), None, False)
+    return None
 
 
 def lazy_live() -> bool:
@@ -421,8 +470,8 @@ def _holders_of(args, kwargs) -> set:
 
 
 def materialize_touched(args, kwargs, writes: bool) -> None:
-    """Run the lazy launches that an op with these arguments depends on: those
-    whose output storage it touches, and, when the op writes (`writes`), those
+    """Run the lazy work that an op with these arguments depends on: records
+    writing a storage it touches, and, when the op writes (`writes`), records
     reading a storage it touches (they must run before it changes)."""
     if not _lazy:
         return
@@ -430,20 +479,22 @@ def materialize_touched(args, kwargs, writes: bool) -> None:
     if not hs:
         return
     with _pending_lock:
-        due = []
-        for key, rec in list(_lazy.items()):
-            if rec.holder() is None:
-                continue
-            if key in hs or (writes and any(id(t._holder) in hs for t in rec.inputs)):
-                due.append(key)
-        for key in due:
-            rec = _lazy.pop(key, None)
-            if rec is not None and rec.holder() is not None:
-                rec.launch()
+        due = {}
+        for key in hs:
+            rec = _lazy.get(key)
+            if rec is not None:
+                due[id(rec)] = rec
+        if writes:
+            for rec in list(_lazy_records.values()):
+                if any(id(t._holder) in hs for t in rec.inputs):
+                    due[id(rec)] = rec
+        for rec in due.values():
+            if _lazy_records.get(id(rec)) is rec:
+                _run(rec)
 
 
 def materialize(t) -> None:
-    """Run the lazy launch that fills t's storage, if one is pending."""
+    """Run the lazy work on t's storage, if any is pending."""
     if _lazy:
         materialize_touched((t,), None, False)
 

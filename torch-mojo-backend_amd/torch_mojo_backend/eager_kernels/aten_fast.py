@@ -23,7 +23,8 @@ import os
 
 import torch
 
-from . import AdamWTensor, Deferred, check, defer, flush_pending, lazy, lib, take_pending
+from . import AdamWTensor, Deferred, check, defer, flush_pending, lazy, lazy_scale, lib, take_pending
+from . import pending_scale as _pending_scale
 from ..mojo_device.torch_mojo_tensor import (
     DTYPE_CODE,
     TorchMojoTensor,
@@ -1440,6 +1441,8 @@ def ws_ptr_or_none(p):
 _LOW_ATTR = "_mojo_low_copy"
 # MI355X_LAZY_LN_OUT=0 writes the f32 layer-norm output eagerly (A/B measurement)
 _LAZY_LN_OUT = os.environ.get("MI355X_LAZY_LN_OUT", "1") != "0"
+# MI355X_LAZY_GRAD_SCALE=0 runs a scalar-tensor _foreach_mul_ at once (A/B measurement)
+_LAZY_GRAD_SCALE = os.environ.get("MI355X_LAZY_GRAD_SCALE", "1") != "0"
 
 
 def _take_low_copy(t: MT, dtype):
@@ -2460,6 +2463,10 @@ def fast_aten__fused_adamw_(
         raise RuntimeError("_fused_adamw_: max_exp_avg_sqs must match params when amsgrad=True")
     f32 = torch.float32
     P, G, M, V, S = ([_require(t) for t in lst] for lst in lists)
+    # a gradient-clipping scale still pending on the gradients is applied as
+    # they are read (they stay logically scaled; the multiply runs only if
+    # something else reads them)
+    gmul = _pending_scale(G)
     fields = []  # AdamWTensor records, flattened (seven 8-byte fields each)
     for i in range(n):
         p, g, m, v, s = P[i], G[i], M[i], V[i], S[i]
@@ -2521,7 +2528,8 @@ def fast_aten__fused_adamw_(
         lib().mi355x_fused_adamw_ex(
             descs, low_ptrs, _code(low_dt) if low_dt else 0, n, lr_value, lr_t._ptr if lr_t is not None else None,
             float(beta1), float(beta2), float(weight_decay), float(eps), flags,
-            gs._ptr if gs is not None else None, fi._ptr if fi is not None else None, _STREAM,
+            gs._ptr if gs is not None else None, fi._ptr if fi is not None else None,
+            gmul._ptr if gmul is not None else None, _STREAM,
         ),
     )
     if fi is not None:
@@ -2581,6 +2589,31 @@ def foreach_apply(opname, a_list, b_list=None, c_list=None, scalars=None, s0=0.0
             ts._ptr if ts is not None else None, _STREAM,
         ),
     )
+    return None
+
+
+def foreach_mul_deferred(a_list, tensor_scalar):
+    """_foreach_mul_(tensors, scalar tensor) held as pending work (see
+    `lazy_scale`) when every tensor is contiguous f32 and the scalar an f32
+    device scalar: gradient clipping's scale, which the fused AdamW step that
+    follows applies as it reads the gradients, so the gradients need no pass
+    of their own.  NOT_HANDLED otherwise."""
+    import weakref
+
+    if not _LAZY_GRAD_SCALE:
+        return NOT_HANDLED
+    a = _foreach_ok(a_list, torch.float32)
+    ts = _t(tensor_scalar)
+    if a is None or not a or ts is None or ts._dtype != torch.float32 or ts._numel != 1:
+        return NOT_HANDLED
+    refs = [weakref.ref(t) for t in a]
+
+    def run(refs=refs, ts=ts):
+        alive = [t for t in (r() for r in refs) if t is not None]
+        if alive:
+            foreach_apply("mul", alive, tensor_scalar=ts)
+
+    lazy_scale(a, ts, run)
     return None
 
 

@@ -69,6 +69,8 @@ def _inplace(op_name, self, *args, **kwargs):
                 return None
             return _seq_binary(kind, a, other)
         if overload == "Tensor":
+            if kind == "mul" and _try(F.foreach_mul_deferred, a, args[0]):
+                return None
             if _try(F.foreach_apply, kind, a, tensor_scalar=args[0]):
                 return None
             return _seq_binary(kind, a, args[0])

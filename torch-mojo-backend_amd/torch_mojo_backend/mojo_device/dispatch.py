@@ -31,9 +31,17 @@ def _is_mutable(func) -> bool:
     return mutable
 
 
+_ADAMW = (torch.ops.aten._fused_adamw_.default, torch.ops.aten._fused_adamw_.tensor_lr)
+
+
 def dispatch(func, args, kwargs):
-    if _ek._lazy:  # outputs whose kernel waits for a first use (autocast layer norm)
-        _ek.materialize_touched(args, kwargs, _is_mutable(func))
+    if _ek._lazy:  # work waiting for a first use: autocast layer-norm outputs, a clip scale
+        if func in _ADAMW and len(args) > 1:
+            # the fused step applies a pending scale on its gradients itself
+            # (fast_aten__fused_adamw_); everything else it touches goes first
+            _ek.materialize_touched(args[:1] + args[2:], kwargs, True)
+        else:
+            _ek.materialize_touched(args, kwargs, _is_mutable(func))
     if _aten_fast._param_low_by_holder and _is_mutable(func):  # parameter copies exist (autocast training)
         _aten_fast.drop_param_copies_written_by(func, args, kwargs)
     impl = DIRECT.get(func)
