@@ -239,6 +239,17 @@ int mi355x_embedding_bwd(void* grad_weight, const void* grad_out, int dtype,
                          int64_t num_weights, int64_t dim,
                          int64_t padding_idx, void* workspace,
                          int64_t ws_bytes, mi355x_stream_t stream);
+/* grad_weight = base + the gradient mi355x_embedding_bwd would write (each
+ * row's sum rounded to dtype, then added): rows idx names get base + sum,
+ * the others (and padding_idx) base's row, copied, or not touched at all
+ * when base == grad_weight (in place).  Same workspace.  No counterpart in
+ * the reference: it serves a tied embedding, whose gradient autograd adds
+ * to the output projection's (`grad + embedding_dense_backward`), in one
+ * pass without the dense sum. */
+int mi355x_embedding_bwd_accumulate(void* grad_weight, const void* base, const void* grad_out, int dtype,
+                                    const int64_t* idx, int64_t n_idx, int64_t num_weights,
+                                    int64_t dim, int64_t padding_idx, void* workspace,
+                                    int64_t ws_bytes, mi355x_stream_t stream);
 
 /* ---- layer norm (LayerNormForward normalization_forward_ops.mojo:118;
  *      LayerNormBackwardF32 normalization_backward_dx.mojo:190-388,

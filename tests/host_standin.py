@@ -242,6 +242,17 @@ class HostStandIn:
         dense(_val(gw), DT[dt], (num, dim)).copy_(acc)
         return 0
 
+    def mi355x_embedding_bwd_accumulate(self, gw, base, go, dt, idx, n, num, dim, pad, ws, wsb, stream):
+        ids = dense(_val(idx), torch.int64, (n,))
+        g = dense(_val(go), DT[dt], (n, dim)).float()
+        acc = torch.zeros(num, dim).index_add_(0, ids, g).to(DT[dt]).float()
+        rows = torch.unique(ids)
+        rows = rows[rows != pad]
+        B = dense(_val(base), DT[dt], (num, dim)).clone()
+        B[rows] = (B[rows].float() + acc[rows]).to(DT[dt])
+        dense(_val(gw), DT[dt], (num, dim)).copy_(B)
+        return 0
+
     # ---- norms / activations ----
     def mi355x_layer_norm_fwd_ex(self, y, y_low, low_dt, mean, rstd, x, g, b, rows, cols, eps, dt, stream):
         self.mi355x_layer_norm_fwd(y, mean, rstd, x, g, b, rows, cols, eps, dt, stream)

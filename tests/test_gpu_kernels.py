@@ -205,6 +205,37 @@ def test_embedding_backward_bit_exact_vs_sequential_f32(kernels):
     assert torch.equal(host(gw), ref)
 
 
+@pytest.mark.parametrize("n,num,dim,dtype", [(4096, 300, 96, torch.float32), (16384, 50304, 768, torch.float32),
+                                             (1000, 70, 30, torch.float32), (512, 90, 64, torch.bfloat16)])
+def test_embedding_backward_accumulate_equals_dense_then_add(kernels, n, num, dim, dtype):
+    """base + embedding gradient in one pass (the tied-embedding case):
+    out of place and in place, the bits of the dense gradient followed by
+    the elementwise add; rows no index names and the padding row keep base's
+    bits.  Includes the nanoGPT shape (16384 ids over 50304 rows)."""
+    idx = torch.randint(0, num, (n,), generator=G)
+    idx[:50] = 7
+    pad = 3
+    g = randn(n, dim).to(dtype)
+    base = randn(num, dim).to(dtype)
+    tg, ti, tb = dev(g), dev(idx), dev(base)
+    ws_n = lib().mi355x_embedding_bwd_workspace_bytes(n, num)
+    ws = workspace(ws_n)
+    code = CODE[dtype]
+    dense = torch.empty(num, dim, dtype=dtype, device="cuda")
+    call("mi355x_embedding_bwd", p(dense), p(tg), code, p(ti), n, num, dim, pad, p(ws), ws_n, None)
+    want = (host(tb).float() + host(dense).float()).to(dtype)
+    out = torch.full_like(tb, float("nan"))
+    call("mi355x_embedding_bwd_accumulate", p(out), p(tb), p(tg), code, p(ti), n, num, dim, pad, p(ws), ws_n, None)
+    assert torch.equal(host(out), want)
+    assert torch.equal(host(tb), base)  # base untouched out of place
+    call("mi355x_embedding_bwd_accumulate", p(tb), p(tb), p(tg), code, p(ti), n, num, dim, pad, p(ws), ws_n, None)
+    assert torch.equal(host(tb), want)
+    absent = torch.ones(num, dtype=torch.bool)
+    absent[idx] = False
+    absent[pad] = True
+    assert torch.equal(host(out)[absent], base[absent])
+
+
 # ---------------------------------------------------------------------------
 # layer norm / gelu / softmax / nll
 # ---------------------------------------------------------------------------

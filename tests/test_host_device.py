@@ -375,6 +375,47 @@ def test_clip_scale_is_applied_inside_the_fused_adamw_step(mojo):
         ek.set_library_for_tests(inner)
 
 
+def test_tied_embedding_gradient_is_added_in_place_of_a_dense_sum(mojo):
+    """With tied input/output embeddings, autograd adds the embedding's dense
+    gradient onto the projection's (`grad += g`); that add takes the lazy
+    embedding gradient as a scatter-add of the named rows
+    (mi355x_embedding_bwd_accumulate): no dense gradient is written and the
+    result matches PyTorch.  An untied embedding's gradient stays lazy until
+    read."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    torch.manual_seed(4)
+    V, D = 50, 16
+    emb = torch.nn.Embedding(V, D)
+    pos = torch.nn.Embedding(12, D)
+    idx = torch.randint(0, V, (3, 12))
+    idx[0, :4] = 7  # repeated rows
+    demb = torch.nn.Embedding(V, D).to("mojo")
+    dpos = torch.nn.Embedding(12, D).to("mojo")
+    demb.load_state_dict({k: v.to("mojo") for k, v in emb.state_dict().items()})
+    dpos.load_state_dict({k: v.to("mojo") for k, v in pos.state_dict().items()})
+
+    tgt = torch.randint(0, V, (36,))
+
+    def loss(e, p_, ids):
+        h = e(ids) + p_(torch.arange(12, device=ids.device))
+        return F.cross_entropy((h @ e.weight.t()).view(-1, V), tgt.to(ids.device))
+
+    inner, counting, calls = _counting_library()
+    ek.set_library_for_tests(counting)
+    try:
+        loss(emb, pos, idx).backward()
+        loss(demb, dpos, idx.to("mojo")).backward()
+        assert calls["mi355x_embedding_bwd_accumulate"] == 1 and calls["mi355x_embedding_bwd"] == 0
+        assert torch.allclose(demb.weight.grad.cpu(), emb.weight.grad, atol=1e-5, rtol=1e-5)
+        assert calls["mi355x_embedding_bwd"] == 0
+        assert torch.allclose(dpos.weight.grad.cpu(), pos.weight.grad, atol=1e-5, rtol=1e-5)
+        assert calls["mi355x_embedding_bwd"] == 1  # the position embedding's, on first read
+    finally:
+        ek.set_library_for_tests(inner)
+    assert not ek._lazy
+
+
 def test_adamw_parameter_copies_feed_next_autocast_forward(mojo):
     """The fused AdamW step writes the bf16 copy of every parameter the
     autocast forward casts; the next forward uses it with no cast kernel.  A

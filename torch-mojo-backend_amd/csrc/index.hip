@@ -106,9 +106,13 @@ __device__ __forceinline__ int64_t wave_lower_bound(const int64_t* __restrict__ 
 // segment sum.  Each lane owns a fixed set of columns and adds the row's
 // grad rows in sorted (= index) order, 16 bytes at a time when the row
 // allows it.
-template <typename T>
+//
+// ACC: gw = base + sum (the sum rounded to T first, then added, as a
+// separate `base + dense_sum` would); rows no index names (and the padding
+// row) are copied from base, or left untouched when base is gw itself.
+template <typename T, bool ACC>
 __global__ void __launch_bounds__(kThreads)
-    embedding_bwd_rows(T* __restrict__ gw, const T* __restrict__ go,
+    embedding_bwd_rows(T* gw, const T* __restrict__ go, const T* base,
                        const int64_t* __restrict__ keys, const int32_t* __restrict__ pos,
                        int64_t n, int64_t num_weights, int64_t dim, int64_t padding_idx, bool vec4) {
   const int lane = threadIdx.x & 63;
@@ -117,6 +121,20 @@ __global__ void __launch_bounds__(kThreads)
        row += (int64_t)gridDim.x * RPB) {
     const int64_t lo = wave_lower_bound(keys, n, row, lane);
     const int64_t end = row == padding_idx ? lo : wave_lower_bound(keys, n, row + 1, lane);
+    if (ACC && lo == end) {  // wave-uniform
+      if (base != gw) {
+        if (vec4) {
+          for (int64_t c = (int64_t)lane * 4; c < dim; c += 64 * 4) {
+            float v[4];
+            Vec4<T>::load(base + row * dim + c, v);
+            Vec4<T>::store(gw + row * dim + c, v);
+          }
+        } else {
+          for (int64_t c = lane; c < dim; c += 64) gw[row * dim + c] = base[row * dim + c];
+        }
+      }
+      continue;
+    }
     if (vec4) {
       for (int64_t c = (int64_t)lane * 4; c < dim; c += 64 * 4) {
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -126,12 +144,19 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[e] += v[e];
         }
+        if constexpr (ACC) {
+          float cur[4];
+          Vec4<T>::load(base + row * dim + c, cur);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] = cur[e] + to_f32(from_f32<T>(acc[e]));
+        }
         Vec4<T>::store(gw + row * dim + c, acc);
       }
     } else {
       for (int64_t c = lane; c < dim; c += 64) {
         float acc = 0.f;
         for (int64_t k = lo; k < end; ++k) acc += to_f32(go[(int64_t)pos[k] * dim + c]);
+        if constexpr (ACC) acc = to_f32(base[row * dim + c]) + to_f32(from_f32<T>(acc));
         gw[row * dim + c] = from_f32<T>(acc);
       }
     }
@@ -189,45 +214,65 @@ extern "C" int64_t mi355x_embedding_bwd_workspace_bytes(int64_t n_idx, int64_t n
   return (int64_t)emb_ws_layout(n_idx).total;
 }
 
-extern "C" int mi355x_embedding_bwd(void* grad_weight, const void* grad_out, int dtype,
-                                    const int64_t* idx, int64_t n_idx, int64_t num_weights,
-                                    int64_t dim, int64_t padding_idx, void* workspace,
-                                    int64_t ws_bytes, mi355x_stream_t stream) {
-  MI_REQUIRE(n_idx >= 0 && n_idx < (1ll << 31), "mi355x_embedding_bwd: bad index count");
-  MI_REQUIRE(num_weights >= 0 && dim >= 0, "mi355x_embedding_bwd: bad shape");
+namespace {
+int embedding_bwd_impl(const char* name, bool accumulate, void* grad_weight, const void* base, const void* grad_out,
+                       int dtype,
+                       const int64_t* idx, int64_t n_idx, int64_t num_weights, int64_t dim, int64_t padding_idx,
+                       void* workspace, int64_t ws_bytes, hipStream_t s) {
+  MI_REQUIRE(n_idx >= 0 && n_idx < (1ll << 31), "%s: bad index count", name);
+  MI_REQUIRE(num_weights >= 0 && dim >= 0, "%s: bad shape", name);
   if (num_weights == 0 || dim == 0) return MI355X_OK;
-  hipStream_t s = (hipStream_t)stream;
   const EmbWs w = emb_ws_layout(n_idx);
   if (n_idx > 0 && (!workspace || ws_bytes < (int64_t)w.total))
-    return fail(MI355X_EWORKSPACE, "mi355x_embedding_bwd: workspace %lld < %lld",
-                (long long)ws_bytes, (long long)w.total);
-  uint8_t* base = (uint8_t*)workspace;
-  int64_t* keys = (int64_t*)(base + w.keys_off);
-  int32_t* vin = (int32_t*)(base + w.vals_in_off);
-  int32_t* vout = (int32_t*)(base + w.vals_out_off);
+    return fail(MI355X_EWORKSPACE, "%s: workspace %lld < %lld", name, (long long)ws_bytes, (long long)w.total);
+  uint8_t* wsb = (uint8_t*)workspace;
+  int64_t* keys = (int64_t*)(wsb + w.keys_off);
+  int32_t* vin = (int32_t*)(wsb + w.vals_in_off);
+  int32_t* vout = (int32_t*)(wsb + w.vals_out_off);
   if (n_idx > 0) {
     iota_i32<<<ceil_div(n_idx, kThreads), kThreads, 0, s>>>(vin, n_idx);
     size_t temp = w.temp_bytes;
-    hipError_t e = hipcub::DeviceRadixSort::SortPairs(base + w.temp_off, temp, idx, keys, vin, vout,
+    hipError_t e = hipcub::DeviceRadixSort::SortPairs(wsb + w.temp_off, temp, idx, keys, vin, vout,
                                                       (int)n_idx, 0, 64, s);
-    if (e != hipSuccess) return fail(MI355X_ELAUNCH, "mi355x_embedding_bwd: sort failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(MI355X_ELAUNCH, "%s: sort failed: %s", name, hipGetErrorString(e));
   }
   const int64_t blocks = (num_weights + kThreads / 64 - 1) / (kThreads / 64);
   const unsigned grid = (unsigned)(blocks < 65536 ? blocks : 65536);
   const size_t es = (size_t)dtype_size(dtype);
-  const bool vec4 = dim % 4 == 0 && ((uintptr_t)grad_weight % (4 * es)) == 0 && ((uintptr_t)grad_out % (4 * es)) == 0;
+  const bool vec4 = dim % 4 == 0 && ((uintptr_t)grad_weight % (4 * es)) == 0 &&
+                    ((uintptr_t)grad_out % (4 * es)) == 0 && ((uintptr_t)base % (4 * es)) == 0;
+  auto go = [&](auto tag) {
+    using T = decltype(tag);
+    if (accumulate)
+      embedding_bwd_rows<T, true><<<grid, kThreads, 0, s>>>((T*)grad_weight, (const T*)grad_out, (const T*)base,
+                                                            keys, vout, n_idx, num_weights, dim, padding_idx, vec4);
+    else
+      embedding_bwd_rows<T, false><<<grid, kThreads, 0, s>>>((T*)grad_weight, (const T*)grad_out, nullptr, keys,
+                                                             vout, n_idx, num_weights, dim, padding_idx, vec4);
+  };
   switch (dtype) {
-    case MI355X_F32:
-      embedding_bwd_rows<float><<<grid, kThreads, 0, s>>>((float*)grad_weight, (const float*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx, vec4);
-      break;
-    case MI355X_BF16:
-      embedding_bwd_rows<bf16><<<grid, kThreads, 0, s>>>((bf16*)grad_weight, (const bf16*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx, vec4);
-      break;
-    case MI355X_F16:
-      embedding_bwd_rows<f16><<<grid, kThreads, 0, s>>>((f16*)grad_weight, (const f16*)grad_out, keys, vout, n_idx, num_weights, dim, padding_idx, vec4);
-      break;
-    default:
-      return fail(MI355X_EUNSUPPORTED, "mi355x_embedding_bwd: unsupported dtype %d", dtype);
+    case MI355X_F32: go(float{}); break;
+    case MI355X_BF16: go(bf16{}); break;
+    case MI355X_F16: go(f16{}); break;
+    default: return fail(MI355X_EUNSUPPORTED, "%s: unsupported dtype %d", name, dtype);
   }
-  return check_launch("mi355x_embedding_bwd");
+  return check_launch(name);
+}
+}  // namespace
+
+extern "C" int mi355x_embedding_bwd(void* grad_weight, const void* grad_out, int dtype,
+                                    const int64_t* idx, int64_t n_idx, int64_t num_weights,
+                                    int64_t dim, int64_t padding_idx, void* workspace,
+                                    int64_t ws_bytes, mi355x_stream_t stream) {
+  return embedding_bwd_impl("mi355x_embedding_bwd", false, grad_weight, nullptr, grad_out, dtype, idx, n_idx,
+                            num_weights, dim, padding_idx, workspace, ws_bytes, (hipStream_t)stream);
+}
+
+extern "C" int mi355x_embedding_bwd_accumulate(void* grad_weight, const void* base, const void* grad_out,
+                                               int dtype, const int64_t* idx, int64_t n_idx, int64_t num_weights,
+                                               int64_t dim, int64_t padding_idx, void* workspace,
+                                               int64_t ws_bytes, mi355x_stream_t stream) {
+  MI_REQUIRE(grad_weight && base, "mi355x_embedding_bwd_accumulate: null pointer");
+  return embedding_bwd_impl("mi355x_embedding_bwd_accumulate", true, grad_weight, base, grad_out, dtype, idx, n_idx,
+                            num_weights, dim, padding_idx, workspace, ws_bytes, (hipStream_t)stream);
 }

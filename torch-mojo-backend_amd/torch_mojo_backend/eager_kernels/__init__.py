@@ -83,6 +83,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
     ),
+    "mi355x_embedding_bwd_accumulate": (
+        c_int,
+        [c_vp, c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp],
+    ),
     "mi355x_layer_norm_fwd": (
         c_int,
         [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_double, c_int, c_vp],
@@ -363,12 +367,18 @@ class Lazy:
     Two kinds: an output the kernel has not filled (the layer norm's f32
     output under autocast), and an in-place scale not yet applied (the
     gradient-clipping `_foreach_mul_`), whose `scale` is the scalar tensor
-    and which a fused optimizer step can apply on the fly."""
+    and which a fused optimizer step can apply on the fly.  `consumers` maps
+    an op to the argument position through which that op takes the record
+    over itself: a set of positions (it neither needs nor triggers the
+    launch there); `accumulate(dst, base)`, when set, writes base + the
+    output into dst without materializing the output (a tied embedding's
+    gradient; dst may be base)."""
 
-    __slots__ = ("refs", "inputs", "launch", "scale")
+    __slots__ = ("refs", "inputs", "launch", "scale", "consumers", "accumulate")
 
-    def __init__(self, inputs, launch, scale=None):
+    def __init__(self, inputs, launch, scale=None, consumers=None, accumulate=None):
         self.refs, self.inputs, self.launch, self.scale = {}, tuple(inputs), launch, scale
+        self.consumers, self.accumulate = consumers or {}, accumulate
 
 
 _lazy: dict = {}  # id(storage holder) -> Lazy, while the holder lives
@@ -408,21 +418,26 @@ def _run(rec: Lazy) -> None:
         rec.launch()
 
 
-def lazy(out, inputs, launch) -> None:
+def lazy(out, inputs, launch, consumers=None, accumulate=None) -> None:
     """Register `out` (a fresh tensor) as filled by `launch` when first
     touched: `materialize_touched` runs it before any op that reads or writes
     out's storage, or that writes the storage of one of `inputs`; if out's
     storage dies first, the launch never runs (the allocator may reuse the
     memory then, so the record holds the storage only weakly)."""
-    _register(Lazy(inputs, launch), (out,))
+    _register(Lazy(inputs, launch, consumers=consumers, accumulate=accumulate), (out,))
 
 
-def lazy_scale(tensors, scale, launch) -> None:
+def lazy_scale(tensors, scale, launch, consumers=None) -> None:
     """Register the in-place multiplication of every tensor in `tensors` by
     the device scalar `scale` as pending: it runs (all of it, by `launch`)
     before any op touches one of those storages or writes `scale`, except a
     fused optimizer step that applies it itself (`pending_scale`)."""
-    _register(Lazy((scale,), launch, scale), tensors)
+    _register(Lazy((scale,), launch, scale, consumers), tensors)
+
+
+def lazy_record(t):
+    """The pending record on t's storage, or None."""
+    return _lazy.get(id(t._holder)) if _lazy and getattr(t, "_holder", None) is not None else None
 
 
 def pending_scale(tensors):
@@ -445,34 +460,37 @@ def lazy_live() -> bool:
     return bool(_lazy)
 
 
-def _holders_of(args, kwargs) -> set:
-    found = set()
+def _holders_of(args, kwargs) -> dict:
+    """id(storage holder) -> the argument positions (kwargs: -1) holding it."""
+    found: dict = {}
 
-    def add(v):
+    def add(v, pos):
         h = getattr(v, "_holder", None)
         if h is not None:
-            found.add(id(h))
+            found.setdefault(id(h), set()).add(pos)
 
-    for v in args:
+    for pos, v in enumerate(args):
         if isinstance(v, (list, tuple)):
             for e in v:
-                add(e)
+                add(e, pos)
         else:
-            add(v)
+            add(v, pos)
     if kwargs:
         for v in kwargs.values():
             if isinstance(v, (list, tuple)):
                 for e in v:
-                    add(e)
+                    add(e, -1)
             else:
-                add(v)
+                add(v, -1)
     return found
 
 
-def materialize_touched(args, kwargs, writes: bool) -> None:
+def materialize_touched(args, kwargs, writes: bool, func=None) -> None:
     """Run the lazy work that an op with these arguments depends on: records
     writing a storage it touches, and, when the op writes (`writes`), records
-    reading a storage it touches (they must run before it changes)."""
+    reading a storage it touches (they must run before it changes).  A record
+    that lists `func` as a consumer at the only position where it is touched
+    is left to the op."""
     if not _lazy:
         return
     hs = _holders_of(args, kwargs)
@@ -480,9 +498,12 @@ def materialize_touched(args, kwargs, writes: bool) -> None:
         return
     with _pending_lock:
         due = {}
-        for key in hs:
+        for key, where in hs.items():
             rec = _lazy.get(key)
             if rec is not None:
+                ok = rec.consumers.get(func) if func is not None else None
+                if ok is not None and where <= ok:
+                    continue
                 due[id(rec)] = rec
         if writes:
             for rec in list(_lazy_records.values()):

@@ -24,6 +24,7 @@ import os
 import torch
 
 from . import AdamWTensor, Deferred, check, defer, flush_pending, lazy, lazy_scale, lib, take_pending
+from . import lazy_live as _lazy_pending
 from . import pending_scale as _pending_scale
 from ..mojo_device.torch_mojo_tensor import (
     DTYPE_CODE,
@@ -750,6 +751,10 @@ def _binary(name, a, b, alpha=1, *, out=None, inplace=False, mode=None):
     tb, sb, db, shb = _operand(b)
     if ta is None and tb is None:
         return NOT_HANDLED
+    if name == "add" and out is None and ta is not None and tb is not None and _lazy_pending():
+        r = _add_lazy(ta, tb, alpha, inplace)
+        if r is not None:
+            return r
     opcode = OP[name]
     if name == "div" and mode == "trunc":
         opcode = OP["div_trunc"]
@@ -1441,6 +1446,8 @@ def ws_ptr_or_none(p):
 _LOW_ATTR = "_mojo_low_copy"
 # MI355X_LAZY_LN_OUT=0 writes the f32 layer-norm output eagerly (A/B measurement)
 _LAZY_LN_OUT = os.environ.get("MI355X_LAZY_LN_OUT", "1") != "0"
+# MI355X_LAZY_EMB_GRAD=0 writes the dense embedding gradient at once (A/B measurement)
+_LAZY_EMB_GRAD = os.environ.get("MI355X_LAZY_EMB_GRAD", "1") != "0"
 # MI355X_LAZY_GRAD_SCALE=0 runs a scalar-tensor _foreach_mul_ at once (A/B measurement)
 _LAZY_GRAD_SCALE = os.environ.get("MI355X_LAZY_GRAD_SCALE", "1") != "0"
 
@@ -2035,14 +2042,52 @@ def fast_aten_embedding_dense_backward(grad_output, indices, num_weights, paddin
     dim = go._shape[-1]
     g = _contig(go)
     gw = _alloc((num_weights, dim), go._dtype, go._device)
-    ws = lib().mi355x_embedding_bwd_workspace_bytes(ids._numel, num_weights)
-    hold, wptr = _workspace(ws, go._device)
-    check(
-        "mi355x_embedding_bwd",
-        lib().mi355x_embedding_bwd(gw._ptr, g._ptr, _code(go._dtype), ids._ptr, ids._numel,
-                                   num_weights, dim, int(padding_idx), wptr, ws, _STREAM),
-    )
+
+    def run(dst, base=None, g=g, ids=ids, pad=int(padding_idx), code=_code(go._dtype), dev=go._device):
+        ws = lib().mi355x_embedding_bwd_workspace_bytes(ids._numel, num_weights)
+        hold, wptr = _workspace(ws, dev)
+        if base is None:
+            check("mi355x_embedding_bwd", lib().mi355x_embedding_bwd(
+                dst, g._ptr, code, ids._ptr, ids._numel, num_weights, dim, pad, wptr, ws, _STREAM))
+        else:
+            check("mi355x_embedding_bwd_accumulate", lib().mi355x_embedding_bwd_accumulate(
+                dst, base, g._ptr, code, ids._ptr, ids._numel, num_weights, dim, pad, wptr, ws, _STREAM))
+
+    if _LAZY_EMB_GRAD:
+        # A tied embedding's gradient is added to the output projection's by
+        # autograd (`a + this` in its input buffer, or `grad += this`): left
+        # lazy, that add takes it as a scatter-add of the named rows (no
+        # dense gradient written, no dense add of it).
+        lazy(gw, [g, ids], lambda y=gw._ptr: run(y),
+             consumers={torch.ops.aten.add.Tensor: {0, 1}, torch.ops.aten.add_.Tensor: {1}},
+             accumulate=lambda dst, base: run(dst._ptr, base._ptr))
+    else:
+        run(gw._ptr)
     return gw
+
+
+def _add_lazy(a: MT, b: MT, alpha, inplace: bool):
+    """a + alpha*b (into a when `inplace`) when one operand is a lazy output
+    that can add itself onto the other (see fast_aten_embedding_dense_backward):
+    the result, written by that record's accumulate.  Otherwise the lazy
+    operands are materialized and None returned (the caller adds as usual)."""
+    from . import lazy_record, materialize
+
+    ra, rb = lazy_record(a), lazy_record(b)
+    if ra is None and rb is None:
+        return None
+    lazy_t, base = (b, a) if rb is not None else (a, b)
+    rec = rb if rb is not None else ra
+    if (rec.accumulate is not None and (ra is None or rb is None) and (rb is not None or not inplace)
+            and float(_scalar_value(alpha)) == 1.0 and a._dtype == b._dtype
+            and tuple(a._shape) == tuple(b._shape) and a._is_contiguous and b._is_contiguous
+            and a._holder is not b._holder):
+        dst = a if inplace else _alloc(a._shape, a._dtype, a._device)
+        rec.accumulate(dst, base)
+        return dst
+    for t in (a, b):
+        materialize(t)
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -2613,7 +2658,8 @@ def foreach_mul_deferred(a_list, tensor_scalar):
         if alive:
             foreach_apply("mul", alive, tensor_scalar=ts)
 
-    lazy_scale(a, ts, run)
+    lazy_scale(a, ts, run, consumers={torch.ops.aten._fused_adamw_.default: {1},
+                                      torch.ops.aten._fused_adamw_.tensor_lr: {1}})
     return None
 
 

@@ -31,17 +31,24 @@ def _is_mutable(func) -> bool:
     return mutable
 
 
-_ADAMW = (torch.ops.aten._fused_adamw_.default, torch.ops.aten._fused_adamw_.tensor_lr)
+_VIEW: dict = {}  # OpOverload -> whether it only makes a view (returns alias an input, nothing written)
+
+
+def _is_view(func) -> bool:
+    view = _VIEW.get(func)
+    if view is None:
+        sch = func._schema
+        view = _VIEW[func] = (not sch.is_mutable and bool(sch.returns)
+                              and all(r.alias_info is not None for r in sch.returns))
+    return view
 
 
 def dispatch(func, args, kwargs):
-    if _ek._lazy:  # work waiting for a first use: autocast layer-norm outputs, a clip scale
-        if func in _ADAMW and len(args) > 1:
-            # the fused step applies a pending scale on its gradients itself
-            # (fast_aten__fused_adamw_); everything else it touches goes first
-            _ek.materialize_touched(args[:1] + args[2:], kwargs, True)
-        else:
-            _ek.materialize_touched(args, kwargs, _is_mutable(func))
+    # work waiting for a first use (autocast layer-norm outputs, a clip scale,
+    # ...) runs before the op, unless the op only makes a view: a view shares
+    # the storage, so its own first use still finds the work pending
+    if _ek._lazy and not _is_view(func):
+        _ek.materialize_touched(args, kwargs, _is_mutable(func), func)
     if _aten_fast._param_low_by_holder and _is_mutable(func):  # parameter copies exist (autocast training)
         _aten_fast.drop_param_copies_written_by(func, args, kwargs)
     impl = DIRECT.get(func)
