@@ -410,6 +410,21 @@ int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx,
                              const float* grad_out, int reduction,
                              const float* total_weight, int64_t n, int64_t c,
                              int64_t ignore_index, mi355x_stream_t stream);
+/* mi355x_cross_entropy_fwd and mi355x_cross_entropy_bwd in one pass over
+ * the logits, for reduction mean (1) or sum (2): writes out, total_weight,
+ * lse and dx with the values the two calls would write (each row's logits
+ * held in registers between its log-sum-exp and its gradient).  Rows of up
+ * to 8192 16-byte chunks (about 65500 bf16/f16 or 32760 f32 classes, and
+ * ld_dx / (16 / element size) <= 8192); longer rows return
+ * MI355X_EUNSUPPORTED, and the two calls remain.
+ * Workspace: mi355x_cross_entropy_workspace_bytes(n).  No counterpart in the
+ * reference: it serves a training step, where the loss is first read after
+ * the backward, so the forward's read of the logits can be skipped. */
+int mi355x_cross_entropy_fwd_bwd(void* out, float* total_weight, float* lse, void* dx, int64_t ld_dx,
+                                 const void* logits, int dtype, int64_t ld, const int64_t* target,
+                                 const float* grad_out, int64_t n, int64_t c, int reduction,
+                                 int64_t ignore_index, int32_t* err_flag, void* workspace,
+                                 int64_t ws_bytes, mi355x_stream_t stream);
 
 /* ---- optimizer (enqueue_fused_adamw_f32 optimizer_kernels.mojo:339-454,
  *      AdamWDesc optimizer_contract.mojo:11-56;

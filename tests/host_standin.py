@@ -419,6 +419,13 @@ class HostStandIn:
         dense(_val(tw), torch.float32, ()).copy_(w)
         return 0
 
+    def mi355x_cross_entropy_fwd_bwd(self, out, tw, lse, dx, lddx, x, dt, ld, tgt, g, n, c, red, ign, err, ws, wsb,
+                                     stream):
+        if max((c + 2 * (16 // DT[dt].itemsize) - 2) // (16 // DT[dt].itemsize), lddx // (16 // DT[dt].itemsize)) > 8192:
+            return 3  # MI355X_EUNSUPPORTED
+        self.mi355x_cross_entropy_fwd(out, tw, lse, x, dt, ld, tgt, n, c, red, ign, err, ws, wsb, stream)
+        return self.mi355x_cross_entropy_bwd(dx, dt, lddx, x, dt, ld, lse, tgt, g, red, tw, n, c, ign, stream)
+
     def mi355x_cross_entropy_bwd(self, dx, dxdt, lddx, x, dt, ld, lse, tgt, g, red, tw, n, c, ign, stream):
         X = view(_val(x), DT[dt], (n, c), (ld, 1)).float()
         T = dense(_val(tgt), torch.int64, (n,))

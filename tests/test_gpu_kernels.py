@@ -513,6 +513,52 @@ def test_fused_cross_entropy_nan_and_infinite_logits(kernels):
     assert (d[2, :1000] == 0).all() and torch.isfinite(d[2]).all() and torch.isfinite(d[0]).all()
 
 
+@pytest.mark.parametrize("reduction", [1, 2])
+@pytest.mark.parametrize("dtype,n,c,ld", [(torch.bfloat16, 16384, 50257, 50257), (torch.bfloat16, 300, 50304, 50304),
+                                          (torch.float16, 40, 4000, 4003), (torch.float32, 64, 1000, 1001),
+                                          (torch.bfloat16, 9, 8, 8), (torch.float32, 7, 32752, 32752)])
+def test_cross_entropy_fwd_bwd_is_the_two_calls_in_one_pass(kernels, reduction, dtype, n, c, ld):
+    """mi355x_cross_entropy_fwd_bwd writes the values of mi355x_cross_entropy_fwd
+    followed by mi355x_cross_entropy_bwd (loss, total_weight, lse, dx): the
+    nanoGPT shape (rows of 50257 bf16, so every phase of row start), odd row
+    strides, the longest f32 row it takes, ignored and NaN rows, padding
+    columns; a longer row is refused."""
+    x = (randn(n, ld) * 4).to(dtype)
+    tgt = torch.randint(0, c, (n,), generator=G)
+    tgt[::7] = -100
+    if n > 3:
+        x[3, 2] = float("nan")
+    tx, tt = dev(x), dev(tgt)
+    g = dev(torch.tensor(1.7))
+    ws_n = lib().mi355x_cross_entropy_workspace_bytes(n)
+    ws = workspace(ws_n)
+    ld_dx = (c + 7) // 8 * 8
+    res = []
+    for fused in (False, True):
+        out, tw = torch.empty((), device="cuda"), torch.empty((), device="cuda")
+        lse = torch.empty(n, device="cuda")
+        dx = torch.full((n, ld_dx), 7.0, dtype=dtype, device="cuda")
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        if fused:
+            call("mi355x_cross_entropy_fwd_bwd", p(out), p(tw), p(lse), p(dx), ld_dx, p(tx), CODE[dtype], ld, p(tt),
+                 p(g), n, c, reduction, -100, p(err), p(ws), ws_n, None)
+        else:
+            call("mi355x_cross_entropy_fwd", p(out), p(tw), p(lse), p(tx), CODE[dtype], ld, p(tt), n, c,
+                 reduction, -100, p(err), p(ws), ws_n, None)
+            call("mi355x_cross_entropy_bwd", p(dx), CODE[dtype], ld_dx, p(tx), CODE[dtype], ld, p(lse), p(tt),
+                 p(g), reduction, p(tw), n, c, -100, None)
+        res.append([host(t) for t in (out, tw, lse, dx, err)])
+    for a, b, what in zip(res[0], res[1], ("loss", "total", "lse", "dx", "err")):
+        # equal values (a NaN's sign bit may differ: the operand order of one
+        # subtraction is the compiler's)
+        torch.testing.assert_close(a, b, rtol=0, atol=0, equal_nan=True, msg=what)
+    if dtype == torch.float32 and c == 32752:  # past 8192 16-byte chunks per row: refused before any access
+        big = 32769
+        rc = lib().mi355x_cross_entropy_fwd_bwd(p(out), p(tw), p(lse), p(dx), (big + 7) // 8 * 8, p(tx), CODE[dtype],
+                                                 big, p(tt), p(g), n, big, reduction, -100, None, p(ws), ws_n, None)
+        assert rc == 3  # MI355X_EUNSUPPORTED
+
+
 # ---------------------------------------------------------------------------
 # optimizer
 # ---------------------------------------------------------------------------

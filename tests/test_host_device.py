@@ -107,6 +107,46 @@ def test_fused_cross_entropy_matches_cpu(mojo):
         F.cross_entropy(lm, tgt.to("mojo"), label_smoothing=0.1)
 
 
+def test_cross_entropy_forward_waits_for_the_backward(mojo):
+    """Under autograd the fused cross-entropy forward is left pending: the
+    backward computes loss, lse and dlogits in one pass
+    (mi355x_cross_entropy_fwd_bwd) and the loss reads correctly afterwards;
+    reading the loss first runs the forward (then the plain backward); an
+    unread pending forward is run when the next one is deferred."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    g = torch.Generator().manual_seed(8)
+    logits, tgt = torch.randn(6, 40, generator=g), torch.tensor([1, 39, -100, 0, 5, 5])
+    lc = logits.clone().requires_grad_()
+    ref = F.cross_entropy(lc, tgt, ignore_index=-100)
+    ref.backward()
+    inner, counting, calls = _counting_library()
+    ek.set_library_for_tests(counting)
+    try:
+        for read_first in (False, True):
+            lm = logits.to("mojo").requires_grad_()
+            loss = F.cross_entropy(lm, tgt.to("mojo"), ignore_index=-100)
+            before = dict(calls)
+            if read_first:
+                assert torch.allclose(loss.cpu(), ref, atol=1e-6)
+            loss.backward()
+            assert torch.allclose(lm.grad.cpu(), lc.grad, atol=1e-6)
+            assert torch.allclose(loss.cpu(), ref, atol=1e-6)
+            fused = calls["mi355x_cross_entropy_fwd_bwd"] - before.get("mi355x_cross_entropy_fwd_bwd", 0)
+            fwd = calls["mi355x_cross_entropy_fwd"] - before.get("mi355x_cross_entropy_fwd", 0)
+            assert (fused, fwd) == ((0, 1) if read_first else (1, 0)), (read_first, fused, fwd)
+        # a pending forward whose backward never comes runs at the next deferral
+        lm = logits.to("mojo").requires_grad_()
+        first = F.cross_entropy(lm, tgt.to("mojo"), ignore_index=-100)
+        n0 = calls["mi355x_cross_entropy_fwd"]
+        second = F.cross_entropy(lm, tgt.to("mojo"), ignore_index=-100)
+        assert calls["mi355x_cross_entropy_fwd"] == n0 + 1
+        second.backward()
+        assert torch.allclose(first.cpu(), ref, atol=1e-6) and torch.allclose(second.cpu(), ref, atol=1e-6)
+    finally:
+        ek.set_library_for_tests(inner)
+
+
 def test_gpt_step_matches_cpu(mojo):
     from torch_mojo_backend.gpt2 import BETAS, LEARNING_RATE, WEIGHT_DECAY, GPT, GPTConfig, make_batches, training_step
 

@@ -26,6 +26,8 @@
 // writes dx once.
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace mi {
@@ -69,12 +71,99 @@ struct RowGeo {
 // results below the f32 normal range only feed sums and bf16/f16 gradients.
 __device__ __forceinline__ float hw_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// One aligned chunk (number j of the row) into a thread's running (max,
+// sum of exp2((x - max) * log2e)); NaN sets `nan` and skips the chunk.
+template <typename T>
+__device__ __forceinline__ void ce_take_chunk(const Chunk<T>& ch, int j, const RowGeo<T>& geo, int ci, float& m,
+                                              float& sum, bool& nan) {
+  constexpr int V = Chunk<T>::V;
+  const int k0 = j * V - geo.p;
+  float v[V];
+  if (k0 >= 0 && k0 + V <= ci) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = ch.get(e);
+  } else {  // the row's first or last chunk
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = (k0 + e >= 0 && k0 + e < ci) ? ch.get(e) : -INFINITY;
+  }
+  // one NaN test per chunk: the chunk maximum propagates NaN
+  const float cm = max_nan(v);
+  if (cm != cm) {
+    nan = true;
+    return;
+  }
+  if (cm == -INFINITY) return;
+  if (cm > m) {
+    sum = (m == -INFINITY) ? 0.f : sum * hw_exp2((m - cm) * kLog2e);
+    m = cm;
+  }
+#pragma unroll
+  for (int e = 0; e < V; ++e) sum += hw_exp2((v[e] - m) * kLog2e);
+}
+
+// The block's (max, sum) merged (wave, then block, in a fixed order) into
+// the row's log-sum-exp, its loss lse - x[t] (0 for ignore_index) and
+// validity; thread 0 writes them and returns the lse (NaN when a NaN was
+// seen); the other threads return garbage.
+template <typename T>
+__device__ __forceinline__ float ce_finish_row(float m, float sum, bool nan, float* red_m, float* red_s, int* red_nan,
+                                               const T* r, int64_t row, float* lse, float* row_loss,
+                                               float* row_valid, const int64_t* target, int64_t c,
+                                               int64_t ignore_index, int32_t* err) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float om = __shfl_xor(m, off, 64), os = __shfl_xor(sum, off, 64);
+    nan |= __shfl_xor((int)nan, off, 64) != 0;
+    const float nm = fmaxf(m, om);
+    if (nm != -INFINITY) {
+      sum = (m == -INFINITY ? 0.f : sum * exp2f((m - nm) * kLog2e)) +
+            (om == -INFINITY ? 0.f : os * exp2f((om - nm) * kLog2e));
+      m = nm;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    red_m[threadIdx.x >> 6] = m;
+    red_s[threadIdx.x >> 6] = sum;
+    red_nan[threadIdx.x >> 6] = nan;
+  }
+  __syncthreads();
+  float l = 0.f;
+  if (threadIdx.x == 0) {
+    float tm = -INFINITY, ts = 0.f;
+    bool tn = false;
+    for (int w = 0; w < kRowThreads / 64; ++w) {
+      tn |= red_nan[w] != 0;
+      const float om = red_m[w], os = red_s[w];
+      const float nm = fmaxf(tm, om);
+      if (nm == -INFINITY) continue;
+      ts = (tm == -INFINITY ? 0.f : ts * exp2f((tm - nm) * kLog2e)) +
+           (om == -INFINITY ? 0.f : os * exp2f((om - nm) * kLog2e));
+      tm = nm;
+    }
+    l = tn ? __int_as_float(0x7fc00000) : tm + log2f(ts) * kLn2;
+    lse[row] = l;
+    const int64_t tg = target[row];
+    float loss = 0.f, valid = 0.f;
+    if (tg != ignore_index) {
+      if (tg < 0 || tg >= c) {
+        if (err) *err = 1;
+      } else {
+        loss = l - to_f32(r[tg]);
+        valid = 1.f;
+      }
+    }
+    row_loss[row] = loss;
+    row_valid[row] = valid;
+  }
+  return l;
+}
+
 template <typename T>
 __global__ void __launch_bounds__(kRowThreads)
     ce_fwd_rows(float* __restrict__ row_loss, float* __restrict__ row_valid, float* __restrict__ lse,
                 const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ target, int64_t n,
                 int64_t c, int64_t ignore_index, int32_t* err) {
-  constexpr int V = Chunk<T>::V, U = 4;
+  constexpr int U = 4;
   __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64];
   __shared__ int red_nan[kRowThreads / 64];
   const int64_t row = blockIdx.x;
@@ -94,75 +183,11 @@ __global__ void __launch_bounds__(kRowThreads)
     for (int u = 0; u < U; ++u) {
       const int j = j0 + u * kRowThreads;
       if (j >= nch) break;
-      const int k0 = j * V - geo.p;
-      float v[V];
-      if (k0 >= 0 && k0 + V <= ci) {
-#pragma unroll
-        for (int e = 0; e < V; ++e) v[e] = ch[u].get(e);
-      } else {  // the row's first or last chunk
-#pragma unroll
-        for (int e = 0; e < V; ++e) v[e] = (k0 + e >= 0 && k0 + e < ci) ? ch[u].get(e) : -INFINITY;
-      }
-      // one NaN test per chunk: the chunk maximum propagates NaN
-      const float cm = max_nan(v);
-      if (cm != cm) {
-        nan = true;
-        continue;
-      }
-      if (cm == -INFINITY) continue;
-      if (cm > m) {
-        sum = (m == -INFINITY) ? 0.f : sum * hw_exp2((m - cm) * kLog2e);
-        m = cm;
-      }
-#pragma unroll
-      for (int e = 0; e < V; ++e) sum += hw_exp2((v[e] - m) * kLog2e);
+      ce_take_chunk<T>(ch[u], j, geo, ci, m, sum, nan);
     }
   }
-  // wave then block merge of (m, sum)
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float om = __shfl_xor(m, off, 64), os = __shfl_xor(sum, off, 64);
-    nan |= __shfl_xor((int)nan, off, 64) != 0;
-    const float nm = fmaxf(m, om);
-    if (nm != -INFINITY) {
-      sum = (m == -INFINITY ? 0.f : sum * exp2f((m - nm) * kLog2e)) +
-            (om == -INFINITY ? 0.f : os * exp2f((om - nm) * kLog2e));
-      m = nm;
-    }
-  }
-  if ((threadIdx.x & 63) == 0) {
-    red_m[threadIdx.x >> 6] = m;
-    red_s[threadIdx.x >> 6] = sum;
-    red_nan[threadIdx.x >> 6] = nan;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float tm = -INFINITY, ts = 0.f;
-    bool tn = false;
-    for (int w = 0; w < kRowThreads / 64; ++w) {
-      tn |= red_nan[w] != 0;
-      const float om = red_m[w], os = red_s[w];
-      const float nm = fmaxf(tm, om);
-      if (nm == -INFINITY) continue;
-      ts = (tm == -INFINITY ? 0.f : ts * exp2f((tm - nm) * kLog2e)) +
-           (om == -INFINITY ? 0.f : os * exp2f((om - nm) * kLog2e));
-      tm = nm;
-    }
-    const float l = tn ? __int_as_float(0x7fc00000) : tm + log2f(ts) * kLn2;
-    lse[row] = l;
-    const int64_t tg = target[row];
-    float loss = 0.f, valid = 0.f;
-    if (tg != ignore_index) {
-      if (tg < 0 || tg >= c) {
-        if (err) *err = 1;
-      } else {
-        loss = l - to_f32(r[tg]);
-        valid = 1.f;
-      }
-    }
-    row_loss[row] = loss;
-    row_valid[row] = valid;
-  }
+  ce_finish_row<T>(m, sum, nan, red_m, red_s, red_nan, r, row, lse, row_loss, row_valid, target, c, ignore_index,
+                   err);
 }
 
 __global__ void __launch_bounds__(1024) ce_fwd_reduce(float* __restrict__ out, float* __restrict__ total,
@@ -201,6 +226,26 @@ __device__ __forceinline__ uint4 shift_pair(uint4 lo, uint4 hi, int bytes) {
   return o;
 }
 
+// dx of the V elements from k0 on: g * (exp(x - lse) - onehot), 0 past c.
+template <typename T, typename TD>
+__device__ __forceinline__ uint4 ce_dx_chunk(const Chunk<T>& ch, int k0, int ci, int tgi, float g, float l) {
+  constexpr int V = Chunk<T>::V;
+  struct alignas(16) Out { TD v[V]; } out;
+  if (k0 + V <= ci && (tgi < k0 || tgi >= k0 + V)) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) out.v[e] = from_f32<TD>(g * hw_exp2((ch.get(e) - l) * kLog2e));
+  } else {  // the last chunk, padding past c, or the target's chunk
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int k = k0 + e;
+      float d = 0.f;
+      if (k < ci) d = g * (hw_exp2((ch.get(e) - l) * kLog2e) - (k == tgi ? 1.f : 0.f));
+      out.v[e] = from_f32<TD>(d);
+    }
+  }
+  return *(const uint4*)&out;
+}
+
 // The backward writes every element of the row.  It has no reduction, so
 // rows are split over blocks: block b covers 16-byte output chunks
 // (b % nb) * 256 .. +255 of row b / nb, one chunk per thread (gfx950,
@@ -237,20 +282,103 @@ __global__ void __launch_bounds__(kBwdThreads)
   }
   Chunk<T> ch;
   ch.w = bytes ? shift_pair(lo, hi, bytes) : lo;
-  struct alignas(16) Out { TD v[V]; } out;
-  if (k0 + V <= ci && (tgi < k0 || tgi >= k0 + V)) {
+  ((uint4*)(dx + row * ld_dx))[t] = ce_dx_chunk<T, TD>(ch, k0, ci, tgi, g, l);
+}
+
+// Forward and backward in one pass, for a row whose loss is read only
+// after its backward (a training step): the row's aligned chunks stay in
+// registers (NC per thread), the (max, sum) runs over them in ce_fwd_rows'
+// order and merge (so lse and the loss have its bits), and the dx chunks are
+// ce_bwd_chunks' from the same registers: the logits are read once instead
+// of twice (a row whose start is not 16-byte aligned takes each dx chunk's
+// second source chunk from the next lane's registers).  Rows have at
+// most NC * kRowThreads chunks.  `total` (the valid-target count, for
+// reduction mean) is written by ce_count_valid before this kernel.
+template <typename T, typename TD, int NC>
+__global__ void __launch_bounds__(kRowThreads)
+    ce_fused_rows(TD* __restrict__ dx, int64_t ld_dx, float* __restrict__ row_loss, float* __restrict__ row_valid,
+                  float* __restrict__ lse, const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ target,
+                  const float* __restrict__ grad, const float* __restrict__ total, int64_t c, int64_t ignore_index,
+                  int32_t* err) {
+  constexpr int V = Chunk<T>::V;
+  static_assert(sizeof(TD) == sizeof(T), "dx chunks follow the logits chunks");
+  __shared__ float red_m[kRowThreads / 64], red_s[kRowThreads / 64], l_s;
+  __shared__ int red_nan[kRowThreads / 64];
+  __shared__ uint4 first[kRowThreads / 64][NC + 1];  // each wave's lane-0 chunks (the next chunk of lane 63)
+  const int64_t row = blockIdx.x;
+  const T* r = x + row * ld;
+  const RowGeo<T> geo(r, c);
+  const int nch = (int)geo.nch, ci = (int)c;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  Chunk<T> ch[NC];
 #pragma unroll
-    for (int e = 0; e < V; ++e) out.v[e] = from_f32<TD>(g * hw_exp2((ch.get(e) - l) * kLog2e));
-  } else {  // the last chunk, padding past c, or the target's chunk
-#pragma unroll
-    for (int e = 0; e < V; ++e) {
-      const int k = k0 + e;
-      float d = 0.f;
-      if (k < ci) d = g * (hw_exp2((ch.get(e) - l) * kLog2e) - (k == tgi ? 1.f : 0.f));
-      out.v[e] = from_f32<TD>(d);
-    }
+  for (int k = 0; k < NC; ++k) {
+    const int j = threadIdx.x + k * kRowThreads;
+    ch[k].w = j < nch ? geo.base[j] : make_uint4(0, 0, 0, 0);
   }
-  ((uint4*)(dx + row * ld_dx))[t] = *(const uint4*)&out;
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) first[wave][k] = ch[k].w;
+    first[wave][NC] = make_uint4(0, 0, 0, 0);
+  }
+  float m = -INFINITY, sum = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int j = threadIdx.x + k * kRowThreads;
+    if (j >= nch) break;
+    ce_take_chunk<T>(ch[k], j, geo, ci, m, sum, nan);
+  }
+  const float l0 = ce_finish_row<T>(m, sum, nan, red_m, red_s, red_nan, r, row, lse, row_loss, row_valid, target,
+                                    c, ignore_index, err);
+  if (threadIdx.x == 0) l_s = l0;
+  __syncthreads();
+  const float l = l_s;
+  const int64_t tg = target[row];
+  float g = grad[0];
+  if (total) g /= total[0];
+  const bool valid = tg != ignore_index && tg >= 0 && tg < c;
+  if (!valid) g = 0.f;
+  const int tgi = valid ? (int)tg : -1;
+  const int nout = (int)(ld_dx / V);
+  const int bytes = geo.p * (int)sizeof(T);
+  uint4* out = (uint4*)(dx + row * ld_dx);
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int t = threadIdx.x + k * kRowThreads;
+    if (k * kRowThreads >= nout) break;  // uniform: every lane takes part in the shuffles below
+    const int k0 = t * V;
+    Chunk<T> cs;
+    if (bytes) {  // uniform per row
+      // chunk t + 1: the next lane's (lane 63: the next wave's lane 0, or
+      // wave 0's lane 0 one group on), zero past the row
+      uint4 hi;
+      hi.x = __shfl_down(ch[k].w.x, 1, 64);
+      hi.y = __shfl_down(ch[k].w.y, 1, 64);
+      hi.z = __shfl_down(ch[k].w.z, 1, 64);
+      hi.w = __shfl_down(ch[k].w.w, 1, 64);
+      if (lane == 63) hi = wave < kRowThreads / 64 - 1 ? first[wave + 1][k] : first[0][k + 1];
+      if (t + 1 >= nch) hi = make_uint4(0, 0, 0, 0);
+      cs.w = k0 < ci ? shift_pair(ch[k].w, hi, bytes) : make_uint4(0, 0, 0, 0);
+    } else {
+      cs.w = k0 < ci ? ch[k].w : make_uint4(0, 0, 0, 0);
+    }
+    if (t < nout) out[t] = ce_dx_chunk<T, TD>(cs, k0, ci, tgi, g, l);
+  }
+}
+
+// total[0] = the number of rows whose target is neither ignore_index nor
+// outside [0, c) (the sum of ce_fwd_rows' row_valid, exact in f32).
+__global__ void __launch_bounds__(1024) ce_count_valid(float* __restrict__ total, const int64_t* __restrict__ target,
+                                                       int64_t n, int64_t c, int64_t ignore_index) {
+  __shared__ float red[16];
+  float w = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) {
+    const int64_t t = target[i];
+    w += (t != ignore_index && t >= 0 && t < c) ? 1.f : 0.f;
+  }
+  w = block_sum(w, red);
+  if (threadIdx.x == 0) total[0] = w;
 }
 
 }  // namespace
@@ -320,4 +448,54 @@ extern "C" int mi355x_cross_entropy_bwd(void* dx, int dx_dtype, int64_t ld_dx, c
   else return fail(MI355X_EUNSUPPORTED, "mi355x_cross_entropy_bwd: unsupported dtypes %d/%d", dtype, dx_dtype);
 #undef CE_BWD
   return check_launch("mi355x_cross_entropy_bwd");
+}
+
+extern "C" int mi355x_cross_entropy_fwd_bwd(void* out, float* total_weight, float* lse, void* dx, int64_t ld_dx,
+                                            const void* logits, int dtype, int64_t ld, const int64_t* target,
+                                            const float* grad_out, int64_t n, int64_t c, int reduction,
+                                            int64_t ignore_index, int32_t* err_flag, void* workspace,
+                                            int64_t ws_bytes, mi355x_stream_t stream) {
+  MI_REQUIRE(n >= 0 && c > 0 && ld >= c && ld_dx >= c, "mi355x_cross_entropy_fwd_bwd: bad shape");
+  MI_REQUIRE(reduction == 1 || reduction == 2, "mi355x_cross_entropy_fwd_bwd: reduction must be mean or sum");
+  MI_REQUIRE(out && total_weight && lse && dx && logits && target && grad_out,
+             "mi355x_cross_entropy_fwd_bwd: null pointer");
+  const int64_t es = (int64_t)dtype_size(dtype);
+  MI_REQUIRE(es > 0, "mi355x_cross_entropy_fwd_bwd: bad dtype");
+  const int64_t v = 16 / es;
+  constexpr int kMaxNC = 32;
+  // chunks per row: the logits' (any phase) and dx's
+  const int64_t chunks = std::max((c + 2 * v - 2) / v, ld_dx / v);
+  MI_REQUIRE((uintptr_t)logits % es == 0 && (uintptr_t)dx % 16 == 0 && ld_dx % v == 0,
+             "mi355x_cross_entropy_fwd_bwd: misaligned logits or dx");
+  if (chunks > (int64_t)kMaxNC * kRowThreads || c >= (1ll << 30))
+    return fail(MI355X_EUNSUPPORTED, "mi355x_cross_entropy_fwd_bwd: rows of at most %d 16-byte chunks",
+                kMaxNC * kRowThreads);
+  if (n == 0) return MI355X_OK;
+  MI_REQUIRE(n < (1ll << 31), "mi355x_cross_entropy_fwd_bwd: too many rows");
+  const int64_t need = mi355x_cross_entropy_workspace_bytes(n);
+  if (!workspace || ws_bytes < need)
+    return fail(MI355X_EWORKSPACE, "mi355x_cross_entropy_fwd_bwd: workspace %lld < %lld", (long long)ws_bytes,
+                (long long)need);
+  hipStream_t s = (hipStream_t)stream;
+  float* row_loss = (float*)workspace;
+  float* row_valid = (float*)workspace + n;
+  ce_count_valid<<<1, 1024, 0, s>>>(total_weight, target, n, c, ignore_index);
+  const float* tw = reduction == 1 ? total_weight : nullptr;
+  auto go = [&](auto tag) {
+    using T = decltype(tag);
+#define CE_FUSED(NC_)                                                                                            ce_fused_rows<T, T, NC_><<<(unsigned)n, kRowThreads, 0, s>>>((T*)dx, ld_dx, row_loss, row_valid, lse,                                                                        (const T*)logits, ld, target, grad_out, tw, c,                                                                ignore_index, err_flag)
+    if (chunks <= 8 * kRowThreads) CE_FUSED(8);
+    else if (chunks <= 16 * kRowThreads) CE_FUSED(16);
+    else if (chunks <= 25 * kRowThreads) CE_FUSED(25);
+    else CE_FUSED(32);
+#undef CE_FUSED
+  };
+  switch (dtype) {
+    case MI355X_F32: go(float{}); break;
+    case MI355X_BF16: go(bf16{}); break;
+    case MI355X_F16: go(f16{}); break;
+    default: return fail(MI355X_EUNSUPPORTED, "mi355x_cross_entropy_fwd_bwd: unsupported dtype %d", dtype);
+  }
+  ce_fwd_reduce<<<1, 1024, 0, s>>>((float*)out, total_weight, row_loss, row_valid, n, reduction);
+  return check_launch("mi355x_cross_entropy_fwd_bwd");
 }

@@ -131,6 +131,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_vp, c_int, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_vp, c_int, c_vp, c_i64, c_i64, c_i64, c_vp],
     ),
+    "mi355x_cross_entropy_fwd_bwd": (
+        c_int,
+        [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_i64, c_int, c_i64, c_vp, c_vp,
+         c_i64, c_vp],
+    ),
     "mi355x_fused_adamw": (
         c_int,
         [
@@ -374,11 +379,11 @@ class Lazy:
     output into dst without materializing the output (a tied embedding's
     gradient; dst may be base)."""
 
-    __slots__ = ("refs", "inputs", "launch", "scale", "consumers", "accumulate")
+    __slots__ = ("refs", "inputs", "launch", "scale", "consumers", "accumulate", "fused", "__weakref__")
 
-    def __init__(self, inputs, launch, scale=None, consumers=None, accumulate=None):
+    def __init__(self, inputs, launch, scale=None, consumers=None, accumulate=None, fused=None):
         self.refs, self.inputs, self.launch, self.scale = {}, tuple(inputs), launch, scale
-        self.consumers, self.accumulate = consumers or {}, accumulate
+        self.consumers, self.accumulate, self.fused = consumers or {}, accumulate, fused
 
 
 _lazy: dict = {}  # id(storage holder) -> Lazy, while the holder lives
@@ -410,12 +415,13 @@ def _register(rec: Lazy, tensors) -> None:
 
 
 def _run(rec: Lazy) -> None:
-    for key in rec.refs:
-        if _lazy.get(key) is rec:
-            del _lazy[key]
-    _lazy_records.pop(id(rec), None)
-    if any(r() is not None for r in rec.refs.values()):
-        rec.launch()
+    with _pending_lock:
+        for key in rec.refs:
+            if _lazy.get(key) is rec:
+                del _lazy[key]
+        _lazy_records.pop(id(rec), None)
+        if any(r() is not None for r in rec.refs.values()):
+            rec.launch()
 
 
 def lazy(out, inputs, launch, consumers=None, accumulate=None) -> None:
@@ -425,6 +431,28 @@ def lazy(out, inputs, launch, consumers=None, accumulate=None) -> None:
     storage dies first, the launch never runs (the allocator may reuse the
     memory then, so the record holds the storage only weakly)."""
     _register(Lazy(inputs, launch, consumers=consumers, accumulate=accumulate), (out,))
+
+
+def lazy_outputs(outs, inputs, launch, fused=None) -> Lazy:
+    """`lazy` for several outputs of one launch (all filled together).
+    `fused` is the caller's own alternative (see `retire`)."""
+    rec = Lazy(inputs, launch, fused=fused)
+    _register(rec, outs)
+    return rec
+
+
+def retire(rec: Lazy) -> None:
+    """Drop a record whose outputs were filled by other means (a launch that
+    computes them along with more): it will not run."""
+    with _pending_lock:
+        for key in rec.refs:
+            if _lazy.get(key) is rec:
+                del _lazy[key]
+        _lazy_records.pop(id(rec), None)
+
+
+def is_pending(rec: Lazy) -> bool:
+    return _lazy_records.get(id(rec)) is rec
 
 
 def lazy_scale(tensors, scale, launch, consumers=None) -> None:

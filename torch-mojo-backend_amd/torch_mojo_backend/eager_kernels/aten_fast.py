@@ -1446,6 +1446,8 @@ def ws_ptr_or_none(p):
 _LOW_ATTR = "_mojo_low_copy"
 # MI355X_LAZY_LN_OUT=0 writes the f32 layer-norm output eagerly (A/B measurement)
 _LAZY_LN_OUT = os.environ.get("MI355X_LAZY_LN_OUT", "1") != "0"
+# MI355X_LAZY_CE=0 runs the fused cross-entropy forward at once (A/B measurement)
+_LAZY_CE = os.environ.get("MI355X_LAZY_CE", "1") != "0"
 # MI355X_LAZY_EMB_GRAD=0 writes the dense embedding gradient at once (A/B measurement)
 _LAZY_EMB_GRAD = os.environ.get("MI355X_LAZY_EMB_GRAD", "1") != "0"
 # MI355X_LAZY_GRAD_SCALE=0 runs a scalar-tensor _foreach_mul_ at once (A/B measurement)
@@ -2728,9 +2730,69 @@ def fused_cross_entropy_forward(x: MT, t: MT, reduction, ignore_index):
     return out, lse, total
 
 
+def fused_cross_entropy_forward_deferred(x: MT, t: MT, reduction, ignore_index):
+    """fused_cross_entropy_forward left lazy: (loss, lse, total) are filled by
+    the backward's single pass over the logits (mi355x_cross_entropy_fwd_bwd),
+    or by the forward kernels if anything reads them first.  None when that
+    pass does not take the shape (the caller runs the forward now)."""
+    import weakref
+
+    from . import _run, is_pending, lazy_outputs
+
+    global _last_ce_rec
+    prev = _last_ce_rec() if _last_ce_rec is not None else None
+    if prev is not None and is_pending(prev):
+        _run(prev)  # at most one deferred forward (each holds its logits)
+    n, c = x._shape
+    ld = x._strides[0] if n > 1 else c
+    es = x._itemsize
+    v = 16 // es
+    if (not _LAZY_CE or reduction not in (1, 2) or n == 0 or x._dtype not in _FLOAT_DTYPES
+            or max((c + 2 * v - 2) // v, ((c + 7) // 8 * 8) // v) > 32 * 256):
+        return None
+    tgt = _contig(t)
+    out = _alloc((), torch.float32, x._device)
+    lse = _alloc((n,), torch.float32, x._device)
+    total = _alloc((), torch.float32, x._device)
+    ptrs = (out._ptr, total._ptr, lse._ptr)
+
+    def forward(x=x, tgt=tgt):
+        o, tw, l_ = ptrs
+        ws = lib().mi355x_cross_entropy_workspace_bytes(n)
+        hold, wptr = _workspace(ws, x._device)
+        check("mi355x_cross_entropy_fwd", lib().mi355x_cross_entropy_fwd(
+            o, tw, l_, x._ptr, _code(x._dtype), ld, tgt._ptr, n, c, int(reduction), int(ignore_index),
+            _error_slot(x._device, _TARGET_ERROR), wptr, ws, _STREAM))
+
+    out_ref = weakref.ref(out._holder)
+
+    def both(dx: MT, ld_dx, g: MT, x=x, tgt=tgt):
+        o, tw, l_ = ptrs
+        hold_o = None
+        if out_ref() is None:  # the loss tensor is gone: its value goes to scratch
+            hold_o = _alloc((), torch.float32, x._device)
+            o = hold_o._ptr
+        ws = lib().mi355x_cross_entropy_workspace_bytes(n)
+        hold, wptr = _workspace(ws, x._device)
+        return lib().mi355x_cross_entropy_fwd_bwd(
+            o, tw, l_, dx._ptr, ld_dx, x._ptr, _code(x._dtype), ld, tgt._ptr, g._ptr, n, c, int(reduction),
+            int(ignore_index), _error_slot(x._device, _TARGET_ERROR), wptr, ws, _STREAM)
+
+    rec = lazy_outputs((out, lse, total), (x, tgt), forward, fused=both)
+    _last_ce_rec = weakref.ref(rec)
+    return out, lse, total
+
+
+_last_ce_rec = None  # weak reference to the last deferred cross-entropy forward
+
+
 def fused_cross_entropy_backward(grad, x: MT, t: MT, lse: MT, total: MT, reduction, ignore_index):
     """dlogits in x's dtype, stored with rows padded to a multiple of 8
-    elements (16-byte aligned rows for the lm_head GEMMs that consume it)."""
+    elements (16-byte aligned rows for the lm_head GEMMs that consume it).
+    When the forward is still pending (fused_cross_entropy_forward_deferred),
+    one pass computes the loss, lse and dlogits together."""
+    from . import lazy_record, materialize, retire
+
     n, c = x._shape
     ld = x._strides[0] if n > 1 else c
     g = _require(grad)
@@ -2738,6 +2800,12 @@ def fused_cross_entropy_backward(grad, x: MT, t: MT, lse: MT, total: MT, reducti
     ld_dx = (c + 7) // 8 * 8
     dense = _alloc((n, ld_dx), x._dtype, x._device)
     dx = MT._view_of(dense, (n, c), (ld_dx, 1), 0, ld_dx == c)
+    rec = lazy_record(lse)
+    if rec is not None and rec.fused is not None and g._numel == 1:
+        if rec.fused(dense, ld_dx, g) == 0:
+            retire(rec)
+            return dx
+    materialize(lse)
     check(
         "mi355x_cross_entropy_bwd",
         lib().mi355x_cross_entropy_bwd(dx._ptr, _code(x._dtype), ld_dx, x._ptr, _code(x._dtype), ld,

@@ -31,22 +31,26 @@ def _is_mutable(func) -> bool:
     return mutable
 
 
-_VIEW: dict = {}  # OpOverload -> whether it only makes a view (returns alias an input, nothing written)
+_VIEW: dict = {}  # OpOverload -> whether it reads no data (a view, or a fresh tensor shaped like an input)
+# fresh tensors shaped like their input, whose values do not depend on it
+_LIKE = ("aten::empty_like", "aten::zeros_like", "aten::ones_like", "aten::full_like", "aten::new_empty",
+         "aten::new_empty_strided", "aten::new_zeros", "aten::new_ones", "aten::new_full")
 
 
 def _is_view(func) -> bool:
     view = _VIEW.get(func)
     if view is None:
         sch = func._schema
-        view = _VIEW[func] = (not sch.is_mutable and bool(sch.returns)
-                              and all(r.alias_info is not None for r in sch.returns))
+        view = _VIEW[func] = sch.name in _LIKE or (
+            not sch.is_mutable and bool(sch.returns) and all(r.alias_info is not None for r in sch.returns))
     return view
 
 
 def dispatch(func, args, kwargs):
     # work waiting for a first use (autocast layer-norm outputs, a clip scale,
-    # ...) runs before the op, unless the op only makes a view: a view shares
-    # the storage, so its own first use still finds the work pending
+    # ...) runs before the op, unless the op reads no data: a view shares the
+    # storage, so its own first use still finds the work pending, and an
+    # `ones_like` (the engine's gradient of a loss) needs only the shape
     if _ek._lazy and not _is_view(func):
         _ek.materialize_touched(args, kwargs, _is_mutable(func), func)
     if _aten_fast._param_low_by_holder and _is_mutable(func):  # parameter copies exist (autocast training)

@@ -184,7 +184,11 @@ class _FusedCrossEntropy(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, logits, target, reduction, ignore_index, out_dtype):
-        loss, lse, total = aten_fast.fused_cross_entropy_forward(logits, target, reduction, ignore_index)
+        # under autograd the loss is normally read after the backward: the
+        # forward is left to the backward's single pass when it takes the shape
+        lazy = (aten_fast.fused_cross_entropy_forward_deferred(logits, target, reduction, ignore_index)
+                if ctx.needs_input_grad[0] else None)
+        loss, lse, total = lazy or aten_fast.fused_cross_entropy_forward(logits, target, reduction, ignore_index)
         ctx.save_for_backward(logits, target, lse, total)
         ctx.reduction = reduction
         ctx.ignore_index = ignore_index
