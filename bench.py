@@ -268,6 +268,14 @@ def bench_hbm(iters):
     out.append({"kernel": "cross_entropy_bwd bf16 [16384,50257] (fused, in the step)", "ms": ms,
                 "gbs": nbytes / ms / 1e6})
     del loss, lse, total
+
+    def one_pass():  # the training step's cross-entropy: forward deferred to the backward's single pass
+        lz = F.fused_cross_entropy_forward_deferred(lg, tgt, 1, -100)
+        return F.fused_cross_entropy_backward(one, lg, tgt, lz[1], lz[2], 1, -100)
+
+    ms = time_gpu(one_pass, max(3, iters // 4))
+    out.append({"kernel": "cross_entropy fwd+bwd in one pass bf16 [16384,50257] (the step's)", "ms": ms,
+                "gbs": nbytes / ms / 1e6})
     lp = F.fast_aten__log_softmax(lg, 1, False)
     del lg
     dlp = torch.randn(16384, 50257, generator=g).bfloat16().to("mojo")
