@@ -394,6 +394,8 @@ def _register(rec: Lazy, tensors) -> None:
     import weakref
 
     def gone(ref, rec=rec):
+        if _pending_lock is None:  # interpreter shutdown: module globals are gone
+            return
         with _pending_lock:
             for key, r in list(rec.refs.items()):
                 if r is ref:
@@ -521,9 +523,27 @@ def materialize_touched(args, kwargs, writes: bool, func=None) -> None:
     is left to the op."""
     if not _lazy:
         return
-    hs = _holders_of(args, kwargs)
-    if not hs:
+    # fast exit (most ops): no argument storage is pending, and the op writes
+    # nothing a record reads
+    ids = set()
+    for v in args:
+        if isinstance(v, (list, tuple)):
+            for e in v:
+                h = getattr(e, "_holder", None)
+                if h is not None:
+                    ids.add(id(h))
+        else:
+            h = getattr(v, "_holder", None)
+            if h is not None:
+                ids.add(id(h))
+    if kwargs:
+        ids.update(_holders_of((), kwargs))
+    if not ids:
         return
+    if ids.isdisjoint(_lazy.keys()) and not (
+            writes and any(id(t._holder) in ids for rec in list(_lazy_records.values()) for t in rec.inputs)):
+        return
+    hs = _holders_of(args, kwargs)
     with _pending_lock:
         due = {}
         for key, where in hs.items():
