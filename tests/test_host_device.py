@@ -415,6 +415,25 @@ def test_clip_scale_is_applied_inside_the_fused_adamw_step(mojo):
         ek.set_library_for_tests(inner)
 
 
+def test_pending_scale_reaches_views_that_outlive_the_scaled_tensor(mojo):
+    """A pending _foreach_mul_ holds the storages, not the tensor objects: a
+    view taken before the scaled tensor itself is dropped still reads the
+    scaled values."""
+    from torch_mojo_backend import eager_kernels as ek
+
+    g = torch.Generator().manual_seed(31)
+    a, b = torch.randn(64, generator=g), torch.randn(8, 8, generator=g)
+    am, bm = a.to("mojo"), b.to("mojo")
+    coef = torch.tensor(0.25).to("mojo")
+    torch._foreach_mul_([am, bm], coef)
+    assert ek._lazy
+    view = bm.detach()[2:5]
+    del bm
+    assert torch.allclose(view.cpu(), b[2:5] * 0.25)
+    assert torch.allclose(am.cpu(), a * 0.25)
+    assert not ek._lazy
+
+
 def test_tied_embedding_gradient_is_added_in_place_of_a_dense_sum(mojo):
     """With tied input/output embeddings, autograd adds the embedding's dense
     gradient onto the projection's (`grad += g`); that add takes the lazy

@@ -1446,6 +1446,8 @@ def ws_ptr_or_none(p):
 _LOW_ATTR = "_mojo_low_copy"
 # MI355X_LAZY_LN_OUT=0 writes the f32 layer-norm output eagerly (A/B measurement)
 _LAZY_LN_OUT = os.environ.get("MI355X_LAZY_LN_OUT", "1") != "0"
+# MI355X_LAZY_DW=1 holds each weight-gradient GEMM until its result is first read (experiment)
+_LAZY_DW = os.environ.get("MI355X_LAZY_DW", "0") == "1"
 # MI355X_LAZY_CE=0 runs the fused cross-entropy forward at once (A/B measurement)
 _LAZY_CE = os.environ.get("MI355X_LAZY_CE", "1") != "0"
 # MI355X_LAZY_EMB_GRAD=0 writes the dense embedding gradient at once (A/B measurement)
@@ -1666,7 +1668,22 @@ def linear_backward(dy: MT, x: MT, w: MT, need_x: bool, need_w: bool, need_b: bo
         x2 = _rows_view(x)
         dw = _alloc((n, k), w_dtype, dy._device)
         dyt = MT._view_of(d2, (n, m), (d2._strides[1], d2._strides[0]), d2._offset)
-        _gemm(dw, dyt, x2, round_out=w_dtype != cdt or (need_b and b_dtype != cdt), rowsum=db)
+        rnd = w_dtype != cdt or (need_b and b_dtype != cdt)
+        if _LAZY_DW:
+            from . import lazy_outputs
+
+            wref = _storage_ref(dw)
+            bref = _storage_ref(db) if db is not None else (lambda: None)
+
+            def run(dyt=dyt, x2=x2):
+                w_, b_ = wref(), bref()
+                if w_ is None:  # dW's storage is gone: its row sums (db) still wanted
+                    w_ = _alloc((n, k), w_dtype, dy._device)
+                _gemm(w_, dyt, x2, round_out=rnd, rowsum=b_)
+
+            lazy_outputs((dw, db) if db is not None else (dw,), (dyt, x2), run)
+        else:
+            _gemm(dw, dyt, x2, round_out=rnd, rowsum=db)
     elif need_b:
         r = _reduce(RED["sum"], d2, [0], False, cdt)
         db = cast_to(r, b_dtype)
@@ -2078,12 +2095,18 @@ def _add_lazy(a: MT, b: MT, alpha, inplace: bool):
     ra, rb = lazy_record(a), lazy_record(b)
     if ra is None and rb is None:
         return None
-    lazy_t, base = (b, a) if rb is not None else (a, b)
-    rec = rb if rb is not None else ra
-    if (rec.accumulate is not None and (ra is None or rb is None) and (rb is not None or not inplace)
-            and float(_scalar_value(alpha)) == 1.0 and a._dtype == b._dtype
-            and tuple(a._shape) == tuple(b._shape) and a._is_contiguous and b._is_contiguous
-            and a._holder is not b._holder):
+    # the operand whose record can add itself onto the other (b first: in
+    # place, only b can); the other operand's own pending work runs first
+    if rb is not None and rb.accumulate is not None:
+        rec, base = rb, a
+    elif ra is not None and ra.accumulate is not None and not inplace:
+        rec, base = ra, b
+    else:
+        rec = base = None
+    if (rec is not None and rec is not lazy_record(base) and float(_scalar_value(alpha)) == 1.0
+            and a._dtype == b._dtype and tuple(a._shape) == tuple(b._shape) and a._is_contiguous
+            and b._is_contiguous and a._holder is not b._holder):
+        materialize(base)
         dst = a if inplace else _alloc(a._shape, a._dtype, a._device)
         rec.accumulate(dst, base)
         return dst
@@ -2639,21 +2662,38 @@ def foreach_apply(opname, a_list, b_list=None, c_list=None, scalars=None, s0=0.0
     return None
 
 
+def _storage_ref(t: MT):
+    """A callable returning a tensor with t's layout over t's storage while
+    that storage lives (None after): a weak reference that survives the
+    death of t's own wrapper when views of the storage remain."""
+    import weakref
+
+    href = weakref.ref(t._holder)
+    meta = (t._ptr, tuple(t._shape), tuple(t._strides), t._offset, t._dtype, t._device, t._is_contiguous)
+
+    def get():
+        h = href()
+        if h is None:
+            return None
+        ptr, shape, strides, offset, dtype, device, contig = meta
+        return MT._make(h, ptr, shape, strides, offset, dtype, device, contig)
+
+    return get
+
+
 def foreach_mul_deferred(a_list, tensor_scalar):
     """_foreach_mul_(tensors, scalar tensor) held as pending work (see
     `lazy_scale`) when every tensor is contiguous f32 and the scalar an f32
     device scalar: gradient clipping's scale, which the fused AdamW step that
     follows applies as it reads the gradients, so the gradients need no pass
     of their own.  NOT_HANDLED otherwise."""
-    import weakref
-
     if not _LAZY_GRAD_SCALE:
         return NOT_HANDLED
     a = _foreach_ok(a_list, torch.float32)
     ts = _t(tensor_scalar)
     if a is None or not a or ts is None or ts._dtype != torch.float32 or ts._numel != 1:
         return NOT_HANDLED
-    refs = [weakref.ref(t) for t in a]
+    refs = [_storage_ref(t) for t in a]
 
     def run(refs=refs, ts=ts):
         alive = [t for t in (r() for r in refs) if t is not None]
