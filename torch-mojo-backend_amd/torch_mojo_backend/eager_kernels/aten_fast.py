@@ -1446,8 +1446,6 @@ def ws_ptr_or_none(p):
 _LOW_ATTR = "_mojo_low_copy"
 # MI355X_LAZY_LN_OUT=0 writes the f32 layer-norm output eagerly (A/B measurement)
 _LAZY_LN_OUT = os.environ.get("MI355X_LAZY_LN_OUT", "1") != "0"
-# MI355X_LAZY_DW=1 holds each weight-gradient GEMM until its result is first read (experiment)
-_LAZY_DW = os.environ.get("MI355X_LAZY_DW", "0") == "1"
 # MI355X_LAZY_CE=0 runs the fused cross-entropy forward at once (A/B measurement)
 _LAZY_CE = os.environ.get("MI355X_LAZY_CE", "1") != "0"
 # MI355X_LAZY_EMB_GRAD=0 writes the dense embedding gradient at once (A/B measurement)
@@ -1668,22 +1666,7 @@ def linear_backward(dy: MT, x: MT, w: MT, need_x: bool, need_w: bool, need_b: bo
         x2 = _rows_view(x)
         dw = _alloc((n, k), w_dtype, dy._device)
         dyt = MT._view_of(d2, (n, m), (d2._strides[1], d2._strides[0]), d2._offset)
-        rnd = w_dtype != cdt or (need_b and b_dtype != cdt)
-        if _LAZY_DW:
-            from . import lazy_outputs
-
-            wref = _storage_ref(dw)
-            bref = _storage_ref(db) if db is not None else (lambda: None)
-
-            def run(dyt=dyt, x2=x2):
-                w_, b_ = wref(), bref()
-                if w_ is None:  # dW's storage is gone: its row sums (db) still wanted
-                    w_ = _alloc((n, k), w_dtype, dy._device)
-                _gemm(w_, dyt, x2, round_out=rnd, rowsum=b_)
-
-            lazy_outputs((dw, db) if db is not None else (dw,), (dyt, x2), run)
-        else:
-            _gemm(dw, dyt, x2, round_out=rnd, rowsum=db)
+        _gemm(dw, dyt, x2, round_out=w_dtype != cdt or (need_b and b_dtype != cdt), rowsum=db)
     elif need_b:
         r = _reduce(RED["sum"], d2, [0], False, cdt)
         db = cast_to(r, b_dtype)
