@@ -2825,9 +2825,12 @@ def fused_cross_entropy_backward(grad, x: MT, t: MT, lse: MT, total: MT, reducti
     dx = MT._view_of(dense, (n, c), (ld_dx, 1), 0, ld_dx == c)
     rec = lazy_record(lse)
     if rec is not None and rec.fused is not None and g._numel == 1:
-        if rec.fused(dense, ld_dx, g) == 0:
+        rc = rec.fused(dense, ld_dx, g)
+        if rc == 0:
             retire(rec)
             return dx
+        if rc != 3:  # anything but MI355X_EUNSUPPORTED (a shape it does not take) is an error
+            check("mi355x_cross_entropy_fwd_bwd", rc)
     materialize(lse)
     check(
         "mi355x_cross_entropy_bwd",
