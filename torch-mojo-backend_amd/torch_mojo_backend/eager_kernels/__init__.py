@@ -393,15 +393,14 @@ _lazy_records: dict = {}  # id(Lazy) -> Lazy, the records with a live holder
 def _register(rec: Lazy, tensors) -> None:
     import weakref
 
-    def gone(ref, rec=rec):
+    def gone(ref, key, rec=rec):
         if _pending_lock is None:  # interpreter shutdown: module globals are gone
             return
         with _pending_lock:
-            for key, r in list(rec.refs.items()):
-                if r is ref:
-                    del rec.refs[key]
-                    if _lazy.get(key) is rec:
-                        del _lazy[key]
+            if rec.refs.get(key) is ref:
+                del rec.refs[key]
+                if _lazy.get(key) is rec:
+                    del _lazy[key]
             if not rec.refs:
                 _lazy_records.pop(id(rec), None)
 
@@ -411,7 +410,7 @@ def _register(rec: Lazy, tensors) -> None:
             old = _lazy.get(key)
             if old is not None and old is not rec:
                 _run(old)  # an earlier record on the same storage goes first
-            rec.refs[key] = weakref.ref(t._holder, gone)
+            rec.refs[key] = weakref.ref(t._holder, lambda ref, key=key: gone(ref, key))
             _lazy[key] = rec
         _lazy_records[id(rec)] = rec
 
